@@ -1,0 +1,329 @@
+#!/usr/bin/env python3
+"""Benchmark of the fh3 Q4_K linear layer on one MI355X (gfx950).
+
+Headline (`value`): small-M GEMV weight throughput on the text-encoder shapes
+-- M in {1, 4, 16} tokens, K = 5120, N in {5120, 17408} -- one step = one call
+of fh3_hip_matmul_dev for each of the six shapes, with the weights rotated
+over distinct device copies (> 256 MB per shape) so the 256 MB MALL cannot
+serve them.  value = sum of Q4_K weight bytes of a step / step time.
+
+Also reported (`extra`): the DiT GEMMs (M = 8192 attention linears, M = 32768
+MLP linears) in TFLOP/s, the M = 64 x 4096 x 4096 single matmul, kernel-only
+rooflines from HIP events on the library's compute stream, and the CPU
+baseline (the reference's fh3_matmul built from its sources by
+oracle/Makefile, or the oracle restatement when that is absent) timed on
+this host's cores on the GEMV shapes.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+import argparse
+import ctypes
+import json
+import os
+import platform
+import subprocess
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from fasth3inc_amd import fh3 as F  # noqa: E402
+
+HBM_PEAK = 8.0e12        # B/s, MI355X HBM3E
+MFMA_F16_PEAK = 2.5e15   # flop/s, MI355X dense fp16/bf16 MFMA
+MALL_BYTES = 256 << 20   # Infinity Cache
+METRIC = "Q4_K GEMM TFLOP/s + GEMV weight GB/s (% roofline); DiT block linear ms"
+
+
+def q4k_bytes(N, K):
+    return N * (K // 256) * 144
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class HipEvents:
+    """hipEvent timing on a given stream (the library's compute stream)."""
+
+    def __init__(self):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def pair(self):
+        a, b = ctypes.c_void_p(), ctypes.c_void_p()
+        assert self.hip.hipEventCreate(ctypes.byref(a)) == 0
+        assert self.hip.hipEventCreate(ctypes.byref(b)) == 0
+        return a, b
+
+    def time_ms(self, fn, iters, stream):
+        a, b = self.pair()
+        assert self.hip.hipEventRecord(a, stream) == 0
+        for i in range(iters):
+            fn(i)
+        assert self.hip.hipEventRecord(b, stream) == 0
+        assert self.hip.hipEventSynchronize(b) == 0
+        ms = ctypes.c_float()
+        assert self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        self.hip.hipEventDestroy(a)
+        self.hip.hipEventDestroy(b)
+        return ms.value / iters
+
+
+# ---------------------------------------------------------------------------
+# Workloads
+# ---------------------------------------------------------------------------
+class Gemv:
+    """One small-M shape with rotated weight copies."""
+
+    def __init__(self, M, K, N, seed):
+        self.M, self.K, self.N = M, K, N
+        wb = q4k_bytes(N, K)
+        raw = F.synth_q4k_weights(seed, 100 + N, N, K, 0.02, 0.0)
+        self.copies = max(2, -(-(MALL_BYTES + (64 << 20)) // wb))
+        self.w = [F.DeviceBuffer.from_array(raw)]
+        for _ in range(self.copies - 1):
+            b = F.DeviceBuffer(wb)
+            F.lib().fh3_hip_memcpy_dtod(b.ptr, self.w[0].ptr, wb)
+            self.w.append(b)
+        self.raw = raw
+        self.x = F.synth_x("normal", seed, 200 + M, M, K)
+        self.dx = F.DeviceBuffer.from_array(self.x)
+        self.dy = F.DeviceBuffer(M * N * 4)
+        self.prep = F.DeviceBuffer(F.prepared_bytes(M, K))
+        F.prepare_x_dev(self.dx, M, K, self.prep)
+        self.wbytes = wb
+        self.alg_bytes = wb + 4 * M * K + 4 * M * N
+
+    def call(self, i):
+        F.matmul_dev(self.w[i % self.copies], self.K, self.N, self.dx, self.dy, self.M)
+
+    def kernel(self, i):
+        F.matmul_prepared_dev(self.w[i % self.copies], self.K, self.N, self.prep, self.dy, self.M)
+
+
+class Gemm:
+    """One large-M projection: weights ~N(0, 0.02) (optionally with a per
+    super-block log-uniform scale spread), activations of a given kind."""
+
+    def __init__(self, name, M, K, N, xkind, spread, seed, x_dev=None):
+        self.name, self.M, self.K, self.N = name, M, K, N
+        self.raw = F.synth_q4k_weights(seed, 300 + N + K, N, K, 0.02, spread)
+        self.dw = F.DeviceBuffer.from_array(self.raw)
+        if x_dev is None:
+            x = F.synth_x(xkind, seed, 400 + K, M, K)
+            self.dx = F.DeviceBuffer.from_array(x)
+            del x
+        else:
+            self.dx = x_dev
+        self.dy = F.DeviceBuffer(M * N * 4)
+        self.prep = F.DeviceBuffer(F.prepared_bytes(M, K))
+        F.prepare_x_dev(self.dx, M, K, self.prep)
+        self.flop = 2.0 * M * N * K
+
+    def call(self, i):
+        F.matmul_dev(self.dw, self.K, self.N, self.dx, self.dy, self.M)
+
+    def kernel(self, i):
+        F.matmul_prepared_dev(self.dw, self.K, self.N, self.prep, self.dy, self.M)
+
+    def free(self):
+        for b in (self.dw, self.dy, self.prep):
+            b.close()
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline
+# ---------------------------------------------------------------------------
+def cpu_baseline(cases, iters=3):
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import helpers as H
+    ref = H.load_ref()
+    if ref is not None:
+        lib, fn, kind = ref, "fh3_matmul", "reference"
+    else:
+        lib, fn, kind = H.load_oracle(), "fh3_oracle_matmul", "port"
+    total_w, total_t, per = 0, 0.0, []
+    for c in cases:
+        H.matmul_with(lib, fn, c.raw, c.K, c.N, c.x)  # warmup
+        best = 1e30
+        for _ in range(iters):
+            t0 = time.perf_counter()
+            H.matmul_with(lib, fn, c.raw, c.K, c.N, c.x)
+            best = min(best, time.perf_counter() - t0)
+        total_w += c.wbytes
+        total_t += best
+        per.append({"M": c.M, "N": c.N, "K": c.K, "ms": round(best * 1e3, 3),
+                    "weight_GBps": round(c.wbytes / best / 1e9, 2)})
+    threads = H.load_oracle().fh3_oracle_threads()
+    cpu = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(total_w / total_t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": "the six GEMV shapes once each (best of %d after 1 warmup), one weight copy, "
+                      "fh3_matmul with OMP_NUM_THREADS=%d; nproc=%d; %s; built -O3 -mavx2 -mfma -mf16c "
+                      "-ffp-contract=off -fopenmp (no -march=native)" % (iters, threads, os.cpu_count(), cpu),
+            "per_case": per}
+
+
+# ---------------------------------------------------------------------------
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="skip the M=32768 MLP GEMMs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(--gpus %d requested)" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+    F.init(0)
+    st = F.stream()
+    ev = HipEvents()
+
+    # ---------------- headline: small-M GEMV -------------------------------
+    log("[bench] building GEMV shapes")
+    gemv = [Gemv(M, 5120, N, seed=0) for N in (5120, 17408) for M in (1, 4, 16)]
+    F.synchronize()
+
+    def step(s):
+        for c in gemv:
+            c.call(s)
+
+    for s in range(args.warmup):
+        step(s)
+    F.synchronize()
+    t0 = time.perf_counter()
+    ms_step = ev.time_ms(step, args.steps, st)
+    F.synchronize()
+    wall = time.perf_counter() - t0
+    step_wbytes = sum(c.wbytes for c in gemv)
+    value = step_wbytes / (ms_step * 1e-3) / 1e9
+    log("[bench] GEMV step %.4f ms -> %.1f GB/s (wall %.2fs)" % (ms_step, value, wall))
+
+    per_gemv = []
+    k_bytes, k_time = 0, 0.0
+    for c in gemv:
+        for i in range(10):
+            c.kernel(i)
+        reps = 400
+        t_k = ev.time_ms(c.kernel, reps, st)
+        t_c = ev.time_ms(c.call, reps, st)
+        k_bytes += c.alg_bytes
+        k_time += t_k
+        per_gemv.append({"M": c.M, "K": c.K, "N": c.N, "kernel_us": round(t_k * 1e3, 2),
+                         "call_us": round(t_c * 1e3, 2),
+                         "kernel_weight_GBps": round(c.wbytes / (t_k * 1e-3) / 1e9, 1),
+                         "kernel_alg_GBps": round(c.alg_bytes / (t_k * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(c.alg_bytes / (t_k * 1e-3) / HBM_PEAK, 4),
+                         "copies": c.copies})
+        log("[bench] GEMV M=%d N=%d kernel %.2f us call %.2f us" % (c.M, c.N, t_k * 1e3, t_c * 1e3))
+    achieved = k_bytes / (k_time * 1e-3)
+    roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                "kernel": "k_skinny (fh3_hip_matmul_prepared_dev, n_tok<=64)",
+                "note": "algorithmic bytes N*K/256*144 + 4MK + 4MN per launch over the mean launch time of "
+                        "the six shapes"}
+
+    cpu = None if args.no_cpu else cpu_baseline(gemv)
+    if cpu:
+        log("[bench] CPU baseline %.2f GB/s (%s, %d threads)" % (cpu["value"], cpu["kind"], cpu["cores"]))
+    for c in gemv:
+        for b in c.w:
+            b.close()
+    del gemv
+
+    # ---------------- M=64 single matmul (4096 x 4096) ---------------------
+    extra = {}
+    g1 = Gemm("single_64x4096x4096", 64, 4096, 4096, "normal", 0.0, seed=0)
+    for i in range(10):
+        g1.call(i)
+    t_k = ev.time_ms(g1.kernel, 200, st)
+    t_c = ev.time_ms(g1.call, 200, st)
+    extra["single_matmul_M64"] = {"M": 64, "K": 4096, "N": 4096, "kernel_us": round(t_k * 1e3, 2),
+                                  "call_us": round(t_c * 1e3, 2),
+                                  "kernel_TFLOPs": round(g1.flop / (t_k * 1e-3) / 1e12, 2),
+                                  "call_TFLOPs": round(g1.flop / (t_c * 1e-3) / 1e12, 2)}
+    g1.free()
+
+    # ---------------- DiT GEMMs --------------------------------------------
+    shapes = [("attn_qkv", 8192, 5120, 15360, "outliers", 0.0), ("attn_out", 8192, 5120, 5120, "outliers", 0.0)]
+    if not args.quick:
+        shapes += [("mlp_up", 32768, 5120, 13824, "normal", 2.0), ("mlp_gate", 32768, 5120, 13824, "normal", 2.0),
+                   ("mlp_down", 32768, 13824, 5120, "silu_gated", 2.0)]
+    gemms = []
+    best_frac, sum_flop, sum_t = 0.0, 0.0, 0.0
+    shared_x = {}
+    for name, M, K, N, xk, spread in shapes:
+        log("[bench] GEMM %s M=%d K=%d N=%d" % (name, M, K, N))
+        key = (M, K, xk)
+        g = Gemm(name, M, K, N, xk, spread, seed=1, x_dev=shared_x.get(key))
+        shared_x[key] = g.dx
+        g.call(0)
+        F.synchronize()
+        reps = 5 if M >= 32768 else 10
+        t_k = ev.time_ms(g.kernel, reps, st)
+        t_c = ev.time_ms(g.call, reps, st)
+        tf_k = g.flop / (t_k * 1e-3) / 1e12
+        gemms.append({"name": name, "M": M, "K": K, "N": N, "kernel_ms": round(t_k, 4), "call_ms": round(t_c, 4),
+                      "kernel_TFLOPs": round(tf_k, 1), "call_TFLOPs": round(g.flop / (t_c * 1e-3) / 1e12, 1),
+                      "mfma_frac": round(tf_k * 1e12 / MFMA_F16_PEAK, 4)})
+        sum_flop += g.flop
+        sum_t += t_k
+        log("[bench]   kernel %.3f ms (%.1f TFLOP/s) call %.3f ms" % (t_k, tf_k, t_c))
+        g.free()
+    shared_x.clear()
+    ach = sum_flop / (sum_t * 1e-3)
+    roofline_gemm = {"bound": "mfma", "achieved": round(ach / 1e12, 1), "peak": MFMA_F16_PEAK / 1e12,
+                     "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK, 4), "traffic": None,
+                     "kernel": "k_gemm (fh3_hip_matmul_prepared_dev, n_tok>64)",
+                     "note": "2*M*N*K per launch over launch time, summed over the DiT GEMMs; "
+                             "fp16 operands, fp32 accumulation; peak is dense fp16 MFMA"}
+    extra["dit_gemms"] = gemms
+    attn = [g for g in gemms if g["name"].startswith("attn")]
+    mlp = [g for g in gemms if g["name"].startswith("mlp")]
+    extra["dit_attn_linears_ms"] = round(sum(g["call_ms"] for g in attn), 4)
+    if mlp:
+        extra["dit_mlp_linears_ms"] = round(sum(g["call_ms"] for g in mlp), 4)
+    extra["gemv"] = per_gemv
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 x f16 -> f32 (Q4_K weights, fp32 activations)",
+        "data": "synthetic: Philox-seeded N(0,0.02) weights Q4_K-encoded, N(0,1) activations",
+        "config": {"workload": "small-M GEMV, text-encoder shapes: M in {1,4,16}, K=5120, N in {5120,17408}; "
+                               "one step = one fh3_hip_matmul_dev per shape, weights rotated over >256 MB of "
+                               "device copies", "parallelism": "single GPU"},
+        "roofline": roofline,
+        "roofline_gemm": roofline_gemm,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

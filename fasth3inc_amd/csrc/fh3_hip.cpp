@@ -1,0 +1,463 @@
+// fh3_hip.cpp -- the thin C-ABI layer of libfh3hip.so: device state, memory
+// helpers, the device-resident matmul/dequant entry points (fh3_hip.h) and the
+// reference-signature host wrappers fh3_matmul / fh3_dequant (fh3.h).
+//
+// There is deliberately no CPU compute path here: if the GPU cannot be used
+// the call fails with a message instead of computing on the host.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+
+#include "fh3/fh3.h"
+#include "fh3/fh3_hip.h"
+#include "fh3_kernels.h"
+#include "fh3_hip_internal.h"
+
+namespace {
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+struct State {
+    bool init = false;
+    int device = -1;
+    hipStream_t stream = nullptr;
+    DevBuf ws;                      // x16 fragments + per-row scales
+    DevBuf st_w, st_x, st_y, st_b;  // staging for the host-pointer wrappers
+    int path = FH3_HIP_PATH_AUTO;
+    std::recursive_mutex mu;
+};
+
+State g;
+thread_local char g_err[512] = "";
+
+int set_err(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return set_err(e == hipErrorOutOfMemory ? FH3_E_NOMEM : FH3_ERR, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define FH3_HIPCALL(expr)                                 \
+    do {                                                  \
+        hipError_t e_ = (expr);                           \
+        if (e_ != hipSuccess) return hip_fail(e_, #expr); \
+    } while (0)
+
+int ensure_init() {
+    if (g.init) return FH3_OK;
+    const char *env = getenv("FH3_HIP_DEVICE");
+    return fh3_hip_init(env ? atoi(env) : 0);
+}
+
+// Grow-only device buffer.  A grow waits for the device first because
+// previously enqueued kernels may still read the old allocation.
+int grow(DevBuf &b, size_t need) {
+    if (b.cap >= need) return FH3_OK;
+    if (b.p) {
+        FH3_HIPCALL(hipDeviceSynchronize());
+        FH3_HIPCALL(hipFree(b.p));
+        b.p = nullptr;
+        b.cap = 0;
+    }
+    FH3_HIPCALL(hipMalloc(&b.p, need));
+    b.cap = need;
+    return FH3_OK;
+}
+
+int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+int choose_path(int n_tok) {
+    if (g.path == FH3_HIP_PATH_SKINNY && n_tok <= fh3k_skinny_max_tokens()) return FH3_HIP_PATH_SKINNY;
+    if (g.path == FH3_HIP_PATH_GEMM) return FH3_HIP_PATH_GEMM;
+    return n_tok <= fh3k_skinny_max_tokens() ? FH3_HIP_PATH_SKINNY : FH3_HIP_PATH_GEMM;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Internal helpers shared with the C trunk streamer (fh3_hip_internal.h)
+// ---------------------------------------------------------------------------
+extern "C" int fh3_hip_set_error(int code, const char *msg) { return set_err(code, "%s", msg); }
+
+extern "C" int fh3_hip_host_alloc(void **p, size_t bytes) {
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    FH3_HIPCALL(hipHostMalloc(p, bytes, hipHostMallocDefault));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_host_free(void *p) {
+    if (!p) return FH3_OK;
+    FH3_HIPCALL(hipHostFree(p));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_stream_create(void **st) {
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    hipStream_t s = nullptr;
+    FH3_HIPCALL(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *st = (void *)s;
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_stream_destroy(void *st) {
+    if (!st) return FH3_OK;
+    FH3_HIPCALL(hipStreamDestroy((hipStream_t)st));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_stream_sync(void *st) {
+    FH3_HIPCALL(hipStreamSynchronize(st ? (hipStream_t)st : g.stream));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_copy_async(void *dst, const void *src, size_t bytes, void *st) {
+    FH3_HIPCALL(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, st ? (hipStream_t)st : g.stream));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_event_create(void **ev) {
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    hipEvent_t e = nullptr;
+    FH3_HIPCALL(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    *ev = (void *)e;
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_event_destroy(void *ev) {
+    if (!ev) return FH3_OK;
+    FH3_HIPCALL(hipEventDestroy((hipEvent_t)ev));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_event_record(void *ev, void *st) {
+    FH3_HIPCALL(hipEventRecord((hipEvent_t)ev, st ? (hipStream_t)st : g.stream));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_stream_wait(void *st, void *ev) {
+    FH3_HIPCALL(hipStreamWaitEvent(st ? (hipStream_t)st : g.stream, (hipEvent_t)ev, 0));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_event_sync(void *ev) {
+    FH3_HIPCALL(hipEventSynchronize((hipEvent_t)ev));
+    return FH3_OK;
+}
+
+// ---------------------------------------------------------------------------
+// fh3_hip.h
+// ---------------------------------------------------------------------------
+extern "C" int fh3_hip_init(int device) {
+    std::lock_guard<std::recursive_mutex> lk(g.mu);
+    if (g.init && g.device == device) return FH3_OK;
+    if (g.init) return set_err(FH3_E_INVALID, "fh3_hip_init: already initialised on device %d", g.device);
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0)
+        return set_err(FH3_ERR, "fh3_hip_init: no HIP device available (%s)",
+                       e != hipSuccess ? hipGetErrorString(e) : "0 devices");
+    if (device < 0 || device >= n) return set_err(FH3_E_INVALID, "fh3_hip_init: device %d of %d", device, n);
+    FH3_HIPCALL(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    FH3_HIPCALL(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return set_err(FH3_ERR, "fh3_hip_init: device %d is %s; this library is built for gfx950", device,
+                       prop.gcnArchName);
+    FH3_HIPCALL(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
+    g.device = device;
+    g.init = true;
+    return FH3_OK;
+}
+
+extern "C" void fh3_hip_shutdown(void) {
+    std::lock_guard<std::recursive_mutex> lk(g.mu);
+    if (!g.init) return;
+    (void)hipDeviceSynchronize();
+    DevBuf *bufs[] = {&g.ws, &g.st_w, &g.st_x, &g.st_y, &g.st_b};
+    for (DevBuf *b : bufs) {
+        if (b->p) (void)hipFree(b->p);
+        b->p = nullptr;
+        b->cap = 0;
+    }
+    (void)hipStreamDestroy(g.stream);
+    g.stream = nullptr;
+    g.init = false;
+    g.device = -1;
+}
+
+extern "C" const char *fh3_hip_last_error(void) { return g_err; }
+
+extern "C" void *fh3_hip_stream(void) { return g.init ? (void *)g.stream : nullptr; }
+
+extern "C" int fh3_hip_malloc(void **dptr, size_t bytes) {
+    if (!dptr) return set_err(FH3_E_INVALID, "fh3_hip_malloc: NULL out pointer");
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    FH3_HIPCALL(hipMalloc(dptr, bytes ? bytes : 1));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_free(void *dptr) {
+    if (!dptr) return FH3_OK;
+    FH3_HIPCALL(hipFree(dptr));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_memcpy_htod(void *dst, const void *src, size_t bytes) {
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    FH3_HIPCALL(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_memcpy_dtoh(void *dst, const void *src, size_t bytes) {
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    FH3_HIPCALL(hipStreamSynchronize(g.stream));
+    FH3_HIPCALL(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_memcpy_dtod(void *dst, const void *src, size_t bytes) {
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    FH3_HIPCALL(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_memset(void *dptr, int value, size_t bytes) {
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    FH3_HIPCALL(hipMemset(dptr, value, bytes));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_synchronize(void) {
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    FH3_HIPCALL(hipDeviceSynchronize());
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_set_path(int path) {
+    if (path < FH3_HIP_PATH_AUTO || path > FH3_HIP_PATH_GEMM)
+        return set_err(FH3_E_INVALID, "fh3_hip_set_path: bad path %d", path);
+    g.path = path;
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_skinny_max(void) { return fh3k_skinny_max_tokens(); }
+
+extern "C" int fh3_hip_matmul_path(int n_tok) { return choose_path(n_tok); }
+
+extern "C" int fh3_hip_dequant_dev(int type, const void *d_src, float *d_dst, int64_t rows, int64_t n,
+                                   void *stream) {
+    if (!d_src || !d_dst || rows <= 0 || n <= 0)
+        return set_err(FH3_E_INVALID, "fh3_hip_dequant_dev: NULL pointer or non-positive size");
+    if (type != FH3_QUANT_Q4_K) return set_err(FH3_E_INVALID, "fh3_hip_dequant_dev: unsupported type %d", type);
+    if (n % 256) return set_err(FH3_E_INVALID, "fh3_hip_dequant_dev: n=%lld is not a multiple of 256", (long long)n);
+    if (((uintptr_t)d_src & 15u) || ((uintptr_t)d_dst & 15u))
+        return set_err(FH3_E_INVALID, "fh3_hip_dequant_dev: pointers must be 16-byte aligned");
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    hipStream_t st = stream ? (hipStream_t)stream : g.stream;
+    FH3_HIPCALL(fh3k_dequant_q4k_f32(d_src, (int64_t)fh3_row_bytes(type, n), n, rows, d_dst, st));
+    return FH3_OK;
+}
+
+static int check_weights(const Fh3W *w, const char *fn) {
+    if (!w || !w->data || w->in <= 0 || w->out <= 0)
+        return set_err(FH3_E_INVALID, "%s: NULL weights or non-positive size", fn);
+    if (w->type != FH3_QUANT_Q4_K)
+        return set_err(FH3_E_INVALID, "%s: unsupported weight type %d (Q4_K only)", fn, w->type);
+    if (w->in % 256)
+        return set_err(FH3_E_INVALID, "%s: in=%lld is not a multiple of 256", fn, (long long)w->in);
+    if (w->in > (1 << 24) || w->out > 0x7FFFFFFF)
+        return set_err(FH3_E_INVALID, "%s: shape out of range", fn);
+    if ((uintptr_t)w->data & 15u) return set_err(FH3_E_INVALID, "%s: weights must be 16-byte aligned", fn);
+    return FH3_OK;
+}
+
+// Prepared-activation layout: fragments of Mpad = round_up(n_tok, 256) rows,
+// then Mpad fp32 inverse scales at a 256-byte aligned offset.
+static int64_t prep_rows(int n_tok) { return round_up(n_tok, fh3k_gemm_row_pad()); }
+static size_t prep_scale_offset(int n_tok, int64_t in) {
+    return (size_t)round_up(prep_rows(n_tok) * in * 2, 256);
+}
+
+extern "C" size_t fh3_hip_prepared_bytes(int n_tok, int64_t in) {
+    if (n_tok <= 0 || in <= 0) return 0;
+    return prep_scale_offset(n_tok, in) + (size_t)prep_rows(n_tok) * sizeof(float);
+}
+
+static int prepare(const float *d_x, int n_tok, int64_t in, void *d_prep, int64_t rows, hipStream_t st) {
+    float *xs_inv = (float *)((char *)d_prep + prep_scale_offset(n_tok, in));
+    FH3_HIPCALL(fh3k_xprep(d_x, n_tok, (int)in, (int)rows, d_prep, xs_inv, st));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, void *d_prep, void *stream) {
+    if (!d_x || !d_prep || n_tok <= 0 || in <= 0 || in % 256 || in > (1 << 24))
+        return set_err(FH3_E_INVALID, "fh3_hip_prepare_x_dev: bad arguments");
+    if (((uintptr_t)d_x & 15u) || ((uintptr_t)d_prep & 15u))
+        return set_err(FH3_E_INVALID, "fh3_hip_prepare_x_dev: pointers must be 16-byte aligned");
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    return prepare(d_x, n_tok, in, d_prep, prep_rows(n_tok), stream ? (hipStream_t)stream : g.stream);
+}
+
+static int product(const Fh3W *w, const void *prep, int n_tok, const float *bias, float *d_y, hipStream_t st) {
+    const int K = (int)w->in, N = (int)w->out;
+    const int64_t row_bytes = (int64_t)fh3_row_bytes(w->type, w->in);
+    const float *xs_inv = (const float *)((const char *)prep + prep_scale_offset(n_tok, w->in));
+    if (choose_path(n_tok) == FH3_HIP_PATH_SKINNY) {
+        FH3_HIPCALL(fh3k_skinny(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, st));
+    } else {
+        FH3_HIPCALL(fh3k_gemm(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, st));
+    }
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_matmul_prepared_dev(const Fh3W *w, const void *d_prep, float *d_y, int n_tok,
+                                           const float *d_bias_or_null, void *stream) {
+    int rc = check_weights(w, "fh3_hip_matmul_prepared_dev");
+    if (rc != FH3_OK) return rc;
+    if (!d_prep || !d_y || n_tok <= 0)
+        return set_err(FH3_E_INVALID, "fh3_hip_matmul_prepared_dev: NULL pointer or n_tok <= 0");
+    if ((uintptr_t)d_prep & 15u)
+        return set_err(FH3_E_INVALID, "fh3_hip_matmul_prepared_dev: prepared buffer must be 16-byte aligned");
+    rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    return product(w, d_prep, n_tok, d_bias_or_null, d_y, stream ? (hipStream_t)stream : g.stream);
+}
+
+extern "C" int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok,
+                                  const float *d_bias_or_null, void *stream) {
+    int rc = check_weights(w, "fh3_hip_matmul_dev");
+    if (rc != FH3_OK) return rc;
+    if (!d_x || !d_y || n_tok <= 0)
+        return set_err(FH3_E_INVALID, "fh3_hip_matmul_dev: NULL pointer or n_tok <= 0");
+    if ((uintptr_t)d_x & 15u) return set_err(FH3_E_INVALID, "fh3_hip_matmul_dev: x must be 16-byte aligned");
+    rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    std::lock_guard<std::recursive_mutex> lk(g.mu);
+    hipStream_t st = stream ? (hipStream_t)stream : g.stream;
+    // the small-M kernel only reads round_up(n_tok, 32) prepared rows
+    const int64_t rows = choose_path(n_tok) == FH3_HIP_PATH_SKINNY ? round_up(n_tok, 32) : prep_rows(n_tok);
+    rc = grow(g.ws, fh3_hip_prepared_bytes(n_tok, w->in));
+    if (rc != FH3_OK) return rc;
+    rc = prepare(d_x, n_tok, w->in, g.ws.p, rows, st);
+    if (rc != FH3_OK) return rc;
+    return product(w, g.ws.p, n_tok, d_bias_or_null, d_y, st);
+}
+
+// ---------------------------------------------------------------------------
+// fh3.h host-pointer wrappers
+// ---------------------------------------------------------------------------
+extern "C" size_t fh3_row_bytes(int type, int64_t n) {
+    if (n <= 0) return 0;
+    const int64_t b32 = (n + 31) / 32, b256 = (n + 255) / 256;
+    switch (type) {
+        case FH3_QUANT_F32: return (size_t)n * 4u;
+        case FH3_QUANT_F16: return (size_t)n * 2u;
+        case FH3_QUANT_BF16: return (size_t)n * 2u;
+        case FH3_QUANT_Q4_0: return (size_t)b32 * 18u;
+        case FH3_QUANT_Q4_1: return (size_t)b32 * 20u;
+        case FH3_QUANT_Q5_0: return (size_t)b32 * 22u;
+        case FH3_QUANT_Q5_1: return (size_t)b32 * 24u;
+        case FH3_QUANT_Q8_0: return (size_t)b32 * 34u;
+        case FH3_QUANT_Q8_1: return (size_t)b32 * 40u;
+        case FH3_QUANT_Q2_K: return (size_t)b256 * 84u;
+        case FH3_QUANT_Q3_K: return (size_t)b256 * 110u;
+        case FH3_QUANT_Q4_K: return (size_t)b256 * 144u;
+        case FH3_QUANT_Q5_K: return (size_t)b256 * 176u;
+        case FH3_QUANT_Q6_K: return (size_t)b256 * 210u;
+        case FH3_QUANT_Q8_K: return (size_t)b256 * 292u;
+        default: return 0;
+    }
+}
+
+static void report(const char *fn, int rc) {
+    fprintf(stderr, "%s: GPU path failed (%d): %s\n", fn, rc, g_err);
+}
+
+extern "C" void fh3_dequant(int type, const void *src, float *dst, int64_t n) {
+    if (!src || !dst || n <= 0) return;
+    if (type != FH3_QUANT_Q4_K) {
+        set_err(FH3_E_INVALID, "fh3_dequant: unsupported type %d", type);
+        fprintf(stderr, "fh3_dequant: unsupported type %d\n", type);
+        return;
+    }
+    const int64_t nsb = n / 256;
+    if (nsb == 0) return;
+    int rc = ensure_init();
+    if (rc != FH3_OK) { report("fh3_dequant", rc); return; }
+    std::lock_guard<std::recursive_mutex> lk(g.mu);
+    const size_t in_bytes = (size_t)nsb * 144u, out_bytes = (size_t)nsb * 256u * sizeof(float);
+    if ((rc = grow(g.st_w, in_bytes)) != FH3_OK || (rc = grow(g.st_y, out_bytes)) != FH3_OK) {
+        report("fh3_dequant", rc);
+        return;
+    }
+    hipError_t e = hipMemcpy(g.st_w.p, src, in_bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = fh3k_dequant_q4k_f32(g.st_w.p, (int64_t)in_bytes, nsb * 256, 1, (float *)g.st_y.p, g.stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g.stream);
+    if (e == hipSuccess) e = hipMemcpy(dst, g.st_y.p, out_bytes, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) report("fh3_dequant", hip_fail(e, "fh3_dequant"));
+}
+
+extern "C" void fh3_matmul(const Fh3W *w, const float *x, float *y, int n_tok, const float *bias_or_null) {
+    if (!w || !x || !y || n_tok <= 0 || w->in <= 0 || w->out <= 0) return;
+    int rc = ensure_init();
+    if (rc != FH3_OK) { report("fh3_matmul", rc); return; }
+    if (w->type != FH3_QUANT_Q4_K || !w->data) {
+        set_err(FH3_E_INVALID, "fh3_matmul: unsupported weight type %d (Q4_K only)", w->type);
+        report("fh3_matmul", FH3_E_INVALID);
+        return;
+    }
+    std::lock_guard<std::recursive_mutex> lk(g.mu);
+    const size_t wb = fh3_row_bytes(w->type, w->in) * (size_t)w->out;
+    const size_t xb = (size_t)n_tok * (size_t)w->in * sizeof(float);
+    const size_t yb = (size_t)n_tok * (size_t)w->out * sizeof(float);
+    const size_t bb = (size_t)w->out * sizeof(float);
+    if ((rc = grow(g.st_w, wb)) || (rc = grow(g.st_x, xb)) || (rc = grow(g.st_y, yb)) ||
+        (bias_or_null && (rc = grow(g.st_b, bb)))) {
+        report("fh3_matmul", rc);
+        return;
+    }
+    hipError_t e = hipMemcpy(g.st_w.p, w->data, wb, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(g.st_x.p, x, xb, hipMemcpyHostToDevice);
+    if (e == hipSuccess && bias_or_null) e = hipMemcpy(g.st_b.p, bias_or_null, bb, hipMemcpyHostToDevice);
+    if (e != hipSuccess) { report("fh3_matmul", hip_fail(e, "fh3_matmul upload")); return; }
+    Fh3W wd = *w;
+    wd.data = (const uint8_t *)g.st_w.p;
+    rc = fh3_hip_matmul_dev(&wd, (const float *)g.st_x.p, (float *)g.st_y.p, n_tok,
+                            bias_or_null ? (const float *)g.st_b.p : nullptr, nullptr);
+    if (rc != FH3_OK) { report("fh3_matmul", rc); return; }
+    e = hipStreamSynchronize(g.stream);
+    if (e == hipSuccess) e = hipMemcpy(y, g.st_y.p, yb, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) report("fh3_matmul", hip_fail(e, "fh3_matmul download"));
+}
+
+extern "C" void fh3_matmul_scalar(const Fh3W *w, const float *x, float *y, int n_tok, const float *bias_or_null) {
+    fh3_matmul(w, x, y, n_tok, bias_or_null);
+}
+
+extern "C" void fh3_matmul_avx2(const Fh3W *w, const float *x, float *y, int n_tok, const float *bias_or_null) {
+    fh3_matmul(w, x, y, n_tok, bias_or_null);
+}

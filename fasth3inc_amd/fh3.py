@@ -1,0 +1,313 @@
+"""ctypes binding of libfh3hip.so -- the Python mirror of fh3's Q4_K linear
+layer interface (reference include/fh3/fh3.h:82-109) and of the HIP module's
+C-ABI (include/fh3/fh3_hip.h).
+
+Functions keep the reference names and argument meaning; where the C entry
+point returns an FH3_* code, the wrapper raises Fh3Error instead.  Nothing in
+this module computes on the CPU: if the library or a GPU is missing, calls
+raise.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "lib", "libfh3hip.so")
+
+# GGML type ids (reference include/fh3/fh3.h:63-79)
+FH3_QUANT_F32 = 0
+FH3_QUANT_F16 = 1
+FH3_QUANT_Q4_K = 12
+FH3_QUANT_Q6_K = 14
+
+FH3_OK = 0
+FH3_ERR = -1
+FH3_E_IO = -2
+FH3_E_TRUNCATED = -3
+FH3_E_BAD_MAGIC = -4
+FH3_E_BAD_VERSION = -5
+FH3_E_NOT_FOUND = -6
+FH3_E_NOMEM = -7
+FH3_E_INVALID = -8
+
+PATH_AUTO, PATH_SKINNY, PATH_GEMM = 0, 1, 2
+
+Q4K_BLOCK_BYTES = 144
+Q4K_BLOCK_WEIGHTS = 256
+
+
+class Fh3Error(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__("%s (code %d)" % (msg, code))
+        self.code = code
+
+
+class Fh3W(ctypes.Structure):
+    """struct Fh3W {int type; int64_t in; int64_t out; const uint8_t *data;}"""
+    _fields_ = [("type", ctypes.c_int), ("in_", ctypes.c_int64),
+                ("out", ctypes.c_int64), ("data", ctypes.c_void_p)]
+
+
+_c_void_p = ctypes.c_void_p
+_c_i64 = ctypes.c_int64
+_c_size = ctypes.c_size_t
+_c_int = ctypes.c_int
+_c_u64 = ctypes.c_uint64
+_c_float = ctypes.c_float
+
+# name: (restype, argtypes).  This table is also the list of symbols the
+# library must export (checked by tests/test_boundary.py against include/).
+SIGNATURES = {
+    # fh3.h
+    "fh3_row_bytes": (_c_size, [_c_int, _c_i64]),
+    "fh3_dequant": (None, [_c_int, _c_void_p, _c_void_p, _c_i64]),
+    "fh3_matmul": (None, [ctypes.POINTER(Fh3W), _c_void_p, _c_void_p, _c_int, _c_void_p]),
+    "fh3_matmul_scalar": (None, [ctypes.POINTER(Fh3W), _c_void_p, _c_void_p, _c_int, _c_void_p]),
+    "fh3_matmul_avx2": (None, [ctypes.POINTER(Fh3W), _c_void_p, _c_void_p, _c_int, _c_void_p]),
+    "fh3_rng_normal": (None, [_c_u64, _c_u64, _c_void_p, _c_size]),
+    # fh3_hip.h
+    "fh3_hip_init": (_c_int, [_c_int]),
+    "fh3_hip_shutdown": (None, []),
+    "fh3_hip_last_error": (ctypes.c_char_p, []),
+    "fh3_hip_stream": (_c_void_p, []),
+    "fh3_hip_malloc": (_c_int, [ctypes.POINTER(_c_void_p), _c_size]),
+    "fh3_hip_free": (_c_int, [_c_void_p]),
+    "fh3_hip_memcpy_htod": (_c_int, [_c_void_p, _c_void_p, _c_size]),
+    "fh3_hip_memcpy_dtoh": (_c_int, [_c_void_p, _c_void_p, _c_size]),
+    "fh3_hip_memcpy_dtod": (_c_int, [_c_void_p, _c_void_p, _c_size]),
+    "fh3_hip_memset": (_c_int, [_c_void_p, _c_int, _c_size]),
+    "fh3_hip_synchronize": (_c_int, []),
+    "fh3_hip_dequant_dev": (_c_int, [_c_int, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_void_p]),
+    "fh3_hip_matmul_dev": (_c_int, [ctypes.POINTER(Fh3W), _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p]),
+    "fh3_hip_prepared_bytes": (_c_size, [_c_int, _c_i64]),
+    "fh3_hip_prepare_x_dev": (_c_int, [_c_void_p, _c_int, _c_i64, _c_void_p, _c_void_p]),
+    "fh3_hip_matmul_prepared_dev": (_c_int, [ctypes.POINTER(Fh3W), _c_void_p, _c_void_p, _c_int, _c_void_p,
+                                             _c_void_p]),
+    "fh3_hip_set_path": (_c_int, [_c_int]),
+    "fh3_hip_skinny_max": (_c_int, []),
+    "fh3_hip_matmul_path": (_c_int, [_c_int]),
+    # fh3_synth.h
+    "fh3_philox4x32_10": (None, [_c_void_p, _c_void_p, _c_void_p]),
+    "fh3_rng_uniform": (None, [_c_u64, _c_u64, _c_void_p, _c_size]),
+    "fh3_q4k_quantize": (_c_int, [_c_void_p, _c_i64, _c_i64, _c_void_p]),
+    "fh3_f32_to_f16": (ctypes.c_uint16, [_c_float]),
+    "fh3_synth_q4k_weights": (_c_int, [_c_u64, _c_u64, _c_i64, _c_i64, _c_float, _c_float, _c_void_p]),
+    "fh3_synth_x_normal": (None, [_c_u64, _c_u64, _c_void_p, _c_size]),
+    "fh3_synth_x_outliers": (None, [_c_u64, _c_u64, _c_void_p, _c_size, _c_float]),
+    "fh3_synth_x_silu_gated": (None, [_c_u64, _c_u64, _c_void_p, _c_size]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libfh3hip.so (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise Fh3Error(FH3_ERR, "libfh3hip.so is not built (%s); run python -m fasth3inc_amd.build"
+                           % LIB_PATH)
+        l = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(l, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = l
+    return _lib
+
+
+def _check(rc, what):
+    if rc != FH3_OK:
+        msg = lib().fh3_hip_last_error()
+        raise Fh3Error(rc, "%s: %s" % (what, msg.decode() if msg else ""))
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ---------------------------------------------------------------------------
+# Reference-named host API
+# ---------------------------------------------------------------------------
+def row_bytes(qtype, n):
+    return lib().fh3_row_bytes(qtype, n)
+
+
+def dequant(qtype, src, n):
+    """fh3_dequant on one row (host bytes -> host fp32, computed on the GPU)."""
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    dst = np.zeros(n, dtype=np.float32)
+    lib().fh3_dequant(qtype, _p(src), _p(dst), n)
+    return dst
+
+
+def matmul(w_bytes, K, N, x, bias=None, qtype=FH3_QUANT_Q4_K, variant="fh3_matmul"):
+    """fh3_matmul on host arrays: y[M][N] = x[M][K] . W^T (+bias)."""
+    w_bytes = np.ascontiguousarray(w_bytes, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M = x.shape[0]
+    y = np.full((M, N), np.nan, dtype=np.float32)
+    w = Fh3W(qtype, K, N, w_bytes.ctypes.data)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    getattr(lib(), variant)(ctypes.byref(w), _p(x), _p(y), M, None if b is None else _p(b))
+    return y
+
+
+def rng_normal(seed, stream, n):
+    out = np.empty(n, dtype=np.float32)
+    lib().fh3_rng_normal(seed, stream, _p(out), n)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Device API
+# ---------------------------------------------------------------------------
+def init(device=0):
+    _check(lib().fh3_hip_init(device), "fh3_hip_init")
+
+
+def shutdown():
+    lib().fh3_hip_shutdown()
+
+
+def stream():
+    return lib().fh3_hip_stream()
+
+
+def synchronize():
+    _check(lib().fh3_hip_synchronize(), "fh3_hip_synchronize")
+
+
+def set_path(path):
+    _check(lib().fh3_hip_set_path(path), "fh3_hip_set_path")
+
+
+def matmul_path(n_tok):
+    return lib().fh3_hip_matmul_path(n_tok)
+
+
+class DeviceBuffer:
+    """A device allocation owned by Python (freed on close / GC)."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        ptr = ctypes.c_void_p()
+        _check(lib().fh3_hip_malloc(ctypes.byref(ptr), self.nbytes), "fh3_hip_malloc")
+        self.ptr = ptr.value
+
+    @classmethod
+    def from_array(cls, a):
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a):
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        _check(lib().fh3_hip_memcpy_htod(self.ptr, _p(a), a.nbytes), "fh3_hip_memcpy_htod")
+
+    def download(self, dtype, shape):
+        out = np.empty(shape, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        _check(lib().fh3_hip_memcpy_dtoh(_p(out), self.ptr, out.nbytes), "fh3_hip_memcpy_dtoh")
+        return out
+
+    def fill(self, value=0):
+        _check(lib().fh3_hip_memset(self.ptr, value, self.nbytes), "fh3_hip_memset")
+
+    def close(self):
+        if self.ptr:
+            lib().fh3_hip_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def matmul_dev(d_w, K, N, d_x, d_y, n_tok, d_bias=None, stream_ptr=None, qtype=FH3_QUANT_Q4_K):
+    """fh3_hip_matmul_dev on device buffers (asynchronous on the stream)."""
+    w = Fh3W(qtype, K, N, d_w.ptr if isinstance(d_w, DeviceBuffer) else d_w)
+    xp = d_x.ptr if isinstance(d_x, DeviceBuffer) else d_x
+    yp = d_y.ptr if isinstance(d_y, DeviceBuffer) else d_y
+    bp = None if d_bias is None else (d_bias.ptr if isinstance(d_bias, DeviceBuffer) else d_bias)
+    _check(lib().fh3_hip_matmul_dev(ctypes.byref(w), xp, yp, n_tok, bp, stream_ptr), "fh3_hip_matmul_dev")
+
+
+def _ptr_of(b):
+    return None if b is None else (b.ptr if isinstance(b, DeviceBuffer) else b)
+
+
+def prepared_bytes(n_tok, K):
+    return lib().fh3_hip_prepared_bytes(n_tok, K)
+
+
+def prepare_x_dev(d_x, n_tok, K, d_prep, stream_ptr=None):
+    _check(lib().fh3_hip_prepare_x_dev(_ptr_of(d_x), n_tok, K, _ptr_of(d_prep), stream_ptr),
+           "fh3_hip_prepare_x_dev")
+
+
+def matmul_prepared_dev(d_w, K, N, d_prep, d_y, n_tok, d_bias=None, stream_ptr=None, qtype=FH3_QUANT_Q4_K):
+    w = Fh3W(qtype, K, N, _ptr_of(d_w))
+    _check(lib().fh3_hip_matmul_prepared_dev(ctypes.byref(w), _ptr_of(d_prep), _ptr_of(d_y), n_tok,
+                                             _ptr_of(d_bias), stream_ptr), "fh3_hip_matmul_prepared_dev")
+
+
+def dequant_dev(d_src, d_dst, rows, n, qtype=FH3_QUANT_Q4_K, stream_ptr=None):
+    sp = d_src.ptr if isinstance(d_src, DeviceBuffer) else d_src
+    dp = d_dst.ptr if isinstance(d_dst, DeviceBuffer) else d_dst
+    _check(lib().fh3_hip_dequant_dev(qtype, sp, dp, rows, n, stream_ptr), "fh3_hip_dequant_dev")
+
+
+# ---------------------------------------------------------------------------
+# Seeded synthetic inputs (host)
+# ---------------------------------------------------------------------------
+def philox4x32_10(ctr, key):
+    c = np.asarray(ctr, dtype=np.uint32)
+    k = np.asarray(key, dtype=np.uint32)
+    out = np.zeros(4, dtype=np.uint32)
+    lib().fh3_philox4x32_10(_p(c), _p(k), _p(out))
+    return out
+
+
+def rng_uniform(seed, stream, n):
+    out = np.empty(n, dtype=np.float32)
+    lib().fh3_rng_uniform(seed, stream, _p(out), n)
+    return out
+
+
+def q4k_quantize(w):
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, n = w.shape
+    out = np.zeros(rows * (n // 256) * 144, dtype=np.uint8)
+    _check(lib().fh3_q4k_quantize(_p(w), rows, n, _p(out)), "fh3_q4k_quantize")
+    return out
+
+
+def f32_to_f16_bits(f):
+    return lib().fh3_f32_to_f16(float(f))
+
+
+def synth_q4k_weights(seed, stream, rows, n, sigma=0.02, spread_decades=0.0):
+    out = np.zeros(rows * (n // 256) * 144, dtype=np.uint8)
+    _check(lib().fh3_synth_q4k_weights(seed, stream, rows, n, sigma, spread_decades, _p(out)),
+           "fh3_synth_q4k_weights")
+    return out
+
+
+def synth_x(kind, seed, stream, rows, n, frac=0.01):
+    x = np.empty((rows, n), dtype=np.float32)
+    cnt = rows * n
+    if kind == "normal":
+        lib().fh3_synth_x_normal(seed, stream, _p(x), cnt)
+    elif kind == "outliers":
+        lib().fh3_synth_x_outliers(seed, stream, _p(x), cnt, frac)
+    elif kind == "silu_gated":
+        lib().fh3_synth_x_silu_gated(seed, stream, _p(x), cnt)
+    else:
+        raise ValueError(kind)
+    return x

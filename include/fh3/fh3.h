@@ -1,0 +1,110 @@
+/*
+ * fh3.h -- the fh3 entry points of the Q4_K linear-layer path, served by the
+ * MI355X (gfx950) library libfh3hip.so.
+ *
+ * Types and signatures keep the reference's ABI so existing C callers link
+ * unchanged; each declaration cites the reference interface it replaces
+ * (paths relative to the fh3 repository root).  Every compute entry point
+ * here runs on the GPU; there is no CPU fallback in this library.  When no
+ * HIP device can be initialised the call prints a diagnostic to stderr, leaves
+ * its outputs unwritten, and fh3_hip_last_error() says why.
+ */
+#ifndef FH3_H
+#define FH3_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <stdbool.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGML/GGUF tensor type ids (reference include/fh3/fh3.h:63-79). */
+typedef enum {
+    FH3_QUANT_F32  = 0,
+    FH3_QUANT_F16  = 1,
+    FH3_QUANT_Q4_0 = 2,
+    FH3_QUANT_Q4_1 = 3,
+    FH3_QUANT_Q5_0 = 6,
+    FH3_QUANT_Q5_1 = 7,
+    FH3_QUANT_Q8_0 = 8,
+    FH3_QUANT_Q8_1 = 9,
+    FH3_QUANT_Q2_K = 10,
+    FH3_QUANT_Q3_K = 11,
+    FH3_QUANT_Q4_K = 12,
+    FH3_QUANT_Q5_K = 13,
+    FH3_QUANT_Q6_K = 14,
+    FH3_QUANT_Q8_K = 15,
+    FH3_QUANT_BF16 = 30
+} Fh3QuantType;
+
+/* A weight matrix W[out][in] stored row-major in `type` blocks
+ * (reference include/fh3/fh3.h:82-87).  For the HIP entry points taking a
+ * device matrix, `data` is a device pointer. */
+typedef struct Fh3W {
+    int type;
+    int64_t in;
+    int64_t out;
+    const uint8_t *data;
+} Fh3W;
+
+/* Per-layer tensor views into a packed trunk layer
+ * (reference include/fh3/fh3.h:90-100; run order src/io/fh3_pack.h:26-37). */
+typedef struct Fh3LayerView {
+    Fh3W qkv;
+    Fh3W gate_compress;
+    Fh3W out;
+    Fh3W fc1;
+    Fh3W fc2;
+    Fh3W norm1;
+    Fh3W norm2;
+    Fh3W q_norm;
+    Fh3W k_norm;
+} Fh3LayerView;
+
+/* Return codes (reference include/fh3/fh3.h:218-226). */
+#define FH3_OK              0
+#define FH3_ERR           (-1)
+#define FH3_E_IO          (-2)
+#define FH3_E_TRUNCATED   (-3)
+#define FH3_E_BAD_MAGIC   (-4)
+#define FH3_E_BAD_VERSION (-5)
+#define FH3_E_NOT_FOUND   (-6)
+#define FH3_E_NOMEM       (-7)
+#define FH3_E_INVALID     (-8)
+
+/* Bytes of one row of n elements of `type`; 0 for n <= 0 or an unknown type.
+ * Replaces src/core/fh3_quant.c:14-34 (same table, Q4_K = ceil(n/256)*144). */
+size_t fh3_row_bytes(int type, int64_t n);
+
+/* Dequantise n elements of one row from host memory to host fp32, on the GPU.
+ * Q4_K output is bit-identical to the reference.  Q4_K writes n/256 whole
+ * super-blocks, as the reference does; other types print "unsupported type"
+ * and write nothing.  Replaces src/core/fh3_quant.c:284-318. */
+void fh3_dequant(int type, const void *src, float *dst, int64_t n);
+
+/* y[n_tok][out] = x[n_tok][in] * W^T (+ bias[out]) on host buffers, computed
+ * on the GPU (inputs are copied in and y out on every call).  NULL pointers or
+ * non-positive sizes are a silent no-op, as in the reference.  Q4_K only, with
+ * in % 256 == 0.  Results are deterministic run to run; they match the CPU
+ * path within rel-Frobenius 2e-3 (fp16 operands, fp32 accumulation).
+ * Replaces src/core/fh3_ops.c:317-404. */
+void fh3_matmul(const Fh3W *w, const float *x, float *y, int n_tok, const float *bias_or_null);
+
+/* The reference's single-thread variants (src/core/fh3_ops.c:210-315) are
+ * bitwise-equal to fh3_matmul by contract; here they run the same GPU path. */
+void fh3_matmul_scalar(const Fh3W *w, const float *x, float *y, int n_tok, const float *bias_or_null);
+void fh3_matmul_avx2(const Fh3W *w, const float *x, float *y, int n_tok, const float *bias_or_null);
+
+/* Seeded N(0,1) fp32 generator: Philox4x32-10 (Salmon et al., SC'11) with
+ * Box-Muller, one counter per 4 outputs.  Same stream layout as the
+ * reference's fh3_rng_normal (src/model/fh3_sched.c:110-159); used to build
+ * seeded synthetic inputs on the host. */
+void fh3_rng_normal(uint64_t seed, uint64_t stream, float *out, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FH3_H */

@@ -1,0 +1,91 @@
+/*
+ * fh3_hip.h -- C-ABI of the MI355X (gfx950) HIP module behind the fh3 Q4_K
+ * linear layer.  Plain pointers and sizes only; streams are passed as the
+ * opaque `void *` of a hipStream_t (NULL = the module's compute stream).
+ *
+ * These entry points have no counterpart in the CPU-only reference; they are
+ * the device-resident form of src/core/fh3_ops.c:317-404 (fh3_matmul) and
+ * src/core/fh3_quant.c:154-196 (dequant_q4_k) that the host wrappers in fh3.h
+ * and the trunk streamer in fh3_trunk.h are built on.  All return FH3_OK or a
+ * negative FH3_* code; fh3_hip_last_error() describes the last failure.
+ */
+#ifndef FH3_HIP_H
+#define FH3_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include "fh3/fh3.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Select and initialise a device; creates the compute stream.  Idempotent for
+ * the same device.  Every other entry point initialises device 0 (or the one
+ * named by the FH3_HIP_DEVICE environment variable) on first use. */
+int fh3_hip_init(int device);
+/* Release streams and library-owned device buffers. */
+void fh3_hip_shutdown(void);
+/* Text of the last error raised in this thread ("" when none). */
+const char *fh3_hip_last_error(void);
+/* The library's compute stream (a hipStream_t) after initialisation, else NULL. */
+void *fh3_hip_stream(void);
+
+/* Device memory helpers (synchronous). */
+int fh3_hip_malloc(void **dptr, size_t bytes);
+int fh3_hip_free(void *dptr);
+int fh3_hip_memcpy_htod(void *dst, const void *src, size_t bytes);
+int fh3_hip_memcpy_dtoh(void *dst, const void *src, size_t bytes);
+int fh3_hip_memcpy_dtod(void *dst, const void *src, size_t bytes);
+int fh3_hip_memset(void *dptr, int value, size_t bytes);
+int fh3_hip_synchronize(void);
+
+/* Bit-exact fp32 dequantisation of `rows` Q4_K rows of n elements each,
+ * rows spaced fh3_row_bytes(type, n) apart in d_src, written densely to d_dst
+ * [rows][n].  n % 256 == 0.  Same bits as src/core/fh3_quant.c:154-196. */
+int fh3_hip_dequant_dev(int type, const void *d_src, float *d_dst, int64_t rows, int64_t n,
+                        void *stream);
+
+/* Device-resident fh3_matmul: d_y[n_tok][w->out] = d_x[n_tok][w->in] * W^T
+ * (+ d_bias).  w->data is a device pointer to the packed Q4_K rows (16-byte
+ * aligned), w->in % 256 == 0.  Work is enqueued on `stream` and the call
+ * returns without synchronising.  Activations are converted to fp16 with a
+ * per-row power-of-two scale, weights are dequantised exactly in fp32 and
+ * rounded once to fp16, products accumulate in fp32 on MFMA.  Deterministic:
+ * no atomics, fixed reduction order.  Uses a library-owned workspace of
+ * about n_tok * in * 2 bytes; calls that overlap on different streams race
+ * on it. */
+int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok,
+                       const float *d_bias_or_null, void *stream);
+
+/* The two stages of fh3_hip_matmul_dev, for callers that feed one activation
+ * matrix to several weight matrices (the DiT's qkv and gate_compress read the
+ * same normalised rows) or that time the product kernel alone.
+ *   fh3_hip_prepared_bytes: device bytes a prepared buffer for n_tok x in
+ *     needs (fragments of round_up(n_tok, 256) rows, fp16, plus one fp32 scale
+ *     per row);
+ *   fh3_hip_prepare_x_dev: fill d_prep (16-byte aligned) from d_x[n_tok][in];
+ *   fh3_hip_matmul_prepared_dev: the product from a prepared buffer; same
+ *     results as fh3_hip_matmul_dev, no library workspace. */
+size_t fh3_hip_prepared_bytes(int n_tok, int64_t in);
+int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, void *d_prep, void *stream);
+int fh3_hip_matmul_prepared_dev(const Fh3W *w, const void *d_prep, float *d_y, int n_tok,
+                                const float *d_bias_or_null, void *stream);
+
+/* Kernel selection for fh3_hip_matmul_dev: FH3_HIP_PATH_AUTO picks the
+ * wavefront-per-row-block GEMV for n_tok <= fh3_hip_skinny_max() and the
+ * LDS-staged MFMA GEMM above it; the other two force one kernel (tests). */
+#define FH3_HIP_PATH_AUTO   0
+#define FH3_HIP_PATH_SKINNY 1
+#define FH3_HIP_PATH_GEMM   2
+int fh3_hip_set_path(int path);
+int fh3_hip_skinny_max(void);
+/* The kernel family fh3_hip_matmul_dev would use for n_tok under the current
+ * setting (FH3_HIP_PATH_SKINNY or FH3_HIP_PATH_GEMM). */
+int fh3_hip_matmul_path(int n_tok);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FH3_HIP_H */

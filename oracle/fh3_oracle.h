@@ -1,0 +1,66 @@
+/*
+ * fh3_oracle.h -- CPU restatement of fh3's Q4_K dequantisation and
+ * weight-stationary matmul.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * product in fasth3inc_amd/.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load it, and only as the checker or the
+ * timed CPU baseline -- never as a compute path of the product.
+ *
+ * Every function restates the arithmetic of the reference file:line it cites
+ * (paths relative to the fh3 repository root).  The restatement is pinned by:
+ *   - tests/golden/Q4_K.bin      (gguf-py dequantize output, bit-exact)
+ *   - tests/golden/matmul_ref.bin (fp64 NumPy product, rel-L2 <= 1e-6)
+ *   - tests/golden/ref_vectors.bin (outputs of the reference's own
+ *     fh3_quant.c + fh3_ops.c compiled by oracle/Makefile, bitwise)
+ *   - closed-form cases in tests/test_oracle.py (fp16 decode of every bit
+ *     pattern, all 64x64 scale/min decodings, brute-force small products).
+ * Nothing in this file is "parity unpinned".
+ */
+#ifndef FH3_ORACLE_H
+#define FH3_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same layout as the reference's Fh3W (include/fh3/fh3.h:82-87). */
+typedef struct Fh3OracleW {
+    int type;
+    int64_t in;
+    int64_t out;
+    const uint8_t *data;
+} Fh3OracleW;
+
+/* src/core/fh3_quant.h:20-41 -- exact fp16 -> fp32 (F16C semantics). */
+float fh3_oracle_f16_to_f32(uint16_t h);
+
+/* src/core/fh3_quant.c:14-34 -- bytes of one weight row (F32 and Q4_K). */
+size_t fh3_oracle_row_bytes(int type, int64_t n);
+
+/* src/core/fh3_quant.c:154-196 (Q4_K) and :284-318 (dispatch, F32 + Q4_K). */
+void fh3_oracle_dequant(int type, const void *src, float *dst, int64_t n);
+
+/* src/core/fh3_ops.c:317-404 -- OpenMP over 64-row output tiles.  Output bits
+ * equal the reference's fh3_matmul / _scalar / _avx2 (fh3_ops.c:210-315). */
+void fh3_oracle_matmul(const Fh3OracleW *w, const float *x, float *y,
+                       int n_tok, const float *bias_or_null);
+
+/* Same arithmetic, restricted to output rows [o_begin, o_end) of W; y keeps
+ * the full [n_tok][w->out] layout and only those columns are written.  Used to
+ * check large shapes on a seeded subset of outputs (rows are independent). */
+void fh3_oracle_matmul_rows(const Fh3OracleW *w, const float *x, float *y,
+                            int n_tok, const float *bias_or_null,
+                            int64_t o_begin, int64_t o_end);
+
+/* Number of OpenMP threads the oracle runs with (omp_get_max_threads()). */
+int fh3_oracle_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FH3_ORACLE_H */

@@ -1,0 +1,75 @@
+"""The C-ABI library loads and exports every entry point include/fh3/*.h
+declares (no compute calls: these run without a GPU)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INC = os.path.join(ROOT, "include", "fh3")
+
+
+def declared_functions():
+    names = set()
+    for fn in sorted(os.listdir(INC)):
+        if not fn.endswith(".h"):
+            continue
+        text = open(os.path.join(INC, fn)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        text = re.sub(r"typedef[^;]*;", "", text)
+        text = re.sub(r"#[^\n]*", "", text)
+        for m in re.finditer(r"\b(fh3_[a-z0-9_]+)\s*\(", text):
+            names.add(m.group(1))
+    return names
+
+
+def test_headers_declare_entry_points():
+    names = declared_functions()
+    for must in ("fh3_row_bytes", "fh3_dequant", "fh3_matmul", "fh3_matmul_scalar", "fh3_matmul_avx2",
+                 "fh3_hip_matmul_dev", "fh3_hip_dequant_dev", "fh3_hip_init"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol(fh3):
+    lib = fh3.lib()
+    missing = [n for n in sorted(declared_functions()) if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_binding_table_matches_headers(fh3):
+    declared = declared_functions()
+    extra = [n for n in fh3.SIGNATURES if n not in declared]
+    assert not extra, extra
+    undeclared = [n for n in declared if n not in fh3.SIGNATURES]
+    assert not undeclared, undeclared
+
+
+def test_library_is_gfx950_only_and_has_no_cpu_matmul():
+    lib = os.path.join(ROOT, "fasth3inc_amd", "lib", "libfh3hip.so")
+    out = subprocess.run(["nm", "-D", "--defined-only", lib], capture_output=True, text=True).stdout
+    # no oracle symbols leak into the product
+    assert "fh3_oracle" not in out
+    bundle = subprocess.run(["strings", "-n", "8", lib], capture_output=True, text=True).stdout
+    assert "gfx950" in bundle
+
+
+def test_row_bytes_table(fh3):
+    """Same table as reference src/core/fh3_quant.c:14-34."""
+    rb = fh3.row_bytes
+    assert rb(fh3.FH3_QUANT_Q4_K, 5120) == 2880
+    assert rb(fh3.FH3_QUANT_Q4_K, 4096) == 2304
+    assert rb(fh3.FH3_QUANT_Q4_K, 13824) == 7776
+    assert rb(fh3.FH3_QUANT_Q4_K, 1) == 144
+    assert rb(fh3.FH3_QUANT_F32, 10) == 40
+    assert rb(fh3.FH3_QUANT_Q6_K, 512) == 420
+    assert rb(fh3.FH3_QUANT_Q4_K, 0) == 0 and rb(fh3.FH3_QUANT_Q4_K, -5) == 0
+    assert rb(99, 256) == 0
+
+
+def test_row_bytes_matches_reference_build(fh3, ref):
+    for t in (0, 1, 2, 3, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 30, 99):
+        for n in (1, 31, 32, 255, 256, 5120, 13824):
+            assert fh3.row_bytes(t, n) == ref.fh3_row_bytes(t, n), (t, n)

@@ -1,0 +1,231 @@
+"""GPU parity of the HIP Q4_K path against the CPU oracle, through the C-ABI.
+
+Bars: dequantisation bit-exact; products within rel-Frobenius 2e-3 of the
+oracle (fh3's CPU fh3_matmul), the tolerance the integration target states;
+results bitwise reproducible run to run.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import helpers as H
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3  # max rel-Frobenius error vs the CPU path
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _dev_matmul(F, raw, K, N, x, bias=None, path=None):
+    """Upload, run fh3_hip_matmul_dev, download."""
+    M = x.shape[0]
+    if path is not None:
+        F.set_path(path)
+    try:
+        dw = F.DeviceBuffer.from_array(raw)
+        dx = F.DeviceBuffer.from_array(np.ascontiguousarray(x, dtype=np.float32))
+        dy = F.DeviceBuffer(M * N * 4)
+        db = None if bias is None else F.DeviceBuffer.from_array(np.asarray(bias, dtype=np.float32))
+        F.matmul_dev(dw, K, N, dx, dy, M, db)
+        F.synchronize()
+        return dy.download(np.float32, (M, N))
+    finally:
+        if path is not None:
+            F.set_path(F.PATH_AUTO)
+
+
+def _bits_equal(a, b):
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    return bool(((a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))).all())
+
+
+# --------------------------------------------------------------------------
+# Dequantisation: bit-exact
+# --------------------------------------------------------------------------
+def _dev_dequant(F, raw, rows, n):
+    src = F.DeviceBuffer.from_array(raw)
+    dst = F.DeviceBuffer(rows * n * 4)
+    F.dequant_dev(src, dst, rows, n)
+    F.synchronize()
+    return dst.download(np.float32, (rows, n))
+
+
+def test_dequant_dev_golden_fixture(gpu):
+    _say("dequant_dev: tests/golden/Q4_K.bin 4x512")
+    t, rows, cols, raw, ref = H.read_q4k_fixture()
+    out = _dev_dequant(gpu, raw, rows, cols)
+    assert _bits_equal(out, ref)
+
+
+def test_dequant_host_wrapper_golden_fixture(gpu):
+    t, rows, cols, raw, ref = H.read_q4k_fixture()
+    rb = gpu.row_bytes(12, cols)
+    out = np.stack([gpu.dequant(12, raw[r * rb:(r + 1) * rb], cols) for r in range(rows)])
+    assert _bits_equal(out, ref)
+
+
+def _special_rows(rng, rows, K):
+    raw = H.random_q4k(rng, rows, K).reshape(-1, 144)
+    pats = np.array([0x0000, 0x8000, 0x0001, 0x0155, 0x03FF, 0x0400, 0x7BFF, 0xFBFF, 0xBC00, 0x3C00,
+                     0x1400, 0xB400, 0x7C00, 0xFC00], dtype=np.uint16)
+    raw[:, 0:2] = pats[rng.integers(0, len(pats), raw.shape[0])].view(np.uint8).reshape(-1, 2)
+    raw[:, 2:4] = pats[rng.integers(0, len(pats), raw.shape[0])].view(np.uint8).reshape(-1, 2)
+    raw[::7, 4:16] = 0xFF      # every scale and min = 63
+    raw[::5, 16:] = 0xFF       # every nibble = 15
+    raw[::11, 16:] = 0x00
+    return raw.reshape(-1)
+
+
+@pytest.mark.parametrize("kind", ["random", "special", "pattern"])
+def test_dequant_dev_vs_oracle(gpu, oracle, kind):
+    _say("dequant_dev vs oracle: %s" % kind)
+    rng = np.random.default_rng(7)
+    if kind == "random":
+        rows, K = 37, 5376
+        raw = H.random_q4k(rng, rows, K)
+    elif kind == "special":
+        rows, K = 64, 1024
+        raw = _special_rows(rng, rows, K)
+    else:
+        # the byte pattern (i*37+13) & 0xFF of the reference's tiny.gguf Q4_K
+        # tensor (tools/make_gguf_fixture.py:37-47): 2016 blocks, unusual d/dmin
+        rows, K = 126, 4096
+        raw = ((np.arange(rows * K // 256 * 144) * 37 + 13) & 0xFF).astype(np.uint8)
+    out = _dev_dequant(gpu, raw, rows, K)
+    want = H.oracle_dequant(oracle, raw, rows, K)
+    assert _bits_equal(out, want)
+
+
+# --------------------------------------------------------------------------
+# Matmul vs the reference fixture
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("path", ["skinny", "gemm"])
+def test_matmul_golden_fixture(gpu, oracle, path):
+    """tests/golden/matmul_ref.bin (K=5376, N=192, M=37, bias)."""
+    _say("matmul_ref.bin via %s" % path)
+    t, K, N, M, raw, x, bias, yref = H.read_matmul_fixture()
+    p = gpu.PATH_SKINNY if path == "skinny" else gpu.PATH_GEMM
+    y = _dev_matmul(gpu, raw, K, N, x, bias, path=p)
+    yo = H.oracle_matmul(oracle, raw, K, N, x, bias)
+    assert H.rel_fro(y, yref) <= TOL
+    assert H.rel_fro(y, yo) <= TOL
+
+
+def test_host_fh3_matmul_variants_bitwise(gpu):
+    """reference tests/unit/test_matmul.c:107-141: fh3_matmul, _scalar and _avx2
+    agree bitwise, with and without bias."""
+    t, K, N, M, raw, x, bias, yref = H.read_matmul_fixture()
+    for b in (bias, None):
+        ys = [gpu.matmul(raw, K, N, x, b, variant=v) for v in ("fh3_matmul", "fh3_matmul_scalar", "fh3_matmul_avx2")]
+        assert _bits_equal(ys[0], ys[1]) and _bits_equal(ys[0], ys[2])
+    assert H.rel_fro(gpu.matmul(raw, K, N, x, bias), yref) <= TOL
+
+
+# --------------------------------------------------------------------------
+# Seeded shapes, both kernels, the workload distributions
+# --------------------------------------------------------------------------
+CASES = [
+    # M, K, N, path, x-distribution, weight spread (decades), bias
+    (1, 256, 16, "skinny", "normal", 0.0, False),
+    (1, 5120, 640, "skinny", "normal", 0.0, True),
+    (4, 5120, 512, "skinny", "outliers", 0.0, False),
+    (16, 2048, 200, "skinny", "silu_gated", 2.0, True),
+    (17, 1024, 96, "skinny", "normal", 0.0, False),
+    (33, 1536, 130, "skinny", "outliers", 2.0, True),
+    (64, 4096, 256, "skinny", "normal", 0.0, False),
+    (1, 512, 128, "gemm", "normal", 0.0, False),
+    (65, 1024, 384, "gemm", "normal", 0.0, True),
+    (300, 5120, 256, "gemm", "outliers", 0.0, False),
+    (512, 2560, 200, "gemm", "silu_gated", 2.0, True),
+    (777, 1280, 640, "gemm", "silu_gated", 0.0, False),
+]
+
+
+@pytest.mark.parametrize("M,K,N,path,dist,spread,use_bias", CASES)
+def test_matmul_vs_oracle(gpu, oracle, M, K, N, path, dist, spread, use_bias):
+    _say("matmul M=%d K=%d N=%d %s %s spread=%g bias=%d" % (M, K, N, path, dist, spread, use_bias))
+    seed = M * 131 + K * 7 + N
+    raw = gpu.synth_q4k_weights(seed, 1, N, K, 0.02, spread)
+    x = gpu.synth_x(dist, seed, 2, M, K)
+    bias = gpu.rng_normal(seed, 3, N) if use_bias else None
+    p = gpu.PATH_SKINNY if path == "skinny" else gpu.PATH_GEMM
+    y = _dev_matmul(gpu, raw, K, N, x, bias, path=p)
+    yo = H.oracle_matmul(oracle, raw, K, N, x, bias)
+    err = H.rel_fro(y, yo)
+    _say("  rel_fro = %.3e" % err)
+    assert np.isfinite(y).all()
+    assert err <= TOL
+
+
+def test_matmul_deterministic_and_paths_agree(gpu, oracle):
+    rng = np.random.default_rng(11)
+    K, N, M = 2048, 256, 48
+    raw = H.random_q4k(rng, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    a = _dev_matmul(gpu, raw, K, N, x, path=gpu.PATH_SKINNY)
+    b = _dev_matmul(gpu, raw, K, N, x, path=gpu.PATH_SKINNY)
+    c = _dev_matmul(gpu, raw, K, N, x, path=gpu.PATH_GEMM)
+    d = _dev_matmul(gpu, raw, K, N, x, path=gpu.PATH_GEMM)
+    assert _bits_equal(a, b) and _bits_equal(c, d)
+    assert H.rel_fro(a, c) <= 1e-5  # same fp16 operands, different fp32 summation order
+
+
+def test_matmul_row_scaling_extreme_magnitudes(gpu, oracle):
+    """Rows of 1e-30 and 1e4 magnitude: the per-row power-of-two scale keeps
+    fp16 activations in range."""
+    rng = np.random.default_rng(12)
+    K, N, M = 1024, 128, 6
+    raw = H.random_q4k(rng, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[0] *= 1e-30
+    x[1] *= 1e4
+    x[2] = 0.0
+    for p in (gpu.PATH_SKINNY, gpu.PATH_GEMM):
+        y = _dev_matmul(gpu, raw, K, N, x, path=p)
+        yo = H.oracle_matmul(oracle, raw, K, N, x)
+        for r in (0, 1, 3, 4, 5):
+            assert H.rel_fro(y[r], yo[r]) <= TOL
+        assert (y[2] == 0).all()
+
+
+def test_matmul_dev_rejects_bad_arguments(gpu):
+    F = gpu
+    dw = F.DeviceBuffer(144 * 16)
+    dx = F.DeviceBuffer(4 * 256)
+    dy = F.DeviceBuffer(4 * 16)
+    with pytest.raises(F.Fh3Error) as e:
+        F.matmul_dev(dw, 256, 16, dx, dy, 1, qtype=F.FH3_QUANT_Q6_K)
+    assert e.value.code == F.FH3_E_INVALID
+    with pytest.raises(F.Fh3Error):
+        F.matmul_dev(dw, 200, 16, dx, dy, 1)          # in % 256 != 0
+    with pytest.raises(F.Fh3Error):
+        F.matmul_dev(dw.ptr + 4, 256, 16, dx, dy, 1)  # misaligned weights
+    with pytest.raises(F.Fh3Error):
+        F.matmul_dev(dw, 256, 16, dx, dy, 0)
+
+
+def test_prepared_two_stage_equals_one_call(gpu):
+    """fh3_hip_prepare_x_dev + fh3_hip_matmul_prepared_dev == fh3_hip_matmul_dev,
+    bitwise, for both kernels, with one prepared buffer feeding two weights."""
+    F = gpu
+    rng = np.random.default_rng(13)
+    K = 1024
+    for M in (5, 300):
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        dx = F.DeviceBuffer.from_array(x)
+        prep = F.DeviceBuffer(F.prepared_bytes(M, K))
+        F.prepare_x_dev(dx, M, K, prep)
+        for N in (96, 256):
+            raw = H.random_q4k(rng, N, K)
+            dw = F.DeviceBuffer.from_array(raw)
+            dy = F.DeviceBuffer(M * N * 4)
+            F.matmul_prepared_dev(dw, K, N, prep, dy, M)
+            F.synchronize()
+            two = dy.download(np.float32, (M, N))
+            one = _dev_matmul(F, raw, K, N, x)
+            assert _bits_equal(one, two)

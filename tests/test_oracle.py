@@ -1,0 +1,165 @@
+"""Pins the CPU oracle (oracle/fh3_oracle.c) before it is trusted as the
+checker: golden fixtures of the reference's own tests, the reference build
+itself, and closed forms that a plausible slip (wrong nibble, swapped scale
+bits, dropped term, transposed operand) would fail.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import helpers as H
+
+
+# --------------------------------------------------------------------------
+# Golden fixtures (reference tests/unit/test_quant.c:40-113, test_matmul.c)
+# --------------------------------------------------------------------------
+def test_dequant_q4k_fixture_bitexact(oracle):
+    t, rows, cols, raw, ref = H.read_q4k_fixture()
+    assert (t, rows, cols, raw.size) == (12, 4, 512, 1152)
+    assert H.load_oracle().fh3_oracle_row_bytes(12, cols) * rows == raw.size
+    out = H.oracle_dequant(oracle, raw, rows, cols)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+def test_matmul_fixture_vs_fp64(oracle):
+    """reference tests/unit/test_matmul.c:143-156: rel-L2 <= 1e-6 vs NumPy fp64."""
+    t, K, N, M, raw, x, bias, y = H.read_matmul_fixture()
+    assert (t, K, N, M) == (12, 5376, 192, 37)
+    yo = H.oracle_matmul(oracle, raw, K, N, x, bias)
+    assert H.rel_fro(yo, y) <= 1e-6
+
+
+# --------------------------------------------------------------------------
+# The reference build (oracle/_ref) and the vectors it wrote
+# --------------------------------------------------------------------------
+def _golden():
+    return np.load(os.path.join(H.GOLDEN, "ref_vectors.npz"), allow_pickle=False)
+
+
+@pytest.mark.parametrize("case", range(5))
+def test_matmul_bitwise_vs_reference_vectors(oracle, case):
+    g = _golden()
+    K, N, M, use_bias = (int(v) for v in g["c%d_shape" % case])
+    bias = g["c%d_bias" % case] if use_bias else None
+    y = H.oracle_matmul(oracle, g["c%d_w" % case], K, N, g["c%d_x" % case], bias)
+    yr = g["c%d_y" % case]
+    same = (y.view(np.uint32) == yr.view(np.uint32)) | (np.isnan(y) & np.isnan(yr))
+    assert same.all()
+    deq = H.oracle_dequant(oracle, g["c%d_w" % case], N, K)
+    dr = g["c%d_deq" % case]
+    same = (deq.view(np.uint32) == dr.view(np.uint32)) | (np.isnan(deq) & np.isnan(dr))
+    assert same.all()
+
+
+@pytest.mark.parametrize("K,N,M", [(256, 1, 1), (512, 70, 9), (2048, 129, 4)])
+def test_matmul_bitwise_vs_reference_build(oracle, ref, K, N, M):
+    rng = np.random.default_rng(K + N + M)
+    raw = H.random_q4k(rng, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    for b in (None, bias):
+        yo = H.oracle_matmul(oracle, raw, K, N, x, b)
+        for fn in ("fh3_matmul", "fh3_matmul_scalar", "fh3_matmul_avx2"):
+            yr = H.matmul_with(ref, fn, raw, K, N, x, b)
+            assert np.array_equal(yo.view(np.uint32), yr.view(np.uint32)), fn
+
+
+def test_matmul_rows_subset_equals_full(oracle):
+    rng = np.random.default_rng(5)
+    K, N, M = 512, 200, 3
+    raw = H.random_q4k(rng, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    full = H.oracle_matmul(oracle, raw, K, N, x)
+    part = H.oracle_matmul_rows(oracle, raw, K, N, x, 37, 150)
+    assert np.array_equal(part[:, 37:150].view(np.uint32), full[:, 37:150].view(np.uint32))
+    assert np.isnan(part[:, :37]).all() and np.isnan(part[:, 150:]).all()
+
+
+# --------------------------------------------------------------------------
+# Closed forms
+# --------------------------------------------------------------------------
+def test_f16_decode_all_patterns(oracle):
+    """Every fp16 bit pattern decodes to NumPy's exact float16 -> float32."""
+    f = oracle.fh3_oracle_f16_to_f32
+    hs = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ours = np.array([f(int(h)) for h in hs], dtype=np.float32)
+    theirs = hs.view(np.float16).astype(np.float32)
+    fin = np.isfinite(theirs) | np.isinf(theirs)
+    assert np.array_equal(ours[fin].view(np.uint32), theirs[fin].view(np.uint32))
+    assert np.isnan(ours[~fin]).all()
+    # F16C quiets signalling NaNs: 0x7C01 -> 0x7FC02000
+    assert np.float32(f(0x7C01)).view(np.uint32) == 0x7FC02000
+
+
+def _pack_scales(sc, mn):
+    """6-bit scale/min packing built bit by bit from the format description."""
+    s = np.zeros(12, dtype=np.uint8)
+    for j in range(4):
+        s[j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
+        s[j + 4] = (mn[j] & 63) | ((mn[j + 4] >> 4) << 6)
+        s[j + 8] = (sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4)
+    return s
+
+
+def _block(d_bits, dmin_bits, sc, mn, q):
+    """One super-block from field values; q[g][l] is the nibble of weight l of group g."""
+    blk = np.zeros(144, dtype=np.uint8)
+    blk[0:2] = np.array([d_bits], dtype=np.uint16).view(np.uint8)
+    blk[2:4] = np.array([dmin_bits], dtype=np.uint16).view(np.uint8)
+    blk[4:16] = _pack_scales(sc, mn)
+    for c in range(4):
+        blk[16 + 32 * c:48 + 32 * c] = (q[2 * c] | (q[2 * c + 1] << 4)).astype(np.uint8)
+    return blk
+
+
+def test_scale_min_layout_exhaustive(oracle):
+    """d = dmin = 1 and q = 15 make every weight of group g equal to 15*sc_g - m_g
+    exactly; sweep all 64 x 64 (sc, m) values through all 8 group slots."""
+    q = np.full((8, 32), 15, dtype=np.uint8)
+    blocks, expect = [], []
+    vals = np.arange(64)
+    rng = np.random.default_rng(1)
+    for rep in range(64):
+        sc = rng.permutation(vals)[:8] if rep else np.arange(8)
+        mn = rng.permutation(vals)[:8]
+        sc[rep % 8] = rep
+        blocks.append(_block(0x3C00, 0x3C00, sc, mn, q))
+        expect.append(np.repeat(15.0 * sc - mn, 32))
+    # every (slot, sc) and (slot, m) pair
+    for slot in range(8):
+        for v in range(64):
+            sc = np.zeros(8, dtype=np.int64); mn = np.zeros(8, dtype=np.int64)
+            sc[slot] = v; mn[(slot + 3) % 8] = v
+            blocks.append(_block(0x3C00, 0x3C00, sc, mn, q))
+            expect.append(np.repeat(15.0 * sc - mn, 32))
+    raw = np.concatenate(blocks)
+    out = H.oracle_dequant(oracle, raw, len(blocks), 256)
+    assert np.array_equal(out, np.array(expect, dtype=np.float32))
+
+
+def test_nibble_order(oracle):
+    """q = position pattern: chunk c byte l carries group 2c (low) and 2c+1 (high)."""
+    q = np.array([[(g * 7 + l) % 16 for l in range(32)] for g in range(8)], dtype=np.uint8)
+    blk = _block(0x3C00, 0x0000, np.ones(8, dtype=np.int64), np.zeros(8, dtype=np.int64), q)
+    out = H.oracle_dequant(oracle, blk, 1, 256)[0]
+    assert np.array_equal(out, q.reshape(-1).astype(np.float32))
+
+
+def test_matmul_exact_integers(oracle):
+    """Integer-valued weights and activations small enough that every fp32 sum
+    is exact: the product must equal the int64 matrix product exactly."""
+    rng = np.random.default_rng(3)
+    K, N, M = 512, 23, 5
+    blocks, wint = [], np.zeros((N, K), dtype=np.int64)
+    for o in range(N):
+        for b in range(K // 256):
+            sc = rng.integers(0, 4, 8); mn = rng.integers(0, 8, 8)
+            q = rng.integers(0, 16, (8, 32)).astype(np.uint8)
+            blocks.append(_block(0x3C00, 0x3C00, sc, mn, q))
+            wint[o, b * 256:(b + 1) * 256] = (sc[:, None] * q - mn[:, None]).reshape(-1)
+    raw = np.concatenate(blocks)
+    x = rng.integers(-3, 4, (M, K))
+    bias = rng.integers(-9, 10, N).astype(np.float32)
+    y = H.oracle_matmul(oracle, raw, K, N, x.astype(np.float32), bias)
+    assert np.array_equal(y, (x @ wint.T + bias).astype(np.float32))

@@ -255,6 +255,37 @@ extern "C" int fh3_hip_synchronize(void) {
     return FH3_OK;
 }
 
+extern "C" int fh3_hip_graph_begin(void *stream) {
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    FH3_HIPCALL(hipStreamBeginCapture(stream ? (hipStream_t)stream : g.stream, hipStreamCaptureModeThreadLocal));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_graph_end(void *stream, void **graph_exec) {
+    if (!graph_exec) return set_err(FH3_E_INVALID, "fh3_hip_graph_end: NULL out pointer");
+    hipGraph_t graph = nullptr;
+    FH3_HIPCALL(hipStreamEndCapture(stream ? (hipStream_t)stream : g.stream, &graph));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    *graph_exec = (void *)exec;
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_graph_launch(void *graph_exec, void *stream) {
+    if (!graph_exec) return set_err(FH3_E_INVALID, "fh3_hip_graph_launch: NULL graph");
+    FH3_HIPCALL(hipGraphLaunch((hipGraphExec_t)graph_exec, stream ? (hipStream_t)stream : g.stream));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_graph_destroy(void *graph_exec) {
+    if (!graph_exec) return FH3_OK;
+    FH3_HIPCALL(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+    return FH3_OK;
+}
+
 extern "C" int fh3_hip_set_path(int path) {
     if (path < FH3_HIP_PATH_AUTO || path > FH3_HIP_PATH_GEMM)
         return set_err(FH3_E_INVALID, "fh3_hip_set_path: bad path %d", path);
@@ -288,8 +319,9 @@ static int check_weights(const Fh3W *w, const char *fn) {
         return set_err(FH3_E_INVALID, "%s: unsupported weight type %d (Q4_K only)", fn, w->type);
     if (w->in % 256)
         return set_err(FH3_E_INVALID, "%s: in=%lld is not a multiple of 256", fn, (long long)w->in);
-    if (w->in > (1 << 24) || w->out > 0x7FFFFFFF)
-        return set_err(FH3_E_INVALID, "%s: shape out of range", fn);
+    if (w->in > fh3k_max_in() || w->out > 0x7FFFFFFF)
+        return set_err(FH3_E_INVALID, "%s: in=%lld out=%lld out of range (in <= %d)", fn, (long long)w->in,
+                       (long long)w->out, fh3k_max_in());
     if ((uintptr_t)w->data & 15u) return set_err(FH3_E_INVALID, "%s: weights must be 16-byte aligned", fn);
     return FH3_OK;
 }
@@ -313,7 +345,7 @@ static int prepare(const float *d_x, int n_tok, int64_t in, void *d_prep, int64_
 }
 
 extern "C" int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, void *d_prep, void *stream) {
-    if (!d_x || !d_prep || n_tok <= 0 || in <= 0 || in % 256 || in > (1 << 24))
+    if (!d_x || !d_prep || n_tok <= 0 || in <= 0 || in % 256 || in > fh3k_max_in())
         return set_err(FH3_E_INVALID, "fh3_hip_prepare_x_dev: bad arguments");
     if (((uintptr_t)d_x & 15u) || ((uintptr_t)d_prep & 15u))
         return set_err(FH3_E_INVALID, "fh3_hip_prepare_x_dev: pointers must be 16-byte aligned");

@@ -25,6 +25,9 @@ hipError_t fh3k_skinny(const void *W, int64_t row_bytes, int N, int K, const voi
                        const float *xs_inv, const float *bias, float *y, int M, hipStream_t st);
 int fh3k_skinny_max_tokens(void);
 
+// Largest in-dimension (K) the activation preparation handles.
+int fh3k_max_in(void);
+
 // y = x * W^T (+bias) from prepared fragments; x16 must hold
 // round_up(M, fh3k_gemm_row_pad()) rows.
 hipError_t fh3k_gemm(const void *W, int64_t row_bytes, int N, int K, const void *x16,

@@ -83,21 +83,45 @@ __device__ __forceinline__ void q4k_group(const u32x4 hdr, int g, float &D, floa
     Mn = __fmul_rn(dmin, (float)mn);
 }
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// Product-path group constants.  The hardware fp16 -> fp32 conversion is exact;
+// D = d*sc and Mn = dmin*m are rounded once as in the reference, and the
+// offset is folded with the magic bias of q4k_deq8_f16: C = -(Mn + 1024*D).
+__device__ __forceinline__ void q4k_group_fast(const u32x4 hdr, int g, float &D, float &C) {
+    uint32_t sc, mn;
+    q4k_scale_min(hdr.y, hdr.z, hdr.w, g, sc, mn);
+    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x & 0xFFFFu));
+    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x >> 16));
+    D = d * (float)sc;
+    C = -(dmin * (float)mn + 1024.0f * D);
+}
+
+// Two nibble bytes (q0, q1 in bytes sel-picked from a) as the fp16 pair
+// (1024 + q0, 1024 + q1): exponent byte 0x64 above each nibble (v_perm_b32).
+__device__ __forceinline__ half2v q4k_magic_pair(uint32_t a, uint32_t sel) {
+    return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, a, sel));
+}
+
 // Eight weights of one group from 8 bytes (u0 = bytes 0-3, u1 = bytes 4-7),
-// low nibbles (hi == false) or high nibbles, as fp16 for the MFMA B/A operand:
-// fma(D, q, -Mn) in fp32 rounded once to fp16 (v_fma_mix).
-__device__ __forceinline__ half8 q4k_deq8_f16(uint32_t u0, uint32_t u1, bool hi, float D, float Mn) {
+// low nibbles (hi == false) or high nibbles, as fp16 for an MFMA operand:
+// fma(D, 1024 + q, C) = D*q - Mn evaluated in fp32 and rounded once to fp16
+// (v_fma_mix).  C carries an fp32 rounding of at most 2^-24 * 1024 * D, far
+// below the fp16 rounding of the result.
+__device__ __forceinline__ half8 q4k_deq8_f16(uint32_t u0, uint32_t u1, bool hi, float D, float C) {
     const uint32_t a = (hi ? (u0 >> 4) : u0) & 0x0F0F0F0Fu;
     const uint32_t b = (hi ? (u1 >> 4) : u1) & 0x0F0F0F0Fu;
+    const half2v p0 = q4k_magic_pair(a, 0x04010400u), p1 = q4k_magic_pair(a, 0x04030402u);
+    const half2v p2 = q4k_magic_pair(b, 0x04010400u), p3 = q4k_magic_pair(b, 0x04030402u);
     half8 r;
-    r[0] = (_Float16)__builtin_fmaf(D, (float)(a & 0xFFu), -Mn);
-    r[1] = (_Float16)__builtin_fmaf(D, (float)((a >> 8) & 0xFFu), -Mn);
-    r[2] = (_Float16)__builtin_fmaf(D, (float)((a >> 16) & 0xFFu), -Mn);
-    r[3] = (_Float16)__builtin_fmaf(D, (float)(a >> 24), -Mn);
-    r[4] = (_Float16)__builtin_fmaf(D, (float)(b & 0xFFu), -Mn);
-    r[5] = (_Float16)__builtin_fmaf(D, (float)((b >> 8) & 0xFFu), -Mn);
-    r[6] = (_Float16)__builtin_fmaf(D, (float)((b >> 16) & 0xFFu), -Mn);
-    r[7] = (_Float16)__builtin_fmaf(D, (float)(b >> 24), -Mn);
+    r[0] = (_Float16)__builtin_fmaf(D, (float)p0[0], C);
+    r[1] = (_Float16)__builtin_fmaf(D, (float)p0[1], C);
+    r[2] = (_Float16)__builtin_fmaf(D, (float)p1[0], C);
+    r[3] = (_Float16)__builtin_fmaf(D, (float)p1[1], C);
+    r[4] = (_Float16)__builtin_fmaf(D, (float)p2[0], C);
+    r[5] = (_Float16)__builtin_fmaf(D, (float)p2[1], C);
+    r[6] = (_Float16)__builtin_fmaf(D, (float)p3[0], C);
+    r[7] = (_Float16)__builtin_fmaf(D, (float)p3[1], C);
     return r;
 }
 
@@ -144,74 +168,177 @@ __global__ __launch_bounds__(256) void k_dequant_q4k_f32(const uint8_t *__restri
 }
 
 // ---------------------------------------------------------------------------
-// Activation preparation.  One workgroup per 32-token block T.  Row t gets the
-// scale 2^e with e = 15 - E, where max|x_t| = f * 2^E (f in [0.5, 1)), so the
-// largest magnitude lands in [2^14, 2^15): fp16 never overflows and small rows
-// keep full fp16 precision.  xs_inv[t] = 2^-e undoes it in the epilogue.
-// Rows M..Mpad-1 are written as zeros.
+// Activation preparation.  One 256-thread workgroup per token row t, the whole
+// row held in registers (V4 float4 per thread, K <= 1024 * V4).  Row t gets
+// the scale 2^e with e = 15 - E, where max|x_t| = f * 2^E (f in [0.5, 1)), so
+// its largest magnitude lands in [2^14, 2^15): fp16 never overflows and small
+// rows keep full fp16 precision.  xs_inv[t] = 2^-e undoes it in the epilogue.
+// Rows M..Mpad-1 are written as zeros.  Thread i owns float4 i, i+256, ...;
+// float4 k4 is half (k4 & 1) of the 8 fp16 lane slot (t%32 + 32*((k4/2)&1))
+// of fragment (t/32, k4/4).
 // ---------------------------------------------------------------------------
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+
+template <int V4>
 __global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ X, int M, int K,
                                                half8 *__restrict__ X16, float *__restrict__ xs_inv) {
-    __shared__ float s_scale[32];
-    const int T = blockIdx.x;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int rr = 0; rr < 8; rr++) {
-        const int r = wave * 8 + rr;
-        const int t = T * 32 + r;
-        float mx = 0.f;
-        if (t < M) {
-            const f32x4 *xr = reinterpret_cast<const f32x4 *>(X + (size_t)t * K);
-            for (int k4 = lane; k4 < K / 4; k4 += 64) {
-                const f32x4 v = xr[k4];
-                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-            }
-        }
+    __shared__ float s_red[4];
+    const int t = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n4 = K / 4;
+    const f32x4 *xr = reinterpret_cast<const f32x4 *>(X + (size_t)t * K);
+    f32x4 v[V4];
+    float mx = 0.f;
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-        if (lane == 0) {
-            int e = 0;
-            if (mx > 0.f && mx <= 3.4028234663852886e38f) {
-                int E;
-                (void)frexpf(mx, &E);
-                e = 15 - E;
-                e = e > 126 ? 126 : (e < -126 ? -126 : e);
-            }
-            s_scale[r] = ldexpf(1.0f, e);
-            xs_inv[t] = ldexpf(1.0f, -e);
-        }
+    for (int i = 0; i < V4; i++) {
+        const int k4 = tid + 256 * i;
+        v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (t < M && k4 < n4) v[i] = xr[k4];
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
     }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (lane == 0) s_red[wave] = mx;
     __syncthreads();
+    mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    int e = 0;
+    if (mx > 0.f && mx <= 3.4028234663852886e38f) {
+        int E;
+        (void)frexpf(mx, &E);
+        e = 15 - E;
+        e = e > 126 ? 126 : (e < -126 ? -126 : e);
+    }
+    const float s = ldexpf(1.0f, e);
+    if (tid == 0) xs_inv[t] = ldexpf(1.0f, -e);
     const int kf_n = K / 16;
-    const int tl = lane & 31;
-    const int t = T * 32 + tl;
-    const float s = s_scale[tl];
-    const int koff = 8 * (lane >> 5);
-    for (int kf = wave; kf < kf_n; kf += 4) {
-        half8 h = {};
-        if (t < M) {
-            const f32x4 *p = reinterpret_cast<const f32x4 *>(X + (size_t)t * K + kf * 16 + koff);
-            const f32x4 a = p[0], b = p[1];
-            h[0] = (_Float16)(a.x * s); h[1] = (_Float16)(a.y * s);
-            h[2] = (_Float16)(a.z * s); h[3] = (_Float16)(a.w * s);
-            h[4] = (_Float16)(b.x * s); h[5] = (_Float16)(b.y * s);
-            h[6] = (_Float16)(b.z * s); h[7] = (_Float16)(b.w * s);
+    half4 *dst = reinterpret_cast<half4 *>(X16 + (size_t)(t >> 5) * kf_n * 64 + (t & 31));
+#pragma unroll
+    for (int i = 0; i < V4; i++) {
+        const int k4 = tid + 256 * i;
+        if (k4 < n4) {
+            const half4 h = {(_Float16)(v[i].x * s), (_Float16)(v[i].y * s), (_Float16)(v[i].z * s),
+                             (_Float16)(v[i].w * s)};
+            // fragment k4/4, lane half (k4/2)&1, 8-byte half k4&1
+            dst[(size_t)(k4 >> 2) * 128 + ((k4 >> 1) & 1) * 64 + (k4 & 1)] = h;
         }
-        X16[((size_t)T * kf_n + kf) * 64 + lane] = h;
     }
 }
 
 // ---------------------------------------------------------------------------
 // Small-M kernel.  Workgroup = NW wavefronts over 16 consecutive weight rows
-// o0..o0+15; wavefront w takes super-blocks sb = w, w+NW, ...
+// o0..o0+15; wavefront w takes super-blocks sb = w, w+NW, ...  in batches of
+// SBB: all weight loads of a batch are issued before any of it is computed, so
+// a wavefront keeps up to SBB * 2304 bytes in flight.
 // MFMA 16x16x32: B lane l = (row j = l%16, chunk q = l/16) loads the 32 bytes of
 // chunk q (both of its groups 2q and 2q+1) plus the 16-byte header, i.e. each
 // super-block of a row is read once, 144 B by 4 lanes.  MFMA m (0..7) takes from
 // lane (j, q) the 8 weights of group 2q + m/4 at offsets 8*(m%4)..+7; the A
 // lane (token i, q) loads the activations of the same k, one 16-byte piece of
-// an X16 fragment.  Partial sums of the NW waves are added in wave order
-// through LDS (deterministic).
+// an X16 fragment (lanes of padding tokens load nothing).  Partial sums of the
+// NW waves are added in wave order through LDS (deterministic).
 // ---------------------------------------------------------------------------
-template <int TB, int NW>
+// Lane-constant field positions of the 6-bit scale/min of group g
+// (reference src/core/fh3_quant.c:168-177): low 4 bits come from byte g of the
+// scale (min) word pair when g < 4, else from the low (high) nibble of byte
+// 8 + g%4; the top 2 bits from bits 4-5 of byte g (g < 4) or bits 6-7 of byte
+// g%4 of the scale (min) word.
+struct Q4kField {
+    int lo_sh;   // shift of the 4 low bits in the selected word
+    int hi_sh;   // shift of the 2 high bits in the scale / min word
+    bool upper;  // g >= 4: low bits live in word s2
+};
+
+__device__ __forceinline__ Q4kField q4k_field(int g) {
+    Q4kField f;
+    const int j = g & 3;
+    f.upper = g >= 4;
+    f.lo_sh = 8 * j;
+    f.hi_sh = 8 * j + (f.upper ? 6 : 4);
+    return f;
+}
+
+__device__ __forceinline__ uint32_t q4k_sc(const u32x4 h, const Q4kField f) {
+    const uint32_t lo = f.upper ? (h.w >> f.lo_sh) : (h.y >> f.lo_sh);
+    return (lo & 15u) | (((h.y >> f.hi_sh) & 3u) << 4);
+}
+
+__device__ __forceinline__ uint32_t q4k_mn(const u32x4 h, const Q4kField f) {
+    const uint32_t lo = f.upper ? (h.w >> (f.lo_sh + 4)) : (h.z >> f.lo_sh);
+    return (lo & 15u) | (((h.z >> f.hi_sh) & 3u) << 4);
+}
+
+__device__ __forceinline__ half2v splat2(uint32_t v) {
+    const _Float16 h = (_Float16)(float)v;
+    return half2v{h, h};
+}
+
+// Eight exact integer weights sc*q (<= 945) of one group as fp16, from 8 bytes
+// of nibbles: (1024 + q) * sc - 1024 * sc in one fused fp16 op per pair
+// (v_pk_fma_f16; the fused result is an integer below 2048, hence exact).
+__device__ __forceinline__ half8 q4k_scq8_f16(uint32_t u0, uint32_t u1, bool hi, half2v sc2, half2v nsc2) {
+    const uint32_t a = (hi ? (u0 >> 4) : u0) & 0x0F0F0F0Fu;
+    const uint32_t b = (hi ? (u1 >> 4) : u1) & 0x0F0F0F0Fu;
+    const half2v p0 = __builtin_elementwise_fma(q4k_magic_pair(a, 0x04010400u), sc2, nsc2);
+    const half2v p1 = __builtin_elementwise_fma(q4k_magic_pair(a, 0x04030402u), sc2, nsc2);
+    const half2v p2 = __builtin_elementwise_fma(q4k_magic_pair(b, 0x04010400u), sc2, nsc2);
+    const half2v p3 = __builtin_elementwise_fma(q4k_magic_pair(b, 0x04030402u), sc2, nsc2);
+    return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+// One super-block of the small-M product with exact weights.  With
+// w = d*sc_g*q - dmin*m_g, the super-block contributes
+//   d * sum_k (sc_g q)_k x_k - dmin * sum_k m_g(k) x_k,
+// two MFMA chains over the same activation fragments (B = sc*q, and B = m
+// broadcast over each group), scaled by d and dmin in fp32 afterwards.
+template <int TB>
+__device__ __forceinline__ void skinny_superblock(const u32x4 hv, const u32x4 ca, const u32x4 cb, int sb,
+                                                  int q, const Q4kField flo, const Q4kField fhi,
+                                                  const half8 *const xb[TB], f32x4 acc[TB]) {
+    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hv.x & 0xFFFFu));
+    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hv.x >> 16));
+    const uint32_t sclo = q4k_sc(hv, flo), schi = q4k_sc(hv, fhi);
+    const half2v sc_lo = splat2(sclo), sc_hi = splat2(schi);
+    const half2v nsc_lo = splat2(sclo) * (_Float16)-1024.0f, nsc_hi = splat2(schi) * (_Float16)-1024.0f;
+    const half2v m_lo = splat2(q4k_mn(hv, flo)), m_hi = splat2(q4k_mn(hv, fhi));
+    const half8 bm_lo = half8{m_lo[0], m_lo[1], m_lo[0], m_lo[1], m_lo[0], m_lo[1], m_lo[0], m_lo[1]};
+    const half8 bm_hi = half8{m_hi[0], m_hi[1], m_hi[0], m_hi[1], m_hi[0], m_hi[1], m_hi[0], m_hi[1]};
+    const int kf_sb = sb * 16 + 4 * q;  // fragment of group 2q, offset 0
+    half8 a[8][TB];
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        // k = sb*256 + (2q + m/4)*32 + 8*(m%4) -> fragment kf_sb + 2*(m/4) + (m%4)/2,
+        // lane half (m % 2) of it
+        const int kf = kf_sb + (m >= 4 ? 2 : 0) + ((m & 3) >> 1);
+        const int lsel = (m & 1) * 32;
+#pragma unroll
+        for (int tb = 0; tb < TB; tb++) a[m][tb] = xb[tb][(size_t)kf * 64 + lsel];
+    }
+    f32x4 aq[TB], am[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++) aq[tb] = am[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        const int part = m & 3;
+        const bool hi = m >= 4;
+        const u32x4 cv = part < 2 ? ca : cb;
+        const uint32_t u0 = (part & 1) ? cv.z : cv.x;
+        const uint32_t u1 = (part & 1) ? cv.w : cv.y;
+        const half8 b = q4k_scq8_f16(u0, u1, hi, hi ? sc_hi : sc_lo, hi ? nsc_hi : nsc_lo);
+#pragma unroll
+        for (int tb = 0; tb < TB; tb++) {
+            aq[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][tb], b, aq[tb], 0, 0, 0);
+            am[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][tb], hi ? bm_hi : bm_lo, am[tb], 0, 0, 0);
+        }
+    }
+    // d and dmin belong to the weight row j = lane % 16, which is the output
+    // column this lane holds
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) acc[tb][v] = __builtin_fmaf(d, aq[tb][v], __builtin_fmaf(-dmin, am[tb][v], acc[tb][v]));
+}
+
+template <int TB, int NW, int SBB>
 __global__ __launch_bounds__(NW * 64) void k_skinny(const uint8_t *__restrict__ W, int64_t row_bytes,
                                                     int N, int K, const half8 *__restrict__ X16,
                                                     const float *__restrict__ xs_inv,
@@ -228,55 +355,46 @@ __global__ __launch_bounds__(NW * 64) void k_skinny(const uint8_t *__restrict__ 
     const int kf_n = K / 16;
 
     f32x4 acc[TB];
-#pragma unroll
-    for (int tb = 0; tb < TB; tb++) acc[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // A-operand base per token block: token i = tb*16 + j
     const half8 *xb[TB];
 #pragma unroll
     for (int tb = 0; tb < TB; tb++) {
-        const int t = tb * 16 + j;
+        acc[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // A-operand token of this lane; padding tokens re-read the last real
+        // row (their output rows are never stored)
+        int t = tb * 16 + j;
+        t = t < M ? t : M - 1;
         xb[tb] = X16 + (size_t)(t >> 5) * kf_n * 64 + (t & 31);
     }
+    const Q4kField flo = q4k_field(2 * q), fhi = q4k_field(2 * q + 1);
 
-    int sb = wave;
-    u32x4 h0 = {}, c0a = {}, c0b = {}, h1 = {}, c1a = {}, c1b = {};
-    if (sb < nsb) {
-        const uint8_t *blk = wrow + (size_t)sb * 144;
-        h0 = ld16(blk); c0a = ld16(blk + 16 + 32 * q); c0b = ld16(blk + 32 + 32 * q);
-    }
-    if (sb + NW < nsb) {
-        const uint8_t *blk = wrow + (size_t)(sb + NW) * 144;
-        h1 = ld16(blk); c1a = ld16(blk + 16 + 32 * q); c1b = ld16(blk + 32 + 32 * q);
-    }
-    for (; sb < nsb; sb += NW) {
-        float Dlo, Mlo, Dhi, Mhi;
-        q4k_group(h0, 2 * q, Dlo, Mlo);
-        q4k_group(h0, 2 * q + 1, Dhi, Mhi);
-        const u32x4 ca = c0a, cb = c0b;
-        // rotate the two-deep prefetch
-        h0 = h1; c0a = c1a; c0b = c1b;
-        if (sb + 2 * NW < nsb) {
-            const uint8_t *blk = wrow + (size_t)(sb + 2 * NW) * 144;
-            h1 = ld16(blk); c1a = ld16(blk + 16 + 32 * q); c1b = ld16(blk + 32 + 32 * q);
+    // Rotating SBB-deep pipeline over this wavefront's super-blocks
+    // sb_i = wave + i*NW: slot s holds sb_i for i = s (mod SBB); after slot s is
+    // consumed it is refilled with sb_{i+SBB}, so SBB-1 super-blocks stay in
+    // flight while one is computed.
+    const int cnt = nsb > wave ? (nsb - wave + NW - 1) / NW : 0;
+    u32x4 hv[SBB], ca[SBB], cb[SBB];
+#pragma unroll
+    for (int s = 0; s < SBB; s++) {
+        if (s < cnt) {
+            const uint8_t *blk = wrow + (size_t)(wave + s * NW) * 144;
+            hv[s] = ld16(blk);
+            ca[s] = ld16(blk + 16 + 32 * q);
+            cb[s] = ld16(blk + 32 + 32 * q);
         }
-        const int kf_sb = sb * 16 + 4 * q;  // fragment of group 2q, offset 0
+    }
+    for (int i0 = 0; i0 < cnt; i0 += SBB) {
 #pragma unroll
-        for (int m = 0; m < 8; m++) {
-            const int part = m & 3;
-            const bool hi = m >= 4;
-            const u32x4 cv = part < 2 ? ca : cb;
-            const uint32_t u0 = (part & 1) ? cv.z : cv.x;
-            const uint32_t u1 = (part & 1) ? cv.w : cv.y;
-            const half8 b = q4k_deq8_f16(u0, u1, hi, hi ? Dhi : Dlo, hi ? Mhi : Mlo);
-            // k = sb*256 + (2q + hi)*32 + 8*part -> fragment kf_sb + 2*hi + part/2,
-            // half (part & 1) of it
-            const int kf = kf_sb + (hi ? 2 : 0) + (part >> 1);
-            const int lsel = (part & 1) * 32;
-#pragma unroll
-            for (int tb = 0; tb < TB; tb++) {
-                const half8 a = xb[tb][(size_t)kf * 64 + lsel];
-                acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[tb], 0, 0, 0);
+        for (int s = 0; s < SBB; s++) {
+            const int i = i0 + s;
+            if (i < cnt) {
+                const u32x4 h = hv[s], a = ca[s], b = cb[s];
+                if (i + SBB < cnt) {
+                    const uint8_t *blk = wrow + (size_t)(wave + (i + SBB) * NW) * 144;
+                    hv[s] = ld16(blk);
+                    ca[s] = ld16(blk + 16 + 32 * q);
+                    cb[s] = ld16(blk + 32 + 32 * q);
+                }
+                skinny_superblock<TB>(h, a, b, wave + i * NW, q, flo, fhi, xb, acc);
             }
         }
     }
@@ -364,13 +482,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
         const int buf = s & 1;
         const int c = s & 3;
         {
-            float Dlo, Mlo, Dhi, Mhi;
-            q4k_group(hv, 2 * c, Dlo, Mlo);
-            q4k_group(hv, 2 * c + 1, Dhi, Mhi);
-            lds[buf][wf + h][wl] = q4k_deq8_f16(qv.x, qv.y, false, Dlo, Mlo);
-            lds[buf][wf + h][wl + 32] = q4k_deq8_f16(qv.z, qv.w, false, Dlo, Mlo);
-            lds[buf][wf + 2 + h][wl] = q4k_deq8_f16(qv.x, qv.y, true, Dhi, Mhi);
-            lds[buf][wf + 2 + h][wl + 32] = q4k_deq8_f16(qv.z, qv.w, true, Dhi, Mhi);
+            float Dlo, Clo, Dhi, Chi;
+            q4k_group_fast(hv, 2 * c, Dlo, Clo);
+            q4k_group_fast(hv, 2 * c + 1, Dhi, Chi);
+            lds[buf][wf + h][wl] = q4k_deq8_f16(qv.x, qv.y, false, Dlo, Clo);
+            lds[buf][wf + h][wl + 32] = q4k_deq8_f16(qv.z, qv.w, false, Dlo, Clo);
+            lds[buf][wf + 2 + h][wl] = q4k_deq8_f16(qv.x, qv.y, true, Dhi, Chi);
+            lds[buf][wf + 2 + h][wl + 32] = q4k_deq8_f16(qv.z, qv.w, true, Dhi, Chi);
         }
         half8 xn[2][4];
         if (s + 1 < S) {
@@ -438,18 +556,39 @@ extern "C" hipError_t fh3k_dequant_q4k_f32(const void *src, int64_t row_bytes, i
 
 extern "C" hipError_t fh3k_xprep(const float *x, int M, int K, int Mpad, void *x16, float *xs_inv,
                                  hipStream_t st) {
-    hipLaunchKernelGGL(k_xprep, dim3((unsigned)(Mpad / 32)), dim3(256), 0, st, x, M, K, (half8 *)x16,
-                       xs_inv);
+    const dim3 grid((unsigned)Mpad), block(256);
+    if (K <= 4096)
+        hipLaunchKernelGGL(k_xprep<4>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv);
+    else if (K <= 8192)
+        hipLaunchKernelGGL(k_xprep<8>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv);
+    else if (K <= 16384)
+        hipLaunchKernelGGL(k_xprep<16>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv);
+    else if (K <= 32768)
+        hipLaunchKernelGGL(k_xprep<32>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+extern "C" int fh3k_max_in(void) { return 32768; }
+
+// NW = 8 wavefronts split K when there are few 16-row blocks (so that the
+// chip holds enough bytes in flight), 4 otherwise; SBB = super-blocks per
+// wavefront batch.
+template <int TB, int NW>
+static hipError_t launch_skinny_nw(const void *W, int64_t rb, int N, int K, const void *x16,
+                                   const float *xs_inv, const float *bias, float *y, int M, hipStream_t st) {
+    const unsigned blocks = (unsigned)((N + 15) / 16);
+    hipLaunchKernelGGL((k_skinny<TB, NW, 3>), dim3(blocks), dim3(NW * 64), 0, st, (const uint8_t *)W, rb, N, K,
+                       (const half8 *)x16, xs_inv, bias, y, M);
     return hipGetLastError();
 }
 
 template <int TB>
 static hipError_t launch_skinny(const void *W, int64_t rb, int N, int K, const void *x16,
                                 const float *xs_inv, const float *bias, float *y, int M, hipStream_t st) {
-    const unsigned blocks = (unsigned)((N + 15) / 16);
-    hipLaunchKernelGGL((k_skinny<TB, 4>), dim3(blocks), dim3(256), 0, st, (const uint8_t *)W, rb, N, K,
-                       (const half8 *)x16, xs_inv, bias, y, M);
-    return hipGetLastError();
+    if ((N + 15) / 16 < 768) return launch_skinny_nw<TB, 8>(W, rb, N, K, x16, xs_inv, bias, y, M, st);
+    return launch_skinny_nw<TB, 4>(W, rb, N, K, x16, xs_inv, bias, y, M, st);
 }
 
 extern "C" hipError_t fh3k_skinny(const void *W, int64_t row_bytes, int N, int K, const void *x16,

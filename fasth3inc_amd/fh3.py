@@ -84,6 +84,10 @@ SIGNATURES = {
     "fh3_hip_prepare_x_dev": (_c_int, [_c_void_p, _c_int, _c_i64, _c_void_p, _c_void_p]),
     "fh3_hip_matmul_prepared_dev": (_c_int, [ctypes.POINTER(Fh3W), _c_void_p, _c_void_p, _c_int, _c_void_p,
                                              _c_void_p]),
+    "fh3_hip_graph_begin": (_c_int, [_c_void_p]),
+    "fh3_hip_graph_end": (_c_int, [_c_void_p, ctypes.POINTER(_c_void_p)]),
+    "fh3_hip_graph_launch": (_c_int, [_c_void_p, _c_void_p]),
+    "fh3_hip_graph_destroy": (_c_int, [_c_void_p]),
     "fh3_hip_set_path": (_c_int, [_c_int]),
     "fh3_hip_skinny_max": (_c_int, []),
     "fh3_hip_matmul_path": (_c_int, [_c_int]),
@@ -255,6 +259,39 @@ def matmul_prepared_dev(d_w, K, N, d_prep, d_y, n_tok, d_bias=None, stream_ptr=N
     w = Fh3W(qtype, K, N, _ptr_of(d_w))
     _check(lib().fh3_hip_matmul_prepared_dev(ctypes.byref(w), _ptr_of(d_prep), _ptr_of(d_y), n_tok,
                                              _ptr_of(d_bias), stream_ptr), "fh3_hip_matmul_prepared_dev")
+
+
+class Graph:
+    """A captured HIP graph of fh3_hip_* calls (see fh3_hip_graph_begin)."""
+
+    def __init__(self, exec_ptr):
+        self.ptr = exec_ptr
+
+    def launch(self, stream_ptr=None):
+        _check(lib().fh3_hip_graph_launch(self.ptr, stream_ptr), "fh3_hip_graph_launch")
+
+    def close(self):
+        if self.ptr:
+            lib().fh3_hip_graph_destroy(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def capture(fn, stream_ptr=None):
+    """Capture the fh3_hip_* work fn() enqueues on the stream into a Graph."""
+    _check(lib().fh3_hip_graph_begin(stream_ptr), "fh3_hip_graph_begin")
+    try:
+        fn()
+    finally:
+        ex = ctypes.c_void_p()
+        rc = lib().fh3_hip_graph_end(stream_ptr, ctypes.byref(ex))
+    _check(rc, "fh3_hip_graph_end")
+    return Graph(ex.value)
 
 
 def dequant_dev(d_src, d_dst, rows, n, qtype=FH3_QUANT_Q4_K, stream_ptr=None):

@@ -72,6 +72,16 @@ int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, void *d_prep,
 int fh3_hip_matmul_prepared_dev(const Fh3W *w, const void *d_prep, float *d_y, int n_tok,
                                 const float *d_bias_or_null, void *stream);
 
+/* HIP graph capture of work enqueued on a stream (NULL = the compute
+ * stream), for launch-bound loops such as small-M text-encoder layers:
+ * begin, enqueue fh3_hip_* calls on that stream, end -> an executable graph
+ * that fh3_hip_graph_launch replays on any stream.  Calls captured this way
+ * must not need to grow the library workspace (run them once eagerly first). */
+int fh3_hip_graph_begin(void *stream);
+int fh3_hip_graph_end(void *stream, void **graph_exec);
+int fh3_hip_graph_launch(void *graph_exec, void *stream);
+int fh3_hip_graph_destroy(void *graph_exec);
+
 /* Kernel selection for fh3_hip_matmul_dev: FH3_HIP_PATH_AUTO picks the
  * wavefront-per-row-block GEMV for n_tok <= fh3_hip_skinny_max() and the
  * LDS-staged MFMA GEMM above it; the other two force one kernel (tests). */

@@ -172,7 +172,11 @@ def test_matmul_deterministic_and_paths_agree(gpu, oracle):
     c = _dev_matmul(gpu, raw, K, N, x, path=gpu.PATH_GEMM)
     d = _dev_matmul(gpu, raw, K, N, x, path=gpu.PATH_GEMM)
     assert _bits_equal(a, b) and _bits_equal(c, d)
-    assert H.rel_fro(a, c) <= 1e-5  # same fp16 operands, different fp32 summation order
+    yo = H.oracle_matmul(oracle, raw, K, N, x)
+    # the small-M kernel keeps the weights exact (only activations are fp16);
+    # the GEMM rounds dequantised weights to fp16 once
+    assert H.rel_fro(a, yo) <= 3e-4
+    assert H.rel_fro(c, yo) <= 6e-4
 
 
 def test_matmul_row_scaling_extreme_magnitudes(gpu, oracle):
@@ -229,3 +233,43 @@ def test_prepared_two_stage_equals_one_call(gpu):
             two = dy.download(np.float32, (M, N))
             one = _dev_matmul(F, raw, K, N, x)
             assert _bits_equal(one, two)
+
+
+def test_graph_replay_matches_eager(gpu):
+    """A captured sequence (two products, both kernel families) replayed
+    several times, with eager work and synchronisations between replays;
+    every replay must equal the eager result bitwise."""
+    F = gpu
+    rng = np.random.default_rng(21)
+    K, N = 1024, 320
+    raw = H.random_q4k(rng, N, K)
+    dw = F.DeviceBuffer.from_array(raw)
+    outs = []
+    for M in (4, 260):
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        dx = F.DeviceBuffer.from_array(x)
+        dy = F.DeviceBuffer(M * N * 4)
+        F.matmul_dev(dw, K, N, dx, dy, M)   # eager (also sizes the workspace)
+        F.synchronize()
+        outs.append((M, dx, dy, dy.download(np.float32, (M, N))))
+
+    def seq():
+        for M, dx, dy, _ in outs:
+            F.matmul_dev(dw, K, N, dx, dy, M)
+
+    g = F.capture(seq)
+    try:
+        for rep in range(4):
+            for M, dx, dy, _ in outs:
+                dy.fill(0)
+            # unrelated eager work between replays
+            F.matmul_dev(dw, K, N, outs[0][1], outs[0][2], outs[0][0])
+            for M, dx, dy, _ in outs:
+                dy.fill(0)
+            F.synchronize()
+            g.launch()
+            F.synchronize()
+            for M, dx, dy, ref in outs:
+                assert _bits_equal(dy.download(np.float32, (M, N)), ref), (rep, M)
+    finally:
+        g.close()

@@ -8,8 +8,9 @@
 // Kernels
 //   k_dequant_q4k_f32   bit-exact fp32 dequantisation (parity / debug path)
 //   k_xprep             fp32 activations -> fp16 MFMA fragments, per-row 2^e scale
-//   k_skinny<TB,NW>     small n_tok: one wavefront per 16 weight rows per K slice,
-//                       v_mfma_f32_16x16x32_f16, K split over NW waves, LDS reduce
+//   k_skinny<TB,C>      small n_tok: one wavefront per 16 weight rows per K slice of
+//                       C super-blocks, exact weights (sc*q in fp16), two
+//                       v_mfma_f32_16x16x32_f16 chains, LDS reduce over the slices
 //   k_gemm              large n_tok: 256x128 output tile, Q4_K dequantised into LDS
 //                       as fp16, v_mfma_f32_32x32x16_f16, fp32 accumulation
 //
@@ -285,34 +286,39 @@ __device__ __forceinline__ half8 q4k_scq8_f16(uint32_t u0, uint32_t u1, bool hi,
     return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
+// Activation fragments of super-block sb for MFMA m = 0..7 of lane (token, q):
+// k = sb*256 + (2q + m/4)*32 + 8*(m%4) -> fragment sb*16 + 4q + 2*(m/4) + (m%4)/2,
+// lane half (m % 2) of it.
+template <int TB>
+__device__ __forceinline__ void skinny_load_a(const half8 *const xb[TB], int sb, int q, half8 (&a)[8][TB]) {
+    const int kf_sb = sb * 16 + 4 * q;
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        const int kf = kf_sb + (m >= 4 ? 2 : 0) + ((m & 3) >> 1);
+        const int lsel = (m & 1) * 32;
+#pragma unroll
+        for (int tb = 0; tb < TB; tb++) a[m][tb] = xb[tb][(size_t)kf * 64 + lsel];
+    }
+}
+
 // One super-block of the small-M product with exact weights.  With
 // w = d*sc_g*q - dmin*m_g, the super-block contributes
 //   d * sum_k (sc_g q)_k x_k - dmin * sum_k m_g(k) x_k,
 // two MFMA chains over the same activation fragments (B = sc*q, and B = m
 // broadcast over each group), scaled by d and dmin in fp32 afterwards.
+// `valid` false (a padding super-block) contributes zero.
 template <int TB>
-__device__ __forceinline__ void skinny_superblock(const u32x4 hv, const u32x4 ca, const u32x4 cb, int sb,
-                                                  int q, const Q4kField flo, const Q4kField fhi,
-                                                  const half8 *const xb[TB], f32x4 acc[TB]) {
-    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hv.x & 0xFFFFu));
-    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hv.x >> 16));
+__device__ __forceinline__ void skinny_superblock(const u32x4 hv, const u32x4 ca, const u32x4 cb, bool valid,
+                                                  const Q4kField flo, const Q4kField fhi,
+                                                  const half8 (&a)[8][TB], f32x4 acc[TB]) {
+    const float d = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(hv.x & 0xFFFFu)) : 0.f;
+    const float dmin = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(hv.x >> 16)) : 0.f;
     const uint32_t sclo = q4k_sc(hv, flo), schi = q4k_sc(hv, fhi);
     const half2v sc_lo = splat2(sclo), sc_hi = splat2(schi);
     const half2v nsc_lo = splat2(sclo) * (_Float16)-1024.0f, nsc_hi = splat2(schi) * (_Float16)-1024.0f;
     const half2v m_lo = splat2(q4k_mn(hv, flo)), m_hi = splat2(q4k_mn(hv, fhi));
     const half8 bm_lo = half8{m_lo[0], m_lo[1], m_lo[0], m_lo[1], m_lo[0], m_lo[1], m_lo[0], m_lo[1]};
     const half8 bm_hi = half8{m_hi[0], m_hi[1], m_hi[0], m_hi[1], m_hi[0], m_hi[1], m_hi[0], m_hi[1]};
-    const int kf_sb = sb * 16 + 4 * q;  // fragment of group 2q, offset 0
-    half8 a[8][TB];
-#pragma unroll
-    for (int m = 0; m < 8; m++) {
-        // k = sb*256 + (2q + m/4)*32 + 8*(m%4) -> fragment kf_sb + 2*(m/4) + (m%4)/2,
-        // lane half (m % 2) of it
-        const int kf = kf_sb + (m >= 4 ? 2 : 0) + ((m & 3) >> 1);
-        const int lsel = (m & 1) * 32;
-#pragma unroll
-        for (int tb = 0; tb < TB; tb++) a[m][tb] = xb[tb][(size_t)kf * 64 + lsel];
-    }
     f32x4 aq[TB], am[TB];
 #pragma unroll
     for (int tb = 0; tb < TB; tb++) aq[tb] = am[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -335,17 +341,37 @@ __device__ __forceinline__ void skinny_superblock(const u32x4 hv, const u32x4 ca
 #pragma unroll
     for (int tb = 0; tb < TB; tb++)
 #pragma unroll
-        for (int v = 0; v < 4; v++) acc[tb][v] = __builtin_fmaf(d, aq[tb][v], __builtin_fmaf(-dmin, am[tb][v], acc[tb][v]));
+        for (int v = 0; v < 4; v++)
+            acc[tb][v] = __builtin_fmaf(d, aq[tb][v], __builtin_fmaf(-dmin, am[tb][v], acc[tb][v]));
 }
 
-template <int TB, int NW, int SBB>
-__global__ __launch_bounds__(NW * 64) void k_skinny(const uint8_t *__restrict__ W, int64_t row_bytes,
-                                                    int N, int K, const half8 *__restrict__ X16,
-                                                    const float *__restrict__ xs_inv,
-                                                    const float *__restrict__ bias,
-                                                    float *__restrict__ Y, int M) {
-    __shared__ f32x4 red[NW][TB][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// ---------------------------------------------------------------------------
+// Small-M kernel.  Workgroup = NW wavefronts (blockDim.x / 64, at most 8) over
+// 16 consecutive weight rows o0..o0+15; wavefront w owns the C contiguous
+// super-blocks [w*C, w*C + C) of those rows (NW*C >= K/256; super-blocks past
+// the end are padding that re-reads the last one and contributes zero).
+// C is a compile-time constant so the code is straight-line: a ring of
+// min(C, 3) super-blocks of weights is in flight (loads pinned ahead of the
+// compute with sched_barrier) and, for one token block, the activation
+// fragments of the next super-block are loaded while the current one computes.
+// MFMA 16x16x32: B lane l = (row j = l%16, chunk q = l/16) holds the 32 bytes of
+// chunk q (groups 2q and 2q+1) plus the 16-byte header: each super-block of a
+// row is read once, 144 B by 4 lanes.  MFMA m (0..7) takes from lane (j, q) the
+// 8 weights of group 2q + m/4 at offsets 8*(m%4)..+7; the A lane (token i, q)
+// holds the activations of the same k (one 16-byte piece of an X16
+// fragment).  Partial sums of the NW waves are added in wave order through LDS
+// (deterministic).
+// ---------------------------------------------------------------------------
+template <int TB, int C>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_skinny(
+    const uint8_t *__restrict__ W, int64_t row_bytes, int N, int K, const half8 *__restrict__ X16,
+    const float *__restrict__ xs_inv, const float *__restrict__ bias, float *__restrict__ Y, int M) {
+    extern __shared__ f32x4 red[];  // [NW][TB][64]
+    constexpr int RING = C < 3 ? C : 3;
+    constexpr int AB = TB == 1 ? 2 : 1;  // activation buffers
+    const int NW = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane & 15, q = lane >> 4;
     const int o0 = blockIdx.x * 16;
     int orow = o0 + j;
@@ -353,6 +379,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny(const uint8_t *__restrict__ 
     const uint8_t *wrow = W + (size_t)orow * row_bytes;
     const int nsb = K / 256;
     const int kf_n = K / 16;
+    const int sb0 = wave * C;
 
     f32x4 acc[TB];
     const half8 *xb[TB];
@@ -367,47 +394,51 @@ __global__ __launch_bounds__(NW * 64) void k_skinny(const uint8_t *__restrict__ 
     }
     const Q4kField flo = q4k_field(2 * q), fhi = q4k_field(2 * q + 1);
 
-    // Rotating SBB-deep pipeline over this wavefront's super-blocks
-    // sb_i = wave + i*NW: slot s holds sb_i for i = s (mod SBB); after slot s is
-    // consumed it is refilled with sb_{i+SBB}, so SBB-1 super-blocks stay in
-    // flight while one is computed.
-    const int cnt = nsb > wave ? (nsb - wave + NW - 1) / NW : 0;
-    u32x4 hv[SBB], ca[SBB], cb[SBB];
+    u32x4 hv[RING], ca[RING], cb[RING];
 #pragma unroll
-    for (int s = 0; s < SBB; s++) {
-        if (s < cnt) {
-            const uint8_t *blk = wrow + (size_t)(wave + s * NW) * 144;
+    for (int s = 0; s < RING; s++) {
+        int sb = sb0 + s;
+        sb = sb < nsb ? sb : nsb - 1;
+        const uint8_t *blk = wrow + (size_t)sb * 144;
+        hv[s] = ld16(blk);
+        ca[s] = ld16(blk + 16 + 32 * q);
+        cb[s] = ld16(blk + 32 + 32 * q);
+    }
+    half8 a[AB][8][TB];
+    skinny_load_a<TB>(xb, sb0 < nsb ? sb0 : nsb - 1, q, a[0]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < C; i++) {
+        const int s = i % RING;
+        const int sb = sb0 + i;
+        const int ab = AB == 2 ? (i & 1) : 0;
+        if (AB == 2 && i + 1 < C) {
+            const int sbn = sb + 1 < nsb ? sb + 1 : nsb - 1;
+            skinny_load_a<TB>(xb, sbn, q, a[(i + 1) & 1]);
+        } else if (AB == 1 && i > 0) {
+            skinny_load_a<TB>(xb, sb < nsb ? sb : nsb - 1, q, a[0]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        skinny_superblock<TB>(hv[s], ca[s], cb[s], sb < nsb, flo, fhi, a[ab], acc);
+        if (i + RING < C) {
+            int sbr = sb + RING;
+            sbr = sbr < nsb ? sbr : nsb - 1;
+            const uint8_t *blk = wrow + (size_t)sbr * 144;
             hv[s] = ld16(blk);
             ca[s] = ld16(blk + 16 + 32 * q);
             cb[s] = ld16(blk + 32 + 32 * q);
         }
-    }
-    for (int i0 = 0; i0 < cnt; i0 += SBB) {
-#pragma unroll
-        for (int s = 0; s < SBB; s++) {
-            const int i = i0 + s;
-            if (i < cnt) {
-                const u32x4 h = hv[s], a = ca[s], b = cb[s];
-                if (i + SBB < cnt) {
-                    const uint8_t *blk = wrow + (size_t)(wave + (i + SBB) * NW) * 144;
-                    hv[s] = ld16(blk);
-                    ca[s] = ld16(blk + 16 + 32 * q);
-                    cb[s] = ld16(blk + 32 + 32 * q);
-                }
-                skinny_superblock<TB>(h, a, b, wave + i * NW, q, flo, fhi, xb, acc);
-            }
-        }
+        __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int tb = 0; tb < TB; tb++) red[wave][tb][lane] = acc[tb];
+    for (int tb = 0; tb < TB; tb++) red[(wave * TB + tb) * 64 + lane] = acc[tb];
     __syncthreads();
     // output D of 16x16: lane l holds column (weight row) l%16, rows (tokens)
-    // 4*(l/16) + v
-    if (threadIdx.x < TB * 64) {
-        const int tb = threadIdx.x >> 6, l = threadIdx.x & 63;
-        f32x4 s = red[0][tb][l];
-#pragma unroll
-        for (int w = 1; w < NW; w++) s += red[w][tb][l];
+    // 4*(l/16) + v; the workgroup may have fewer threads than TB*64
+    for (int idx = threadIdx.x; idx < TB * 64; idx += blockDim.x) {
+        const int tb = idx >> 6, l = idx & 63;
+        f32x4 s = red[tb * 64 + l];
+        for (int w = 1; w < NW; w++) s += red[(w * TB + tb) * 64 + l];
         const int o = o0 + (l & 15);
         if (o < N) {
             const float bo = bias ? bias[o] : 0.f;
@@ -575,11 +606,30 @@ extern "C" int fh3k_max_in(void) { return 32768; }
 // NW = 8 wavefronts split K when there are few 16-row blocks (so that the
 // chip holds enough bytes in flight), 4 otherwise; SBB = super-blocks per
 // wavefront batch.
-template <int TB, int NW>
-static hipError_t launch_skinny_nw(const void *W, int64_t rb, int N, int K, const void *x16,
-                                   const float *xs_inv, const float *bias, float *y, int M, hipStream_t st) {
+// Super-blocks per wavefront C (compile-time) and wavefronts per workgroup NW
+// (<= 8, runtime) for K/256 = nsb super-blocks: the fewest padding
+// super-blocks NW*C - nsb, then C closest to 5 (the best measured balance of
+// per-wave work and parallelism at K = 5120).
+static const int kSkinnyC[] = {2, 3, 4, 5, 6, 7, 8, 10, 13, 16};
+
+static void skinny_split(int nsb, int &C, int &NW) {
+    int best = -1, bw = 1 << 30, bd = 1 << 30;
+    for (int i = 0; i < (int)(sizeof kSkinnyC / sizeof kSkinnyC[0]); i++) {
+        const int c = kSkinnyC[i], nw = (nsb + c - 1) / c;
+        if (nw > 8) continue;
+        const int waste = nw * c - nsb, dist = c > 5 ? c - 5 : 5 - c;
+        if (waste < bw || (waste == bw && dist < bd)) best = i, bw = waste, bd = dist;
+    }
+    C = best >= 0 ? kSkinnyC[best] : 0;
+    NW = C ? (nsb + C - 1) / C : 0;
+}
+
+template <int TB, int C>
+static hipError_t launch_skinny_c(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,
+                                  const float *bias, float *y, int M, int NW, hipStream_t st) {
     const unsigned blocks = (unsigned)((N + 15) / 16);
-    hipLaunchKernelGGL((k_skinny<TB, NW, 3>), dim3(blocks), dim3(NW * 64), 0, st, (const uint8_t *)W, rb, N, K,
+    const size_t lds = (size_t)NW * TB * 64 * sizeof(f32x4);
+    hipLaunchKernelGGL((k_skinny<TB, C>), dim3(blocks), dim3(NW * 64), lds, st, (const uint8_t *)W, rb, N, K,
                        (const half8 *)x16, xs_inv, bias, y, M);
     return hipGetLastError();
 }
@@ -587,8 +637,21 @@ static hipError_t launch_skinny_nw(const void *W, int64_t rb, int N, int K, cons
 template <int TB>
 static hipError_t launch_skinny(const void *W, int64_t rb, int N, int K, const void *x16,
                                 const float *xs_inv, const float *bias, float *y, int M, hipStream_t st) {
-    if ((N + 15) / 16 < 768) return launch_skinny_nw<TB, 8>(W, rb, N, K, x16, xs_inv, bias, y, M, st);
-    return launch_skinny_nw<TB, 4>(W, rb, N, K, x16, xs_inv, bias, y, M, st);
+    int C, NW;
+    skinny_split(K / 256, C, NW);
+    switch (C) {
+        case 2: return launch_skinny_c<TB, 2>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 3: return launch_skinny_c<TB, 3>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 4: return launch_skinny_c<TB, 4>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 5: return launch_skinny_c<TB, 5>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 6: return launch_skinny_c<TB, 6>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 7: return launch_skinny_c<TB, 7>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 8: return launch_skinny_c<TB, 8>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 10: return launch_skinny_c<TB, 10>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 13: return launch_skinny_c<TB, 13>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 16: return launch_skinny_c<TB, 16>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 extern "C" hipError_t fh3k_skinny(const void *W, int64_t row_bytes, int N, int K, const void *x16,

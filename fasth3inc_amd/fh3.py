@@ -49,6 +49,67 @@ class Fh3W(ctypes.Structure):
                 ("out", ctypes.c_int64), ("data", ctypes.c_void_p)]
 
 
+# FH3P pack and trunk structures (include/fh3/fh3_trunk.h)
+LAYER_TENSORS = ("qkv", "gate_compress", "out", "fc1", "fc2", "norm1", "norm2", "q_norm", "k_norm")
+FH3_PACK_MAGIC = 0x50334846
+FH3_PACK_VERSION = 1
+FH3_PACK_ALIGNMENT = 4096
+FH3_PACK_MAX_TENSORS_PER_LAYER = 16
+
+
+class Fh3LayerView(ctypes.Structure):
+    _fields_ = [(n, Fh3W) for n in LAYER_TENSORS]
+
+
+class Fh3PackTensorDesc(ctypes.Structure):
+    _pack_ = 1
+    _fields_ = [("name", ctypes.c_char * 64), ("type", ctypes.c_uint32), ("n_dims", ctypes.c_uint32),
+                ("shape", ctypes.c_int64 * 4), ("offset_in_layer", ctypes.c_uint64),
+                ("size_bytes", ctypes.c_uint64), ("in_dim", ctypes.c_int64), ("out_dim", ctypes.c_int64),
+                ("reserved", ctypes.c_uint8 * 32)]
+
+
+class Fh3PackLayerDesc(ctypes.Structure):
+    _pack_ = 1
+    _fields_ = [("file_offset", ctypes.c_uint64), ("size_bytes", ctypes.c_uint64),
+                ("n_tensors", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+                ("tensors", Fh3PackTensorDesc * FH3_PACK_MAX_TENSORS_PER_LAYER)]
+
+
+class Fh3PackHeader(ctypes.Structure):
+    _pack_ = 1
+    _fields_ = [("magic", ctypes.c_uint32), ("version", ctypes.c_uint32), ("num_layers", ctypes.c_uint32),
+                ("layer_alignment", ctypes.c_uint32), ("index_offset", ctypes.c_uint64),
+                ("index_bytes", ctypes.c_uint64), ("data_offset", ctypes.c_uint64),
+                ("total_bytes", ctypes.c_uint64), ("reserved", ctypes.c_uint8 * 80)]
+
+
+class Fh3Pack(ctypes.Structure):
+    _fields_ = [("fd", ctypes.c_int), ("file_size", ctypes.c_uint64), ("header", Fh3PackHeader),
+                ("num_layers", ctypes.c_int), ("layers", ctypes.POINTER(Fh3PackLayerDesc)),
+                ("mapped_base", ctypes.c_void_p), ("mapped_size", ctypes.c_size_t)]
+
+
+class Fh3TrunkStats(ctypes.Structure):
+    _fields_ = [("hits", ctypes.c_uint64), ("misses", ctypes.c_uint64), ("bytes_read", ctypes.c_uint64),
+                ("read_s", ctypes.c_double), ("wait_s", ctypes.c_double)]
+
+
+class Fh3TrunkDevStats(ctypes.Structure):
+    _fields_ = [("hits", ctypes.c_uint64), ("misses", ctypes.c_uint64), ("uploads", ctypes.c_uint64),
+                ("bytes_uploaded", ctypes.c_uint64), ("resident_bytes", ctypes.c_uint64)]
+
+
+class Fh3TrunkInfo(ctypes.Structure):
+    _fields_ = [("num_layers", ctypes.c_int), ("npin", ctypes.c_int), ("slot_size", ctypes.c_uint64),
+                ("dpin", ctypes.c_int), ("dev_slot_size", ctypes.c_uint64)]
+
+
+class Fh3Plan(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in ("budget_bytes", "min_bytes", "pinned_bytes", "ring_bytes",
+                                               "activation_bytes", "table_bytes", "total_bytes")]
+
+
 _c_void_p = ctypes.c_void_p
 _c_i64 = ctypes.c_int64
 _c_size = ctypes.c_size_t
@@ -100,6 +161,26 @@ SIGNATURES = {
     "fh3_synth_x_normal": (None, [_c_u64, _c_u64, _c_void_p, _c_size]),
     "fh3_synth_x_outliers": (None, [_c_u64, _c_u64, _c_void_p, _c_size, _c_float]),
     "fh3_synth_x_silu_gated": (None, [_c_u64, _c_u64, _c_void_p, _c_size]),
+    # fh3_trunk.h (struct pointers are passed as addresses)
+    "fh3_pack_open": (_c_int, [ctypes.c_char_p, ctypes.POINTER(Fh3Pack)]),
+    "fh3_pack_close": (None, [ctypes.POINTER(Fh3Pack)]),
+    "fh3_pack_layer": (Fh3LayerView, [ctypes.POINTER(Fh3Pack), _c_int, _c_void_p]),
+    "fh3_trunk_open": (_c_int, [ctypes.c_char_p, _c_u64, _c_void_p]),
+    "fh3_trunk_close": (None, [_c_void_p]),
+    "fh3_trunk_prefetch": (None, [_c_void_p, _c_int]),
+    "fh3_trunk_acquire": (_c_void_p, [_c_void_p, _c_int]),
+    "fh3_trunk_stats": (Fh3TrunkStats, [_c_void_p]),
+    "fh3_trunk_layer": (Fh3LayerView, [_c_void_p, _c_int, _c_void_p]),
+    "fh3_trunk_pack": (ctypes.POINTER(Fh3Pack), [_c_void_p]),
+    "fh3_trunk_attach_device": (_c_int, [_c_void_p, _c_u64, _c_void_p]),
+    "fh3_trunk_prefetch_dev": (None, [_c_void_p, _c_int]),
+    "fh3_trunk_acquire_dev": (_c_void_p, [_c_void_p, _c_int]),
+    "fh3_trunk_dev_stats": (Fh3TrunkDevStats, [_c_void_p]),
+    "fh3_trunk_struct_bytes": (_c_size, []),
+    "fh3_trunk_info": (_c_int, [_c_void_p, ctypes.POINTER(Fh3TrunkInfo)]),
+    "fh3_plan_bytes": (_c_u64, [ctypes.POINTER(Fh3Plan)]),
+    "fh3_plan_check": (_c_int, [ctypes.POINTER(Fh3Plan)]),
+    "fh3_mem_available": (_c_u64, []),
 }
 
 _lib = None
@@ -348,3 +429,142 @@ def synth_x(kind, seed, stream, rows, n, frac=0.01):
     else:
         raise ValueError(kind)
     return x
+
+
+# ---------------------------------------------------------------------------
+# FH3P pack and trunk streamer (include/fh3/fh3_trunk.h)
+# ---------------------------------------------------------------------------
+def _open_error(what, rc, path):
+    return Fh3Error(rc, "%s(%s) failed" % (what, path))
+
+
+class Pack:
+    """An open FH3P pack (fh3_pack_open / fh3_pack_close / fh3_pack_layer)."""
+
+    def __init__(self, path):
+        self._p = Fh3Pack()
+        rc = lib().fh3_pack_open(os.fsencode(path), ctypes.byref(self._p))
+        if rc != FH3_OK:
+            raise _open_error("fh3_pack_open", rc, path)
+        self._open = True
+
+    @property
+    def num_layers(self):
+        return self._p.num_layers
+
+    @property
+    def header(self):
+        return self._p.header
+
+    def layer_desc(self, L):
+        if not 0 <= L < self.num_layers:
+            raise IndexError(L)
+        return self._p.layers[L]
+
+    def layer(self, L, base=None):
+        """Fh3LayerView of layer L at base (an address), or into the mapping."""
+        return lib().fh3_pack_layer(ctypes.byref(self._p), L, base)
+
+    def close(self):
+        if self._open:
+            lib().fh3_pack_close(ctypes.byref(self._p))
+            self._open = False
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Trunk:
+    """The layer streamer (fh3_trunk_open ... fh3_trunk_close), and its device
+    extension (attach_device / prefetch_dev / acquire_dev).  acquire* return the
+    layer run's address as an int (host or device), or None on a failed read."""
+
+    def __init__(self, path, budget_bytes):
+        self._buf = ctypes.create_string_buffer(lib().fh3_trunk_struct_bytes())
+        self._t = ctypes.addressof(self._buf)
+        rc = lib().fh3_trunk_open(os.fsencode(path), budget_bytes, self._t)
+        if rc != FH3_OK:
+            raise _open_error("fh3_trunk_open", rc, path)
+        self._open = True
+
+    def info(self):
+        inf = Fh3TrunkInfo()
+        _check(lib().fh3_trunk_info(self._t, ctypes.byref(inf)), "fh3_trunk_info")
+        return inf
+
+    def stats(self):
+        return lib().fh3_trunk_stats(self._t)
+
+    def dev_stats(self):
+        return lib().fh3_trunk_dev_stats(self._t)
+
+    def prefetch(self, L):
+        lib().fh3_trunk_prefetch(self._t, L)
+
+    def acquire(self, L):
+        return lib().fh3_trunk_acquire(self._t, L)
+
+    def layer(self, L, base=None):
+        return lib().fh3_trunk_layer(self._t, L, base)
+
+    def layer_desc(self, L):
+        return lib().fh3_trunk_pack(self._t).contents.layers[L]
+
+    def attach_device(self, dev_budget_bytes, stream_ptr=None):
+        _check(lib().fh3_trunk_attach_device(self._t, dev_budget_bytes, stream_ptr), "fh3_trunk_attach_device")
+
+    def prefetch_dev(self, L):
+        lib().fh3_trunk_prefetch_dev(self._t, L)
+
+    def acquire_dev(self, L):
+        return lib().fh3_trunk_acquire_dev(self._t, L)
+
+    def close(self):
+        if self._open:
+            lib().fh3_trunk_close(self._t)
+            self._open = False
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def host_bytes(addr, n):
+    """numpy uint8 view of n host bytes at addr (no copy)."""
+    return np.ctypeslib.as_array((ctypes.c_uint8 * n).from_address(addr))
+
+
+def plan(**fields):
+    p = Fh3Plan()
+    for k, v in fields.items():
+        setattr(p, k, v)
+    return p
+
+
+def plan_bytes(p):
+    return lib().fh3_plan_bytes(ctypes.byref(p))
+
+
+def plan_check(p):
+    return lib().fh3_plan_check(ctypes.byref(p))
+
+
+def mem_available():
+    return lib().fh3_mem_available()

@@ -140,6 +140,72 @@ def rel_fro(y, yref):
     return float(np.linalg.norm(y - yref) / np.linalg.norm(yref))
 
 
+REF_IO_SO = os.path.join(ROOT, "oracle", "_ref", "libfh3_ref_io.so")
+REF_TRUNK_BYTES = 1 << 16  # generous room for the reference's struct Fh3Trunk
+
+
+class TrunkStats(ctypes.Structure):
+    """Layout of Fh3TrunkStats (reference include/fh3/fh3.h:134-140)."""
+    _fields_ = [("hits", ctypes.c_uint64), ("misses", ctypes.c_uint64), ("bytes_read", ctypes.c_uint64),
+                ("read_s", ctypes.c_double), ("wait_s", ctypes.c_double)]
+
+
+def load_ref_io():
+    """The reference's own fh3_pack.c/fh3_trunk.c built by oracle/Makefile, or None."""
+    if not os.path.exists(REF_IO_SO):
+        return None
+    lib = ctypes.CDLL(REF_IO_SO)
+    lib.fh3_trunk_open.restype = ctypes.c_int
+    lib.fh3_trunk_open.argtypes = [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_void_p]
+    lib.fh3_trunk_close.restype = None
+    lib.fh3_trunk_close.argtypes = [ctypes.c_void_p]
+    lib.fh3_trunk_prefetch.restype = None
+    lib.fh3_trunk_prefetch.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    lib.fh3_trunk_acquire.restype = ctypes.c_void_p
+    lib.fh3_trunk_acquire.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    lib.fh3_trunk_stats.restype = TrunkStats
+    lib.fh3_trunk_stats.argtypes = [ctypes.c_void_p]
+    return lib
+
+
+def write_pattern_pack(path, sizes, pattern_base=0xA0, truncate_last=0):
+    """A synthetic FH3P pack whose layer L is sizes[L] bytes of (pattern_base + L),
+    laid out as the reference's trunk test writes it (tests/unit/test_trunk.c:45-131:
+    index at 4096, descriptors of the full in-memory size, nine F32 tensor
+    descriptors per layer).  truncate_last cuts that many bytes off the file end."""
+    from fasth3inc_amd import fh3 as F
+    n = len(sizes)
+    hdr = F.Fh3PackHeader()
+    hdr.magic, hdr.version, hdr.num_layers, hdr.layer_alignment = F.FH3_PACK_MAGIC, F.FH3_PACK_VERSION, n, 4096
+    hdr.index_offset = 4096
+    hdr.index_bytes = n * ctypes.sizeof(F.Fh3PackLayerDesc)
+    data_off = (hdr.index_offset + hdr.index_bytes + 4095) // 4096 * 4096
+    hdr.data_offset = data_off
+    hdr.total_bytes = data_off + sum(sizes)
+    descs = (F.Fh3PackLayerDesc * n)()
+    at = data_off
+    for L, sz in enumerate(sizes):
+        descs[L].file_offset, descs[L].size_bytes, descs[L].n_tensors = at, sz, 9
+        for t in range(9):
+            td = descs[L].tensors[t]
+            td.name = b"tensor_%d_%d" % (L, t)
+            td.type, td.n_dims = F32, 2
+            td.shape[0] = td.shape[1] = 64
+            td.offset_in_layer, td.size_bytes = t * 4096, 4096
+            td.in_dim = td.out_dim = 64
+        at += sz
+    with open(path, "wb") as f:
+        f.write(bytes(hdr))
+        f.write(b"\0" * (hdr.index_offset - ctypes.sizeof(hdr)))
+        f.write(bytes(descs))
+        f.write(b"\0" * (data_off - hdr.index_offset - hdr.index_bytes))
+        for L, sz in enumerate(sizes):
+            f.write(bytes([(pattern_base + L) & 0xFF]) * sz)
+        if truncate_last:
+            f.truncate(hdr.total_bytes - truncate_last)
+    return path
+
+
 def random_q4k(rng, n_rows, K, d_range=(0.1, 0.45), dmin_range=(0.02, 0.06)):
     """Random Q4_K bytes with normal positive fp16 d/dmin (the reference fixtures'
     recipe, tools/emit_quant_fixtures.py:113-119) -- every 6-bit scale/min and

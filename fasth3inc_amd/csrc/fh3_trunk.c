@@ -39,25 +39,30 @@ static size_t page_up(uint64_t n) { return (size_t)((n + PAGE - 1) & ~(uint64_t)
 static size_t run_bytes(const Fh3Trunk *t, int L) { return (size_t)t->pack.layers[L].size_bytes; }
 
 /* Read n bytes of the file at off (clamped to the file end) into dst.  The
- * O_DIRECT descriptor is used when dst, off and n are page aligned; anything
- * else, or a filesystem that rejects O_DIRECT, goes through the buffered
- * descriptor.  Returns the bytes read or FH3_E_IO. */
-static int64_t read_run(Fh3Trunk *t, void *dst, size_t n, uint64_t off) {
+ * O_DIRECT descriptor is used when dst, off and n are page aligned and dst is
+ * ordinary memory; anything else goes through the buffered descriptor, and so
+ * does every later read once a direct read fails (a filesystem without
+ * O_DIRECT, or a destination the kernel cannot pin for DMA: page-locked
+ * memory mapped by the GPU driver gives EFAULT).  Returns the bytes read, or
+ * FH3_E_IO with *err set to errno. */
+static int64_t read_run(Fh3Trunk *t, void *dst, size_t n, uint64_t off, int *err) {
     const uint64_t size = t->pack.file_size;
     if (off >= size) return 0;
     if (n > size - off) n = (size_t)(size - off);
     int fd = t->pack.fd;
-    if (t->direct && (uintptr_t)dst % PAGE == 0 && off % PAGE == 0 && n % PAGE == 0) fd = t->direct_fd;
+    if (t->direct && !t->host_pinned && (uintptr_t)dst % PAGE == 0 && off % PAGE == 0 && n % PAGE == 0)
+        fd = t->direct_fd;
     size_t got = 0;
     while (got < n) {
         ssize_t r = pread(fd, (uint8_t *)dst + got, n - got, (off_t)(off + got));
         if (r < 0) {
             if (errno == EINTR) continue;
-            if (fd == t->direct_fd && (errno == EINVAL || errno == EOPNOTSUPP)) {
+            if (fd == t->direct_fd) {
                 t->direct = false;
                 fd = t->pack.fd;
                 continue;
             }
+            if (err) *err = errno;
             return FH3_E_IO;
         }
         if (r == 0) break;
@@ -110,16 +115,20 @@ static void *worker_main(void *arg) {
         pthread_mutex_unlock(&t->mutex);
 
         int64_t got = FH3_ERR;
+        int err = 0;
         double io = 0.0;
         /* an upload enqueued earlier may still be reading host slot s */
         if (!host_read || fh3_hip_event_sync(host_read) == FH3_OK) {
             const double t0 = now_s();
-            got = read_run(t, t->ring_buf[s], run_bytes(t, L), t->pack.layers[L].file_offset);
+            got = read_run(t, t->ring_buf[s], run_bytes(t, L), t->pack.layers[L].file_offset, &err);
             io = now_s() - t0;
+        } else {
+            err = -1; /* the wait for the previous upload failed */
         }
 
         pthread_mutex_lock(&t->mutex);
         t->worker_read_bytes = got;
+        t->worker_errno = err;
         t->prefetch_io_time = io;
         t->worker_has_work = false;
         t->worker_done = true;
@@ -191,7 +200,7 @@ int fh3_trunk_open(const char *path, uint64_t budget_bytes, Fh3Trunk *t) {
         for (int L = 0; L < t->npin; L++) {
             const size_t n = run_bytes(t, L);
             if (!(t->pinned_layers[L] = (uint8_t *)alloc_page_aligned(page_up(n)))) return open_fail(t, FH3_E_NOMEM);
-            if (read_run(t, t->pinned_layers[L], n, t->pack.layers[L].file_offset) != (int64_t)n)
+            if (read_run(t, t->pinned_layers[L], n, t->pack.layers[L].file_offset, NULL) != (int64_t)n)
                 return open_fail(t, FH3_E_IO);
         }
     }
@@ -384,7 +393,7 @@ static int fill_resident(Fh3Trunk *t) {
                 rc = FH3_E_NOMEM;
                 break;
             }
-            if (read_run(t, bounce, n, t->pack.layers[L].file_offset) != (int64_t)n) {
+            if (read_run(t, bounce, n, t->pack.layers[L].file_offset, NULL) != (int64_t)n) {
                 rc = fh3_hip_set_error(FH3_E_IO, "fh3_trunk_attach_device: short read of a resident layer");
                 break;
             }
@@ -473,7 +482,15 @@ const uint8_t *fh3_trunk_acquire_dev(Fh3Trunk *t, int L) {
     if (s < 0) {
         s = t->dev_active == 0 ? 1 : 0;
         const uint8_t *src = fh3_trunk_acquire(t, L); /* host prefix or a host ring slot */
-        if (!src) return NULL;
+        if (!src) {
+            char msg[160];
+            snprintf(msg, sizeof msg, "fh3_trunk_acquire_dev: layer %d: read %lld of %zu bytes (%s)", L,
+                     (long long)t->worker_read_bytes, run_bytes(t, L),
+                     t->worker_errno > 0 ? strerror(t->worker_errno)
+                                         : t->worker_errno < 0 ? "waiting for an upload failed" : "short file");
+            fh3_hip_set_error(FH3_E_IO, msg);
+            return NULL;
+        }
         if (upload(t, s, L, src, L < t->npin ? -1 : t->active_slot) != FH3_OK) return NULL;
     }
     if (fh3_hip_stream_wait(t->compute_stream, t->ev_uploaded[s]) != FH3_OK) return NULL;

@@ -161,7 +161,7 @@ typedef struct Fh3Trunk {
     int worker_req_layer;
     int worker_req_slot;
     int64_t worker_read_bytes;
-    int worker_upload_rc;         /* FH3_OK or the upload error of the last job */
+    int worker_errno;             /* errno of the last job's failed read, or 0 */
     Fh3TrunkStats stats;
     /* device extension (zero until fh3_trunk_attach_device) */
     bool device;

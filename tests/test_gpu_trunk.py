@@ -21,6 +21,12 @@ pytestmark = pytest.mark.gpu
 MB = 1 << 20
 
 
+def acquired(fh3, tr, L):
+    d = tr.acquire_dev(L)
+    assert d is not None, "layer %d: %s" % (L, fh3.lib().fh3_hip_last_error().decode())
+    return d
+
+
 def read_back(fh3, addr, n):
     out = np.empty(n, dtype=np.uint8)
     fh3._check(fh3.lib().fh3_hip_memcpy_dtoh(out.ctypes.data, addr, n), "fh3_hip_memcpy_dtoh")
@@ -37,8 +43,7 @@ def test_dev_stream_pattern_bytes(gpu, tmp_path):
         assert (inf.npin, inf.dpin, inf.dev_slot_size) == (6, 3, MB)
         for scan in range(3):
             for L in range(10):
-                d = tr.acquire_dev(L)
-                assert d is not None
+                d = acquired(fh3, tr, L)
                 if scan < 2:
                     tr.prefetch_dev((L + 1) % 10)
                 b = read_back(fh3, d, MB)
@@ -60,10 +65,10 @@ def test_dev_slot_pointer_identity(gpu, tmp_path):
     with fh3.Trunk(path, 8 * MB) as tr:
         tr.attach_device(2 * MB)
         assert tr.info().dpin == 0
-        a1 = tr.acquire_dev(7)
+        a1 = acquired(fh3, tr, 7)
         tr.prefetch_dev(8)
         assert tr.acquire_dev(7) == a1
-        b1 = tr.acquire_dev(8)
+        b1 = acquired(fh3, tr, 8)
         assert b1 != a1
         for L, want in [(7, a1), (8, b1), (7, a1), (8, b1)]:
             assert tr.acquire_dev(L) == want
@@ -80,8 +85,9 @@ def test_dev_short_read_returns_null(gpu, tmp_path):
     with fh3.Trunk(path, 4 * MB) as tr:
         tr.attach_device(2 * MB)
         assert tr.acquire_dev(9) is None
-        d = tr.acquire_dev(8)
-        assert d is not None and np.all(read_back(fh3, d, MB) == 0xA0 + 8)
+        assert "layer 9" in fh3.lib().fh3_hip_last_error().decode()
+        d = acquired(fh3, tr, 8)
+        assert np.all(read_back(fh3, d, MB) == 0xA0 + 8)
 
 
 # ---------------------------------------------------------------------------
@@ -169,9 +175,7 @@ def test_streamed_matmul_matches_resident(gpu, oracle, dit_pack, host_budget, de
         tr.attach_device(dev_budget)
 
         def streamed_view(L):
-            d = tr.acquire_dev(L)
-            assert d is not None, L
-            return tr.layer(L, d)
+            return tr.layer(L, acquired(fh3, tr, L))
 
         got = _run_layers(fh3, streamed_view, xs, outs,
                           prefetch=lambda L: tr.prefetch_dev(L) if L < N_LAYERS else None)

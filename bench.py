@@ -139,6 +139,75 @@ class Gemm:
             b.close()
 
 
+def dit_blocks_streamed(ev, st, n_blocks=8, M=16384, passes=2):
+    """Eight synthetic DiT blocks (QKV 15360x5120, out 5120x5120, fc1 = up|gate
+    27648x5120, fc2 = down 5120x13824; 178.4 MB of Q4_K each) written to an
+    FH3P pack, held in page-locked host memory by the trunk and streamed
+    through two device slots (hipMemcpyAsync on the upload stream), M = 16384
+    tokens.  Per block: acquire_dev(L), prefetch_dev(L+1), the four
+    fh3_hip_matmul_dev calls.  Timed beside the same blocks resident in HBM,
+    and beside the uploads alone."""
+    import tempfile
+    from fasth3inc_amd import pack as P
+    hidden, qkv, mlp = 5120, 15360, 13824
+    specs = P.dit_block_specs(hidden=hidden, qkv_out=qkv, mlp_hidden=mlp)
+    q4 = [s for s in specs if s.qtype == F.FH3_QUANT_Q4_K]
+    block_wbytes = sum(s.nbytes for s in q4)
+    block_flop = sum(2.0 * M * s.ne1 * s.ne0 for s in q4)
+    path = os.path.join(tempfile.gettempdir(), "fh3_bench_dit_%d.fh3p" % os.getpid())
+    t0 = time.perf_counter()
+    P.write_pack(path, n_blocks, specs, lambda L: P.synth_dit_block(specs, 5, L))
+    log("[bench] DiT pack: %d blocks x %.1f MB written in %.1fs" % (n_blocks, block_wbytes / 1e6,
+                                                                     time.perf_counter() - t0))
+    try:
+        xa = F.DeviceBuffer.from_array(F.synth_x("outliers", 5, 1, M, hidden))
+        xm = F.DeviceBuffer.from_array(F.synth_x("silu_gated", 5, 2, M, mlp))
+        ys = [F.DeviceBuffer(M * n * 4) for n in (qkv, hidden, 2 * mlp, hidden)]
+        res = {"blocks": n_blocks, "M": M, "block_weight_bytes": block_wbytes, "block_flop": block_flop,
+               "shapes": "qkv 5120->15360, out 5120->5120, fc1 (up|gate) 5120->27648, fc2 (down) 13824->5120"}
+
+        def run_pass(tr, compute=True):
+            for L in range(n_blocks):
+                d = tr.acquire_dev(L)
+                if d is None:
+                    raise F.Fh3Error(F.FH3_E_IO, F.lib().fh3_hip_last_error().decode())
+                tr.prefetch_dev((L + 1) % n_blocks)
+                if not compute:
+                    continue
+                v = tr.layer(L, d)
+                for w, x, y in ((v.qkv, xa, ys[0]), (v.out, xa, ys[1]), (v.fc1, xa, ys[2]), (v.fc2, xm, ys[3])):
+                    F.matmul_dev(w.data, w.in_, w.out, x, y, M)
+
+        for label, dev_budget, compute in (("streamed", 0, True), ("resident", 1 << 40, True),
+                                           ("uploads_only", 0, False)):
+            with F.Trunk(path, 1 << 40) as tr:
+                tr.attach_device(dev_budget)
+                run_pass(tr, compute)
+                F.synchronize()
+                u0 = tr.dev_stats().uploads
+                w0 = time.perf_counter()
+                ms = ev.time_ms(lambda i: run_pass(tr, compute), passes, st)
+                F.synchronize()
+                wall = (time.perf_counter() - w0) / passes
+                ups = tr.dev_stats().uploads - u0
+            per_block = ms / n_blocks
+            entry = {"ms_per_block": round(per_block, 3), "wall_ms_per_block": round(wall * 1e3 / n_blocks, 3),
+                     "uploads_per_pass": ups // passes}
+            if compute:
+                entry["TFLOPs"] = round(block_flop / (per_block * 1e-3) / 1e12, 1)
+            else:
+                entry["upload_GBps"] = round(block_wbytes / (per_block * 1e-3) / 1e9, 1)
+            res[label] = entry
+            log("[bench] DiT blocks %s: %.3f ms/block %s" % (label, per_block, entry))
+        res["unhidden_upload_ms_per_block"] = round(res["streamed"]["ms_per_block"] -
+                                                    res["resident"]["ms_per_block"], 3)
+        for b in [xa, xm] + ys:
+            b.close()
+        return res
+    finally:
+        os.unlink(path)
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline
 # ---------------------------------------------------------------------------
@@ -186,6 +255,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="skip the M=32768 MLP GEMMs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-stream", action="store_true", help="skip the streamed DiT blocks")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -319,6 +389,14 @@ def main():
     if mlp:
         extra["dit_mlp_linears_ms"] = round(sum(g["call_ms"] for g in mlp), 4)
     extra["gemv"] = per_gemv
+
+    # ---------------- DiT blocks streamed through the trunk ----------------
+    if not args.no_stream:
+        try:
+            extra["dit_blocks_streamed"] = dit_blocks_streamed(ev, st)
+        except Exception as e:  # keep the headline line when this leg fails
+            log("[bench] DiT streamed blocks failed: %r" % (e,))
+            extra["dit_blocks_streamed"] = {"error": repr(e)}
 
     out = {
         "metric": METRIC,

@@ -37,6 +37,15 @@ MFMA_F16_PEAK = 2.5e15   # flop/s, MI355X dense fp16/bf16 MFMA
 MALL_BYTES = 256 << 20   # Infinity Cache
 METRIC = "Q4_K GEMM TFLOP/s + GEMV weight GB/s (% roofline); DiT block linear ms"
 
+# HBM bytes per launch, measured with rocprofv3 --pmc FETCH_SIZE and --pmc
+# WRITE_SIZE (one run each) over `python3 -m fasth3inc_amd.profile_kernels all
+# --reps 5`, scaled by 2.0 and 1.0: a 256 MiB device-to-device copy reads
+# FETCH_SIZE = 128 MiB and WRITE_SIZE = 256 MiB.  Summaries:
+# profiles/k_skinny_gemv_m1-16_k5120.md, profiles/k_gemm_dit_attention_m8192_k5120.md,
+# profiles/hbm_counters_copy_256MiB.md.  Re-measure when the kernels change.
+TRAFFIC_SKINNY_MEAN = 33932940      # mean over the six GEMV shapes (algorithmic mean 32899072)
+TRAFFIC_GEMM = {"attn_qkv": 2200560763, "attn_out": 631555288}
+
 
 def q4k_bytes(N, K):
     return N * (K // 256) * 144
@@ -323,7 +332,8 @@ def main():
         log("[bench] GEMV M=%d N=%d kernel %.2f us call %.2f us" % (c.M, c.N, t_k * 1e3, t_c * 1e3))
     achieved = k_bytes / (k_time * 1e-3)
     roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK, 4), "traffic": TRAFFIC_SKINNY_MEAN,
+                "traffic_over_algorithmic": round(TRAFFIC_SKINNY_MEAN / (k_bytes / len(gemv)), 3),
                 "kernel": "k_skinny (fh3_hip_matmul_prepared_dev, n_tok<=64)",
                 "note": "algorithmic bytes N*K/256*144 + 4MK + 4MN per launch over the mean launch time "
                         "(graph of 64 back-to-back launches, rotating weight copies) of the six shapes"}
@@ -378,7 +388,8 @@ def main():
     shared_x.clear()
     ach = sum_flop / (sum_t * 1e-3)
     roofline_gemm = {"bound": "mfma", "achieved": round(ach / 1e12, 1), "peak": MFMA_F16_PEAK / 1e12,
-                     "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK, 4),
+                     "traffic": TRAFFIC_GEMM["attn_qkv"], "traffic_kernel": "k_gemm attn_qkv M=8192 N=15360",
                      "kernel": "k_gemm (fh3_hip_matmul_prepared_dev, n_tok>64)",
                      "note": "2*M*N*K per launch over launch time, summed over the DiT GEMMs; "
                              "fp16 operands, fp32 accumulation; peak is dense fp16 MFMA"}

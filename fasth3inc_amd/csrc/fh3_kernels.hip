@@ -226,17 +226,7 @@ __global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ X, int 
 }
 
 // ---------------------------------------------------------------------------
-// Small-M kernel.  Workgroup = NW wavefronts over 16 consecutive weight rows
-// o0..o0+15; wavefront w takes super-blocks sb = w, w+NW, ...  in batches of
-// SBB: all weight loads of a batch are issued before any of it is computed, so
-// a wavefront keeps up to SBB * 2304 bytes in flight.
-// MFMA 16x16x32: B lane l = (row j = l%16, chunk q = l/16) loads the 32 bytes of
-// chunk q (both of its groups 2q and 2q+1) plus the 16-byte header, i.e. each
-// super-block of a row is read once, 144 B by 4 lanes.  MFMA m (0..7) takes from
-// lane (j, q) the 8 weights of group 2q + m/4 at offsets 8*(m%4)..+7; the A
-// lane (token i, q) loads the activations of the same k, one 16-byte piece of
-// an X16 fragment (lanes of padding tokens load nothing).  Partial sums of the
-// NW waves are added in wave order through LDS (deterministic).
+// Small-M helpers
 // ---------------------------------------------------------------------------
 // Lane-constant field positions of the 6-bit scale/min of group g
 // (reference src/core/fh3_quant.c:168-177): low 4 bits come from byte g of the

@@ -1,0 +1,81 @@
+"""Launch the hot kernels at the benchmark shapes, for rocprofv3.
+
+    rocprofv3 --kernel-trace --stats -d OUT -- python3 -m fasth3inc_amd.profile_kernels gemv
+    rocprofv3 --pmc FETCH_SIZE -d OUT -- python3 -m fasth3inc_amd.profile_kernels gemv
+    rocprofv3 --pmc WRITE_SIZE -d OUT -- python3 -m fasth3inc_amd.profile_kernels copy
+
+Workloads (each launch sequence is preceded by one untimed warmup launch):
+  gemv   the six small-M shapes (M in {1,4,16}, K=5120, N in {5120,17408}):
+         fh3_hip_matmul_prepared_dev -> k_skinny, weights rotated over more
+         than 256 MB of device copies so they come from HBM
+  gemm   the DiT attention shapes (M=8192, K=5120, N in {15360,5120}):
+         fh3_hip_matmul_prepared_dev -> k_gemm, and the activation prep k_xprep
+  copy   hipMemcpy device-to-device of 256 MiB: a copy of known size that
+         calibrates FETCH_SIZE / WRITE_SIZE against the bytes moved
+"""
+import argparse
+import sys
+
+from . import fh3 as F
+
+MALL_BYTES = 256 << 20
+
+
+def gemv(reps):
+    for N in (5120, 17408):
+        for M in (1, 4, 16):
+            K = 5120
+            raw = F.synth_q4k_weights(0, 100 + N, N, K, 0.02, 0.0)
+            copies = max(2, -(-(MALL_BYTES + (64 << 20)) // raw.nbytes))
+            ws = [F.DeviceBuffer.from_array(raw) for _ in range(copies)]
+            dx = F.DeviceBuffer.from_array(F.synth_x("normal", 0, 200 + M, M, K))
+            dy = F.DeviceBuffer(M * N * 4)
+            prep = F.DeviceBuffer(F.prepared_bytes(M, K))
+            F.prepare_x_dev(dx, M, K, prep)
+            for i in range(reps + 1):
+                F.matmul_prepared_dev(ws[i % copies], K, N, prep, dy, M)
+            F.synchronize()
+            print("gemv M=%d N=%d K=%d: %d launches, %d weight copies" % (M, N, K, reps, copies), flush=True)
+            for b in ws + [dx, dy, prep]:
+                b.close()
+
+
+def gemm(reps):
+    M, K = 8192, 5120
+    dx = F.DeviceBuffer.from_array(F.synth_x("outliers", 1, 400 + K, M, K))
+    prep = F.DeviceBuffer(F.prepared_bytes(M, K))
+    for N in (15360, 5120):
+        dw = F.DeviceBuffer.from_array(F.synth_q4k_weights(1, 300 + N + K, N, K, 0.02, 0.0))
+        dy = F.DeviceBuffer(M * N * 4)
+        for _ in range(reps + 1):
+            F.prepare_x_dev(dx, M, K, prep)
+            F.matmul_prepared_dev(dw, K, N, prep, dy, M)
+        F.synchronize()
+        print("gemm M=%d N=%d K=%d: %d launches" % (M, N, K, reps), flush=True)
+        dw.close()
+        dy.close()
+
+
+def copy(reps):
+    n = 256 << 20
+    a, b = F.DeviceBuffer(n), F.DeviceBuffer(n)
+    a.fill(1)
+    for _ in range(reps + 1):
+        F._check(F.lib().fh3_hip_memcpy_dtod(b.ptr, a.ptr, n), "fh3_hip_memcpy_dtod")
+    F.synchronize()
+    print("copy %d bytes: %d launches" % (n, reps), flush=True)
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("workload", choices=("gemv", "gemm", "copy", "all"))
+    ap.add_argument("--reps", type=int, default=20)
+    args = ap.parse_args(argv)
+    F.init(0)
+    for name in (("gemv", "gemm", "copy") if args.workload == "all" else (args.workload,)):
+        globals()[name](args.reps)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -276,18 +276,18 @@ __device__ __forceinline__ half8 q4k_scq8_f16(uint32_t u0, uint32_t u1, bool hi,
     return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
-// Activation fragments of super-block sb for MFMA m = 0..7 of lane (token, q):
-// k = sb*256 + (2q + m/4)*32 + 8*(m%4) -> fragment sb*16 + 4q + 2*(m/4) + (m%4)/2,
-// lane half (m % 2) of it.
+// Activation fragments of super-block s0 + i for MFMA m = 0..7 of lane
+// (token, q): k = sb*256 + (2q + m/4)*32 + 8*(m%4) -> fragment
+// sb*16 + 4q + 2*(m/4) + (m%4)/2, lane half (m % 2) of it.  xq[tb] already
+// points at fragment s0*16 + 4q of the lane's token, so with i a compile-time
+// constant every offset below is one too.
 template <int TB>
-__device__ __forceinline__ void skinny_load_a(const half8 *const xb[TB], int sb, int q, half8 (&a)[8][TB]) {
-    const int kf_sb = sb * 16 + 4 * q;
+__device__ __forceinline__ void skinny_load_a(const half8 *const xq[TB], int i, half8 (&a)[8][TB]) {
 #pragma unroll
     for (int m = 0; m < 8; m++) {
-        const int kf = kf_sb + (m >= 4 ? 2 : 0) + ((m & 3) >> 1);
-        const int lsel = (m & 1) * 32;
+        const int off = (i * 16 + (m >= 4 ? 2 : 0) + ((m & 3) >> 1)) * 64 + (m & 1) * 32;
 #pragma unroll
-        for (int tb = 0; tb < TB; tb++) a[m][tb] = xb[tb][(size_t)kf * 64 + lsel];
+        for (int tb = 0; tb < TB; tb++) a[m][tb] = xq[tb][off];
     }
 }
 
@@ -338,12 +338,15 @@ __device__ __forceinline__ void skinny_superblock(const u32x4 hv, const u32x4 ca
 // ---------------------------------------------------------------------------
 // Small-M kernel.  Workgroup = NW wavefronts (blockDim.x / 64, at most 8) over
 // 16 consecutive weight rows o0..o0+15; wavefront w owns the C contiguous
-// super-blocks [w*C, w*C + C) of those rows (NW*C >= K/256; super-blocks past
-// the end are padding that re-reads the last one and contributes zero).
-// C is a compile-time constant so the code is straight-line: a ring of
-// min(C, 3) super-blocks of weights is in flight (loads pinned ahead of the
-// compute with sched_barrier) and, for one token block, the activation
-// fragments of the next super-block are loaded while the current one computes.
+// super-blocks [w*C, w*C + C) of those rows (NW*C >= K/256 >= C).  The last
+// wavefront's window is moved back to [K/256 - C, K/256) so that every load
+// stays inside the row; the super-blocks it shares with the previous
+// wavefront count as padding (zero).  C is a compile-time constant, so the
+// code is straight-line and every load has a compile-time offset from one
+// per-lane pointer: a ring of min(C, RMAX) super-blocks of weights is in
+// flight (loads pinned ahead of the compute with sched_barrier) and, for one
+// token block, the activation fragments of the next super-block are loaded
+// while the current one computes.
 // MFMA 16x16x32: B lane l = (row j = l%16, chunk q = l/16) holds the 32 bytes of
 // chunk q (groups 2q and 2q+1) plus the 16-byte header: each super-block of a
 // row is read once, 144 B by 4 lanes.  MFMA m (0..7) takes from lane (j, q) the
@@ -352,27 +355,28 @@ __device__ __forceinline__ void skinny_superblock(const u32x4 hv, const u32x4 ca
 // fragment).  Partial sums of the NW waves are added in wave order through LDS
 // (deterministic).
 // ---------------------------------------------------------------------------
-template <int TB, int C>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_skinny(
+template <int TB, int C, int MAXT = 512, int RMAX = (TB == 1 ? 5 : 3)>
+__global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_skinny(
     const uint8_t *__restrict__ W, int64_t row_bytes, int N, int K, const half8 *__restrict__ X16,
     const float *__restrict__ xs_inv, const float *__restrict__ bias, float *__restrict__ Y, int M) {
     extern __shared__ f32x4 red[];  // [NW][TB][64]
-    constexpr int RING = C < 3 ? C : 3;
+    constexpr int RING = C < RMAX ? C : RMAX;
     constexpr int AB = TB == 1 ? 2 : 1;  // activation buffers
     const int NW = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane & 15, q = lane >> 4;
     const int o0 = blockIdx.x * 16;
-    int orow = o0 + j;
-    orow = orow < N ? orow : N - 1;
-    const uint8_t *wrow = W + (size_t)orow * row_bytes;
+    const int orow = o0 + j < N ? o0 + j : N - 1;
     const int nsb = K / 256;
     const int kf_n = K / 16;
-    const int sb0 = wave * C;
+    const int own = wave * C;                          // first super-block this wave owns
+    const int s0 = own < nsb - C ? own : nsb - C;      // window start, inside the row
+    const uint8_t *wh = W + (size_t)orow * row_bytes + (size_t)s0 * 144;  // header of s0
+    const uint8_t *wc = wh + 16 + 32 * q;                                 // chunk q of s0
 
     f32x4 acc[TB];
-    const half8 *xb[TB];
+    const half8 *xq[TB];
 #pragma unroll
     for (int tb = 0; tb < TB; tb++) {
         acc[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -380,43 +384,35 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
         // row (their output rows are never stored)
         int t = tb * 16 + j;
         t = t < M ? t : M - 1;
-        xb[tb] = X16 + (size_t)(t >> 5) * kf_n * 64 + (t & 31);
+        xq[tb] = X16 + ((size_t)(t >> 5) * kf_n + (size_t)s0 * 16 + 4 * q) * 64 + (t & 31);
     }
     const Q4kField flo = q4k_field(2 * q), fhi = q4k_field(2 * q + 1);
 
     u32x4 hv[RING], ca[RING], cb[RING];
 #pragma unroll
     for (int s = 0; s < RING; s++) {
-        int sb = sb0 + s;
-        sb = sb < nsb ? sb : nsb - 1;
-        const uint8_t *blk = wrow + (size_t)sb * 144;
-        hv[s] = ld16(blk);
-        ca[s] = ld16(blk + 16 + 32 * q);
-        cb[s] = ld16(blk + 32 + 32 * q);
+        hv[s] = ld16(wh + s * 144);
+        ca[s] = ld16(wc + s * 144);
+        cb[s] = ld16(wc + s * 144 + 16);
     }
     half8 a[AB][8][TB];
-    skinny_load_a<TB>(xb, sb0 < nsb ? sb0 : nsb - 1, q, a[0]);
+    skinny_load_a<TB>(xq, 0, a[0]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < C; i++) {
         const int s = i % RING;
-        const int sb = sb0 + i;
         const int ab = AB == 2 ? (i & 1) : 0;
         if (AB == 2 && i + 1 < C) {
-            const int sbn = sb + 1 < nsb ? sb + 1 : nsb - 1;
-            skinny_load_a<TB>(xb, sbn, q, a[(i + 1) & 1]);
+            skinny_load_a<TB>(xq, i + 1, a[(i + 1) & 1]);
         } else if (AB == 1 && i > 0) {
-            skinny_load_a<TB>(xb, sb < nsb ? sb : nsb - 1, q, a[0]);
+            skinny_load_a<TB>(xq, i, a[0]);
         }
         __builtin_amdgcn_sched_barrier(0);
-        skinny_superblock<TB>(hv[s], ca[s], cb[s], sb < nsb, flo, fhi, a[ab], acc);
+        skinny_superblock<TB>(hv[s], ca[s], cb[s], s0 + i >= own, flo, fhi, a[ab], acc);
         if (i + RING < C) {
-            int sbr = sb + RING;
-            sbr = sbr < nsb ? sbr : nsb - 1;
-            const uint8_t *blk = wrow + (size_t)sbr * 144;
-            hv[s] = ld16(blk);
-            ca[s] = ld16(blk + 16 + 32 * q);
-            cb[s] = ld16(blk + 32 + 32 * q);
+            hv[s] = ld16(wh + (i + RING) * 144);
+            ca[s] = ld16(wc + (i + RING) * 144);
+            cb[s] = ld16(wc + (i + RING) * 144 + 16);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -593,20 +589,17 @@ extern "C" hipError_t fh3k_xprep(const float *x, int M, int K, int Mpad, void *x
 
 extern "C" int fh3k_max_in(void) { return 32768; }
 
-// NW = 8 wavefronts split K when there are few 16-row blocks (so that the
-// chip holds enough bytes in flight), 4 otherwise; SBB = super-blocks per
-// wavefront batch.
-// Super-blocks per wavefront C (compile-time) and wavefronts per workgroup NW
-// (<= 8, runtime) for K/256 = nsb super-blocks: the fewest padding
-// super-blocks NW*C - nsb, then C closest to 5 (the best measured balance of
-// per-wave work and parallelism at K = 5120).
-static const int kSkinnyC[] = {2, 3, 4, 5, 6, 7, 8, 10, 13, 16};
+// Super-blocks per wavefront C (compile-time, C <= nsb) and wavefronts per
+// workgroup NW (<= 8, runtime) for K/256 = nsb super-blocks: the fewest
+// padding super-blocks NW*C - nsb, then C closest to 5 (the best measured
+// balance of per-wave work and parallelism at K = 5120).
+static const int kSkinnyC[] = {1, 2, 3, 4, 5, 6, 7, 8, 10, 13, 16};
 
 static void skinny_split(int nsb, int &C, int &NW) {
     int best = -1, bw = 1 << 30, bd = 1 << 30;
     for (int i = 0; i < (int)(sizeof kSkinnyC / sizeof kSkinnyC[0]); i++) {
         const int c = kSkinnyC[i], nw = (nsb + c - 1) / c;
-        if (nw > 8) continue;
+        if (nw > 8 || c > nsb) continue;
         const int waste = nw * c - nsb, dist = c > 5 ? c - 5 : 5 - c;
         if (waste < bw || (waste == bw && dist < bd)) best = i, bw = waste, bd = dist;
     }
@@ -630,6 +623,7 @@ static hipError_t launch_skinny(const void *W, int64_t rb, int N, int K, const v
     int C, NW;
     skinny_split(K / 256, C, NW);
     switch (C) {
+        case 1: return launch_skinny_c<TB, 1>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
         case 2: return launch_skinny_c<TB, 2>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
         case 3: return launch_skinny_c<TB, 3>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
         case 4: return launch_skinny_c<TB, 4>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);

@@ -440,18 +440,69 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) vo
 // ---------------------------------------------------------------------------
 // Large-M kernel.  Output tile 256 tokens x 128 weight rows, 4 wavefronts, each
 // owning 64 tokens x all 128 rows (2 x 4 tiles of 32x32, 128 fp32 accumulators
-// per lane).  Per K step of 64 (one Q4_K chunk: groups 2c and 2c+1):
-//   - thread (r = tid%128, h = tid/128) loads 16 bytes of row r's chunk and
-//     writes 32 dequantised fp16 weights into the LDS B-fragments;
+// per lane).  Per K step s of 64 (one Q4_K chunk: groups 2c and 2c+1):
+//   - thread (r = tid%128, h = tid/128) holds 16 raw bytes of row r's chunk
+//     and writes 32 dequantised fp16 weights into the LDS B-fragments;
 //   - each wavefront loads its X16 fragments straight from global memory
-//     (1 KiB contiguous per load), one step ahead;
-//   - LDS is double buffered, one barrier per step.
+//     (1 KiB contiguous per load);
+//   - software pipelined: in the interval between two barriers the MFMAs of
+//     step s read lds[s&1] while step s+1 is dequantised into lds[(s+1)&1],
+//     so the dequant VALU work overlaps the matrix work; the loop is unrolled
+//     by two so that activation and raw-weight registers ping-pong.
 // Workgroup ids are remapped so that the 8 XCDs each run a contiguous run of
 // tiles in token-major order: concurrent tiles on one XCD share the same 256
 // activation rows in that XCD's L2.
 // ---------------------------------------------------------------------------
 constexpr int GEMM_BM = 256;
 constexpr int GEMM_BN = 128;
+
+// Raw Q4_K bytes one thread needs for K step s: the super-block header and 16
+// bytes of chunk s%4 (the header is reused within a super-block).
+struct GemmRaw {
+    u32x4 hv, qv;
+};
+
+__device__ __forceinline__ void gemm_load_raw(const uint8_t *wrow, int s, int h, GemmRaw &r, const GemmRaw &prev) {
+    const uint8_t *blk = wrow + (size_t)(s >> 2) * 144;
+    r.hv = (s & 3) == 0 ? ld16(blk) : prev.hv;
+    r.qv = ld16(blk + 16 + 32 * (s & 3) + 16 * h);
+}
+
+// B-fragment layout: fragment rb*4 + kk holds rows 32rb..32rb+31 x k 16kk..16kk+15
+// of the step; lane l holds row l%32 at k offset 8*(l/32).
+__device__ __forceinline__ void gemm_dequant(half8 (*ldsb)[64], const GemmRaw &r, int s, int wf, int wl, int h) {
+    const int c = s & 3;
+    float Dlo, Clo, Dhi, Chi;
+    q4k_group_fast(r.hv, 2 * c, Dlo, Clo);
+    q4k_group_fast(r.hv, 2 * c + 1, Dhi, Chi);
+    ldsb[wf + h][wl] = q4k_deq8_f16(r.qv.x, r.qv.y, false, Dlo, Clo);
+    ldsb[wf + h][wl + 32] = q4k_deq8_f16(r.qv.z, r.qv.w, false, Dlo, Clo);
+    ldsb[wf + 2 + h][wl] = q4k_deq8_f16(r.qv.x, r.qv.y, true, Dhi, Chi);
+    ldsb[wf + 2 + h][wl + 32] = q4k_deq8_f16(r.qv.z, r.qv.w, true, Dhi, Chi);
+}
+
+__device__ __forceinline__ void gemm_load_x(const half8 *xa0, const half8 *xa1, int s, half8 (&xf)[2][4]) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        xf[0][k] = xa0[(size_t)(s * 4 + k) * 64];
+        xf[1][k] = xa1[(size_t)(s * 4 + k) * 64];
+    }
+}
+
+__device__ __forceinline__ void gemm_mfma(half8 (*ldsb)[64], int lane, const half8 (&xf)[2][4],
+                                          f32x16 (&acc)[2][4]) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        half8 bfr[4];
+#pragma unroll
+        for (int ob = 0; ob < 4; ob++) bfr[ob] = ldsb[ob * 4 + k][lane];
+#pragma unroll
+        for (int ob = 0; ob < 4; ob++) {
+            acc[0][ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf[0][k], bfr[ob], acc[0][ob], 0, 0, 0);
+            acc[1][ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf[1][k], bfr[ob], acc[1][ob], 0, 0, 0);
+        }
+    }
+}
 
 __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, int64_t row_bytes,
                                                  int N, int K, const half8 *__restrict__ X16,
@@ -482,59 +533,35 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
     const half8 *xa0 = X16 + ((size_t)(m0 / 32 + 2 * wave) * kf_n) * 64 + lane;
     const half8 *xa1 = xa0 + (size_t)kf_n * 64;
 
-    const int S = K / 64;
+    const int S = K / 64;  // a multiple of 4 (K % 256 == 0)
     f32x16 acc[2][4];
 #pragma unroll
     for (int a = 0; a < 2; a++)
 #pragma unroll
         for (int b = 0; b < 4; b++) acc[a][b] = f32x16{};
 
-    u32x4 hv = ld16(wrow);
-    u32x4 qv = ld16(wrow + 16 + 16 * h);
-    half8 xf[2][4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) { xf[0][k] = xa0[k * 64]; xf[1][k] = xa1[k * 64]; }
-
-    for (int s = 0; s < S; s++) {
-        const int buf = s & 1;
-        const int c = s & 3;
-        {
-            float Dlo, Clo, Dhi, Chi;
-            q4k_group_fast(hv, 2 * c, Dlo, Clo);
-            q4k_group_fast(hv, 2 * c + 1, Dhi, Chi);
-            lds[buf][wf + h][wl] = q4k_deq8_f16(qv.x, qv.y, false, Dlo, Clo);
-            lds[buf][wf + h][wl + 32] = q4k_deq8_f16(qv.z, qv.w, false, Dlo, Clo);
-            lds[buf][wf + 2 + h][wl] = q4k_deq8_f16(qv.x, qv.y, true, Dhi, Chi);
-            lds[buf][wf + 2 + h][wl + 32] = q4k_deq8_f16(qv.z, qv.w, true, Dhi, Chi);
-        }
-        half8 xn[2][4];
-        if (s + 1 < S) {
-            const int s1 = s + 1;
-            const uint8_t *blk = wrow + (size_t)(s1 >> 2) * 144;
-            if ((s1 & 3) == 0) hv = ld16(blk);
-            qv = ld16(blk + 16 + 32 * (s1 & 3) + 16 * h);
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                xn[0][k] = xa0[(size_t)(s1 * 4 + k) * 64];
-                xn[1][k] = xa1[(size_t)(s1 * 4 + k) * 64];
-            }
-        }
+    GemmRaw re, ro;            // raw weights of even / odd steps
+    half8 xe[2][4], xo[2][4];  // activations of even / odd steps
+    gemm_load_raw(wrow, 0, h, re, re);
+    gemm_load_x(xa0, xa1, 0, xe);
+    gemm_load_raw(wrow, 1, h, ro, re);
+    gemm_dequant(lds[0], re, 0, wf, wl, h);
+    __syncthreads();
+    for (int s = 0; s < S; s += 2) {
+        // even step s: MFMA(s) from lds[0]; dequant(s+1) into lds[1]
+        gemm_load_x(xa0, xa1, s + 1, xo);
+        if (s + 2 < S) gemm_load_raw(wrow, s + 2, h, re, ro);
+        gemm_dequant(lds[1], ro, s + 1, wf, wl, h);
+        gemm_mfma(lds[0], lane, xe, acc);
         __syncthreads();
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            half8 bfr[4];
-#pragma unroll
-            for (int ob = 0; ob < 4; ob++) bfr[ob] = lds[buf][ob * 4 + k][lane];
-#pragma unroll
-            for (int ob = 0; ob < 4; ob++) {
-                acc[0][ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf[0][k], bfr[ob], acc[0][ob], 0, 0, 0);
-                acc[1][ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf[1][k], bfr[ob], acc[1][ob], 0, 0, 0);
-            }
+        // odd step s+1: MFMA(s+1) from lds[1]; dequant(s+2) into lds[0]
+        if (s + 2 < S) {
+            gemm_load_x(xa0, xa1, s + 2, xe);
+            gemm_load_raw(wrow, s + 3, h, ro, re);
+            gemm_dequant(lds[0], re, s + 2, wf, wl, h);
         }
-        if (s + 1 < S) {
-#pragma unroll
-            for (int k = 0; k < 4; k++) { xf[0][k] = xn[0][k]; xf[1][k] = xn[1][k]; }
-        }
+        gemm_mfma(lds[1], lane, xo, acc);
+        __syncthreads();
     }
 
     // epilogue: 32x32 output D, lane l holds column l%32 (weight row) and rows

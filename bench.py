@@ -43,8 +43,8 @@ METRIC = "Q4_K GEMM TFLOP/s + GEMV weight GB/s (% roofline); DiT block linear ms
 # FETCH_SIZE = 128 MiB and WRITE_SIZE = 256 MiB.  Summaries:
 # profiles/k_skinny_gemv_m1-16_k5120.md, profiles/k_gemm_dit_attention_m8192_k5120.md,
 # profiles/hbm_counters_copy_256MiB.md.  Re-measure when the kernels change.
-TRAFFIC_SKINNY_MEAN = 33932940      # mean over the six GEMV shapes (algorithmic mean 32899072)
-TRAFFIC_GEMM = {"attn_qkv": 2200560763, "attn_out": 631555288}
+TRAFFIC_SKINNY_MEAN = 33767392      # mean over the six GEMV shapes (algorithmic mean 32899072)
+TRAFFIC_GEMM = {"attn_qkv": 2329190762, "attn_out": 782388133}
 
 
 def q4k_bytes(N, K):

@@ -184,7 +184,11 @@ template <int V4>
 __global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ X, int M, int K,
                                                half8 *__restrict__ X16, float *__restrict__ xs_inv) {
     __shared__ float s_red[4];
-    const int t = blockIdx.x;
+    // Consecutive workgroup ids go to different XCDs; give each XCD a
+    // contiguous run of rows instead, so that neighbouring rows, which share
+    // 32-byte pieces of the same fragments, are written through one L2 and
+    // merge there (gridDim.x = Mpad, a multiple of 8).
+    const int t = (int)(blockIdx.x & 7) * (int)(gridDim.x >> 3) + (int)(blockIdx.x >> 3);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n4 = K / 4;
     const f32x4 *xr = reinterpret_cast<const f32x4 *>(X + (size_t)t * K);
@@ -600,6 +604,7 @@ extern "C" hipError_t fh3k_dequant_q4k_f32(const void *src, int64_t row_bytes, i
 
 extern "C" hipError_t fh3k_xprep(const float *x, int M, int K, int Mpad, void *x16, float *xs_inv,
                                  hipStream_t st) {
+    if (Mpad % 8 || Mpad < M) return hipErrorInvalidValue;
     const dim3 grid((unsigned)Mpad), block(256);
     if (K <= 4096)
         hipLaunchKernelGGL(k_xprep<4>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv);

@@ -1,6 +1,8 @@
 /*
- * fh3_oracle.c -- CPU restatement of fh3's Q4_K path.  TEST INFRASTRUCTURE
- * ONLY (see fh3_oracle.h): the checker and CPU baseline for the HIP product.
+ * fh3_oracle.c -- CPU restatement of fh3's Q4_K linear layer and of every
+ * block decoder of src/core/fh3_quant.c (F32, F16, BF16, Q8_0, Q2_K, Q3_K,
+ * Q4_K, Q5_K, Q6_K).  TEST INFRASTRUCTURE ONLY (see fh3_oracle.h): the checker
+ * and CPU baseline for the HIP product.
  *
  * Build flags follow the reference (CMakeLists.txt:15-26): -O3 -mavx2 -mfma
  * -mf16c -ffp-contract=off -fopenmp.  -ffp-contract=off matters: the
@@ -48,13 +50,32 @@ float fh3_oracle_f16_to_f32(uint16_t h) {
     return f;
 }
 
-/* src/core/fh3_quant.c:14-34, restricted to the two types on this path. */
+/* src/core/fh3_quant.c:14-34: bytes per row, by (block bytes, block length). */
 size_t fh3_oracle_row_bytes(int type, int64_t n) {
     if (n <= 0) return 0;
-    if (type == ORACLE_F32) return (size_t)n * sizeof(float);
-    if (type == ORACLE_Q4_K) return (size_t)((n + 255) / 256) * 144u;
-    return 0;
+    int bb, bl;
+    switch (type) {
+        case 0: bb = 4, bl = 1; break;      /* F32 */
+        case 1: bb = 2, bl = 1; break;      /* F16 */
+        case 30: bb = 2, bl = 1; break;     /* BF16 */
+        case 2: bb = 18, bl = 32; break;    /* Q4_0 */
+        case 3: bb = 20, bl = 32; break;    /* Q4_1 */
+        case 6: bb = 22, bl = 32; break;    /* Q5_0 */
+        case 7: bb = 24, bl = 32; break;    /* Q5_1 */
+        case 8: bb = 34, bl = 32; break;    /* Q8_0 */
+        case 9: bb = 40, bl = 32; break;    /* Q8_1 */
+        case 10: bb = 84, bl = 256; break;  /* Q2_K */
+        case 11: bb = 110, bl = 256; break; /* Q3_K */
+        case 12: bb = 144, bl = 256; break; /* Q4_K */
+        case 13: bb = 176, bl = 256; break; /* Q5_K */
+        case 14: bb = 210, bl = 256; break; /* Q6_K */
+        case 15: bb = 292, bl = 256; break; /* Q8_K */
+        default: return 0;
+    }
+    return (size_t)((n + bl - 1) / bl) * (size_t)bb;
 }
+
+static uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 
 /* ------------------------------------------------------------------------ */
 /* Q4_K super-block decode: src/core/fh3_quant.c:154-196.                     */
@@ -104,14 +125,137 @@ static void oracle_dequant_q4_k(const uint8_t *src, float *dst, int64_t n) {
     }
 }
 
+/* ------------------------------------------------------------------------ */
+/* The other block formats of src/core/fh3_quant.c:36-282.  Every value is     */
+/* formed with the reference's roundings: scale products first (d*sc,         */
+/* dmin*m), then the weight product, then the offset subtraction, each in      */
+/* fp32.  Only whole blocks are written (n / block length).                   */
+/* ------------------------------------------------------------------------ */
+
+/* F16 (:36-49): exact conversion; BF16 (:51-56, fh3_quant.h:44-49): the 16 bits
+ * are the top half of the fp32 word. */
+static void oracle_dequant_f16(const uint8_t *src, float *dst, int64_t n) {
+    for (int64_t i = 0; i < n; i++) dst[i] = fh3_oracle_f16_to_f32(rd16(src + 2 * i));
+}
+
+static void oracle_dequant_bf16(const uint8_t *src, float *dst, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        const uint32_t bits = (uint32_t)rd16(src + 2 * i) << 16;
+        memcpy(&dst[i], &bits, sizeof bits);
+    }
+}
+
+/* Q8_0 (:58-72): 34-byte blocks of 32, fp16 d then 32 int8; w = q * d. */
+static void oracle_dequant_q8_0(const uint8_t *src, float *dst, int64_t n) {
+    for (int64_t b = 0; b < n / 32; b++) {
+        const uint8_t *blk = src + b * 34;
+        const float d = fh3_oracle_f16_to_f32(rd16(blk));
+        for (int i = 0; i < 32; i++) dst[b * 32 + i] = (float)(int8_t)blk[2 + i] * d;
+    }
+}
+
+/* Q2_K (:74-114): 84-byte super-blocks.  Bytes 0-15: one byte per 16-weight
+ * group, scale in the low nibble and min in the high nibble; 16-79: two
+ * 32-byte chunks of 2-bit values; 80-81 d, 82-83 dmin.  Weight j of the
+ * super-block lives in chunk j/128 at bit pair (j/32)%4, byte (j%32); its
+ * group is j/16.  w = (d*sc)*q - dmin*m. */
+static void oracle_dequant_q2_k(const uint8_t *src, float *dst, int64_t n) {
+    for (int64_t b = 0; b < n / 256; b++) {
+        const uint8_t *blk = src + b * 84;
+        const float d = fh3_oracle_f16_to_f32(rd16(blk + 80));
+        const float dmin = fh3_oracle_f16_to_f32(rd16(blk + 82));
+        for (int j = 0; j < 256; j++) {
+            const int g = j / 16;
+            const uint8_t q = (uint8_t)((blk[16 + (j / 128) * 32 + (j % 32)] >> (2 * ((j / 32) % 4))) & 3u);
+            const float dl = d * (float)(blk[g] & 15u);
+            const float ml = dmin * (float)(blk[g] >> 4);
+            dst[b * 256 + j] = dl * (float)q - ml;
+        }
+    }
+}
+
+/* Q3_K (:116-152): 110-byte super-blocks.  Bytes 0-31 high-bit mask, 32-95
+ * two 32-byte chunks of 2-bit values, 96-107 the 16 signed 6-bit group scales
+ * (low 4 bits: byte g, low nibble for g < 8, high nibble of byte g-8 after;
+ * top 2 bits: bits 2*(g/4).. of byte 8 + g%4; minus 32), 108-109 d.  Weight j:
+ * group g = j/16; low bits from chunk g/8, byte (g%2)*16 + j%16 of it, bit
+ * pair (g%8)/2; mask bit g/2 of byte (g%2)*16 + j%16; q = low - 4 when the mask
+ * bit is clear.  w = (d*sc)*q. */
+static void oracle_dequant_q3_k(const uint8_t *src, float *dst, int64_t n) {
+    for (int64_t b = 0; b < n / 256; b++) {
+        const uint8_t *blk = src + b * 110;
+        const uint8_t *hm = blk, *qs = blk + 32, *sc = blk + 96;
+        const float d = fh3_oracle_f16_to_f32(rd16(blk + 108));
+        for (int j = 0; j < 256; j++) {
+            const int g = j / 16, l = j % 16;
+            const int lo4 = g < 8 ? (sc[g] & 15) : (sc[g - 8] >> 4);
+            const int hi2 = (sc[8 + g % 4] >> (2 * (g / 4))) & 3;
+            const int scale = (lo4 | (hi2 << 4)) - 32;
+            const int low = (qs[(g / 8) * 32 + (g % 2) * 16 + l] >> (2 * ((g % 8) / 2))) & 3;
+            const int hbit = (hm[(g % 2) * 16 + l] >> (g / 2)) & 1;
+            const float dl = d * (float)scale;
+            dst[b * 256 + j] = dl * (float)(low - (hbit ? 0 : 4));
+        }
+    }
+}
+
+/* Q5_K (:198-236): 176-byte super-blocks.  d, dmin, 12 bytes of 6-bit scales
+ * and mins packed as in Q4_K, 16-47 fifth bits (bit g of byte l for element l
+ * of group g), 48-175 four 32-byte chunks of nibbles (chunk g/2, low nibble
+ * for even g).  w = (d*sc)*q - dmin*m. */
+static void oracle_dequant_q5_k(const uint8_t *src, float *dst, int64_t n) {
+    for (int64_t b = 0; b < n / 256; b++) {
+        const uint8_t *blk = src + b * 176;
+        const float d = fh3_oracle_f16_to_f32(rd16(blk));
+        const float dmin = fh3_oracle_f16_to_f32(rd16(blk + 2));
+        uint8_t sc[8], mn[8];
+        oracle_q4k_scales(blk + 4, sc, mn);
+        for (int g = 0; g < 8; g++) {
+            const float dl = d * (float)sc[g], ml = dmin * (float)mn[g];
+            for (int l = 0; l < 32; l++) {
+                const int nib = (blk[48 + (g / 2) * 32 + l] >> (4 * (g % 2))) & 15;
+                const int bit5 = (blk[16 + l] >> g) & 1;
+                dst[b * 256 + g * 32 + l] = dl * (float)(nib | (bit5 << 4)) - ml;
+            }
+        }
+    }
+}
+
+/* Q6_K (:238-282): 210-byte super-blocks.  0-127 low nibbles, 128-191 high bit
+ * pairs, 192-207 16 int8 group scales, 208-209 d.  Weight j: half h = j/128,
+ * r = (j%128)/16, l = j%16; low nibble of byte h*64 + (r%4)*16 + l (high
+ * nibble when r >= 4); bit pair r/2 of byte 128 + h*32 + (r%2)*16 + l;
+ * q = (nibble | pair << 4) - 32.  w = (d*sc)*q. */
+static void oracle_dequant_q6_k(const uint8_t *src, float *dst, int64_t n) {
+    for (int64_t b = 0; b < n / 256; b++) {
+        const uint8_t *blk = src + b * 210;
+        const float d = fh3_oracle_f16_to_f32(rd16(blk + 208));
+        for (int j = 0; j < 256; j++) {
+            const int h = j / 128, r = (j % 128) / 16, l = j % 16;
+            const int nib = (blk[h * 64 + (r % 4) * 16 + l] >> (4 * (r / 4))) & 15;
+            const int pair = (blk[128 + h * 32 + (r % 2) * 16 + l] >> (2 * (r / 2))) & 3;
+            const float dl = d * (float)(int8_t)blk[192 + j / 16];
+            dst[b * 256 + j] = dl * (float)((nib | (pair << 4)) - 32);
+        }
+    }
+}
+
 /* src/core/fh3_quant.c:284-318: NULL / non-positive n is a silent no-op and an
  * unsupported type writes nothing. */
 void fh3_oracle_dequant(int type, const void *src, float *dst, int64_t n) {
     if (!src || !dst || n <= 0) return;
-    if (type == ORACLE_F32) {
-        memcpy(dst, src, (size_t)n * sizeof(float));
-    } else if (type == ORACLE_Q4_K) {
-        oracle_dequant_q4_k((const uint8_t *)src, dst, n);
+    const uint8_t *s = (const uint8_t *)src;
+    switch (type) {
+        case ORACLE_F32: memcpy(dst, src, (size_t)n * sizeof(float)); break;
+        case 1: oracle_dequant_f16(s, dst, n); break;
+        case 30: oracle_dequant_bf16(s, dst, n); break;
+        case 8: oracle_dequant_q8_0(s, dst, n); break;
+        case 10: oracle_dequant_q2_k(s, dst, n); break;
+        case 11: oracle_dequant_q3_k(s, dst, n); break;
+        case ORACLE_Q4_K: oracle_dequant_q4_k(s, dst, n); break;
+        case 13: oracle_dequant_q5_k(s, dst, n); break;
+        case 14: oracle_dequant_q6_k(s, dst, n); break;
+        default: break;
     }
 }
 

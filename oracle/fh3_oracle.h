@@ -1,6 +1,6 @@
 /*
- * fh3_oracle.h -- CPU restatement of fh3's Q4_K dequantisation and
- * weight-stationary matmul.
+ * fh3_oracle.h -- CPU restatement of fh3's block dequantisation (every type
+ * src/core/fh3_quant.c decodes) and of its Q4_K weight-stationary matmul.
  *
  * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
  * product in fasth3inc_amd/.  Only tests/, __graft_entry__.smoke() and the
@@ -9,10 +9,12 @@
  *
  * Every function restates the arithmetic of the reference file:line it cites
  * (paths relative to the fh3 repository root).  The restatement is pinned by:
- *   - tests/golden/Q4_K.bin      (gguf-py dequantize output, bit-exact)
+ *   - tests/golden/Q4_K.bin and tests/golden/quant/<TYPE>.bin for F16, BF16,
+ *     Q8_0, Q2_K, Q3_K, Q5_K, Q6_K (gguf-py dequantize output, bit-exact)
  *   - tests/golden/matmul_ref.bin (fp64 NumPy product, rel-L2 <= 1e-6)
- *   - tests/golden/ref_vectors.bin (outputs of the reference's own
- *     fh3_quant.c + fh3_ops.c compiled by oracle/Makefile, bitwise)
+ *   - tests/golden/ref_vectors.npz and live calls into oracle/_ref (the
+ *     reference's own fh3_quant.c + fh3_ops.c compiled by oracle/Makefile),
+ *     bitwise, for the matmul and for every decoder on random blocks
  *   - closed-form cases in tests/test_oracle.py (fp16 decode of every bit
  *     pattern, all 64x64 scale/min decodings, brute-force small products).
  * Nothing in this file is "parity unpinned".
@@ -38,10 +40,11 @@ typedef struct Fh3OracleW {
 /* src/core/fh3_quant.h:20-41 -- exact fp16 -> fp32 (F16C semantics). */
 float fh3_oracle_f16_to_f32(uint16_t h);
 
-/* src/core/fh3_quant.c:14-34 -- bytes of one weight row (F32 and Q4_K). */
+/* src/core/fh3_quant.c:14-34 -- bytes of one weight row, every type id. */
 size_t fh3_oracle_row_bytes(int type, int64_t n);
 
-/* src/core/fh3_quant.c:154-196 (Q4_K) and :284-318 (dispatch, F32 + Q4_K). */
+/* src/core/fh3_quant.c:36-282 (per-type decoders) and :284-318 (dispatch):
+ * F32, F16, BF16, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K; other ids write nothing. */
 void fh3_oracle_dequant(int type, const void *src, float *dst, int64_t n);
 
 /* src/core/fh3_ops.c:317-404 -- OpenMP over 64-row output tiles.  Output bits

@@ -120,6 +120,54 @@ def read_q4k_fixture():
     return t, rows, cols, raw, ref
 
 
+# Type ids (reference include/fh3/fh3.h:23-39) -> (block length, block bytes,
+# byte offsets of the fp16 scale fields).  The decodable set of
+# src/core/fh3_quant.c:284-318.
+QTYPES = {
+    "F16": (1, 1, 2, ()),
+    "BF16": (30, 1, 2, ()),
+    "Q8_0": (8, 32, 34, (0,)),
+    "Q2_K": (10, 256, 84, (80, 82)),
+    "Q3_K": (11, 256, 110, (108,)),
+    "Q4_K": (12, 256, 144, (0, 2)),
+    "Q5_K": (13, 256, 176, (0, 2)),
+    "Q6_K": (14, 256, 210, (208,)),
+}
+
+
+def read_quant_fixture(name):
+    """tests/golden/quant/<name>.bin (Q4_K: tests/golden/Q4_K.bin), same layout
+    as read_q4k_fixture."""
+    path = os.path.join(GOLDEN, "Q4_K.bin" if name == "Q4_K" else os.path.join("quant", name + ".bin"))
+    with open(path, "rb") as f:
+        buf = f.read()
+    t, rows, cols, nraw = struct.unpack_from("<IIII", buf, 0)
+    raw = np.frombuffer(buf, dtype=np.uint8, count=nraw, offset=16).copy()
+    ref = np.frombuffer(buf, dtype=np.float32, count=rows * cols, offset=16 + nraw).reshape(rows, cols).copy()
+    return t, rows, cols, raw, ref
+
+
+def random_blocks(rng, name, rows, cols, scale_lo=-14, scale_hi=-4, finite=True):
+    """Random rows of format `name`: uniform random bytes, then every fp16 scale
+    field overwritten with +-2^e * (1 + m/1024), e in [scale_lo, scale_hi]
+    (`finite`), so the decoded values are finite and of DiT-like magnitude.
+    F16/BF16 payloads get finite halves of magnitude 2^-8..2^8."""
+    t, bl, bb, scale_offs = QTYPES[name]
+    nblk = cols // bl
+    raw = rng.integers(0, 256, size=(rows, nblk, bb), dtype=np.uint8)
+    if name in ("F16", "BF16"):
+        v = (rng.standard_normal((rows, cols)) * 4.0).astype(np.float32)
+        bits = v.astype(np.float16).view(np.uint16) if name == "F16" else (v.view(np.uint32) >> 16).astype(np.uint16)
+        return bits.reshape(rows, -1).view(np.uint8).reshape(-1).copy()
+    for off in scale_offs:
+        e = rng.integers(scale_lo, scale_hi + 1, size=(rows, nblk))
+        m = rng.integers(0, 1024, size=(rows, nblk))
+        s = rng.integers(0, 2, size=(rows, nblk))
+        h = np.asarray(np.ldexp(1.0 + m / 1024.0, e) * np.where(s, -1.0, 1.0), dtype=np.float16)
+        raw[:, :, off:off + 2] = h.view(np.uint8).reshape(rows, nblk, 2) if finite else raw[:, :, off:off + 2]
+    return raw.reshape(-1)
+
+
 def read_matmul_fixture():
     """tests/golden/matmul_ref.bin: <IIIII> type, in, out, n_tok, w_bytes; W; X; bias;
     y_ref computed in fp64 (reference tools/emit_quant_fixtures.py:125-132)."""

@@ -4,6 +4,7 @@ itself, and closed forms that a plausible slip (wrong nibble, swapped scale
 bits, dropped term, transposed operand) would fail.
 """
 import os
+import zlib
 
 import numpy as np
 import pytest
@@ -20,6 +21,66 @@ def test_dequant_q4k_fixture_bitexact(oracle):
     assert H.load_oracle().fh3_oracle_row_bytes(12, cols) * rows == raw.size
     out = H.oracle_dequant(oracle, raw, rows, cols)
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", sorted(H.QTYPES))
+def test_dequant_fixture_bitexact_every_type(oracle, name):
+    """reference tests/unit/test_quant.c:40-130 for each decodable type; the
+    fixtures were written by gguf-py's own dequantize, an implementation
+    independent of the reference's C."""
+    t, rows, cols, raw, ref = H.read_quant_fixture(name)
+    assert (t, rows, cols) == (H.QTYPES[name][0], 4, 512)
+    assert oracle.fh3_oracle_row_bytes(t, cols) * rows == raw.size
+    out = H.oracle_dequant(oracle, raw, rows, cols, qtype=t)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", sorted(H.QTYPES))
+@pytest.mark.parametrize("finite", [True, False])
+def test_dequant_bitwise_vs_reference_build(oracle, ref, name, finite):
+    """Random blocks (with raw, possibly Inf/NaN scale fields when not
+    `finite`), odd lengths that leave a partial block unwritten."""
+    rng = np.random.default_rng(zlib.crc32(("%s/%d" % (name, finite)).encode()))
+    t, bl, bb, _ = H.QTYPES[name]
+    rows, cols = 7, 1024
+    raw = H.random_blocks(rng, name, rows, cols, finite=finite)
+    if not finite and name not in ("F16", "BF16"):
+        raw = rng.integers(0, 256, size=raw.size, dtype=np.uint8)
+    for n in (cols, cols - 1, bl):
+        a = np.full((rows, cols), 7.0, np.float32)
+        b = np.full((rows, cols), 7.0, np.float32)
+        rb = oracle.fh3_oracle_row_bytes(t, cols)
+        for r in range(rows):
+            p = raw[r * rb:]
+            oracle.fh3_oracle_dequant(t, p.ctypes.data, a[r].ctypes.data, n)
+            ref.fh3_dequant(t, p.ctypes.data, b[r].ctypes.data, n)
+        same = (a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))
+        assert same.all(), (name, n)
+        written = n if bl == 1 else (n // bl) * bl
+        assert (a[:, written:] == 7.0).all()
+
+
+def test_dequant_unsupported_types_write_nothing(oracle):
+    """src/core/fh3_quant.c:314-316: Q4_0/Q4_1/Q5_0/Q5_1/Q8_1/Q8_K have row sizes
+    but no decoder."""
+    raw = np.arange(4096, dtype=np.uint8)
+    for t in (2, 3, 6, 7, 9, 15, 99):
+        out = np.full(256, 3.0, np.float32)
+        oracle.fh3_oracle_dequant(t, raw.ctypes.data, out.ctypes.data, 256)
+        assert (out == 3.0).all()
+
+
+def test_q8_0_closed_form(oracle):
+    """w = q * d with q int8 and d the block's fp16 scale."""
+    raw = np.zeros(34 * 2, np.uint8)
+    raw[0:2] = np.array([0.5], np.float16).view(np.uint8)
+    raw[2:34] = np.arange(-16, 16, dtype=np.int8).view(np.uint8)
+    raw[34:36] = np.array([-3.0], np.float16).view(np.uint8)
+    raw[36:68] = np.array([127, -128] * 16, dtype=np.int8).view(np.uint8)
+    out = np.zeros(64, np.float32)
+    oracle.fh3_oracle_dequant(8, raw.ctypes.data, out.ctypes.data, 64)
+    assert np.array_equal(out[:32], np.arange(-16, 16) * 0.5)
+    assert np.array_equal(out[32:], np.array([127, -128] * 16) * -3.0)
 
 
 def test_matmul_fixture_vs_fp64(oracle):

@@ -301,14 +301,17 @@ extern "C" int fh3_hip_dequant_dev(int type, const void *d_src, float *d_dst, in
                                    void *stream) {
     if (!d_src || !d_dst || rows <= 0 || n <= 0)
         return set_err(FH3_E_INVALID, "fh3_hip_dequant_dev: NULL pointer or non-positive size");
-    if (type != FH3_QUANT_Q4_K) return set_err(FH3_E_INVALID, "fh3_hip_dequant_dev: unsupported type %d", type);
-    if (n % 256) return set_err(FH3_E_INVALID, "fh3_hip_dequant_dev: n=%lld is not a multiple of 256", (long long)n);
+    const int bl = fh3k_dequant_block_len(type);
+    if (bl == 0) return set_err(FH3_E_INVALID, "fh3_hip_dequant_dev: unsupported type %d", type);
+    if (n % bl)
+        return set_err(FH3_E_INVALID, "fh3_hip_dequant_dev: n=%lld is not a multiple of the block length %d",
+                       (long long)n, bl);
     if (((uintptr_t)d_src & 15u) || ((uintptr_t)d_dst & 15u))
         return set_err(FH3_E_INVALID, "fh3_hip_dequant_dev: pointers must be 16-byte aligned");
     int rc = ensure_init();
     if (rc != FH3_OK) return rc;
     hipStream_t st = stream ? (hipStream_t)stream : g.stream;
-    FH3_HIPCALL(fh3k_dequant_q4k_f32(d_src, (int64_t)fh3_row_bytes(type, n), n, rows, d_dst, st));
+    FH3_HIPCALL(fh3k_dequant_f32(type, d_src, (int64_t)fh3_row_bytes(type, n), n, rows, d_dst, st));
     return FH3_OK;
 }
 
@@ -431,23 +434,25 @@ static void report(const char *fn, int rc) {
 
 extern "C" void fh3_dequant(int type, const void *src, float *dst, int64_t n) {
     if (!src || !dst || n <= 0) return;
-    if (type != FH3_QUANT_Q4_K) {
+    const int bl = fh3k_dequant_block_len(type);
+    if (bl == 0) {
         set_err(FH3_E_INVALID, "fh3_dequant: unsupported type %d", type);
         fprintf(stderr, "fh3_dequant: unsupported type %d\n", type);
         return;
     }
-    const int64_t nsb = n / 256;
-    if (nsb == 0) return;
+    // whole blocks only, as the reference's decoders
+    const int64_t cnt = (n / bl) * bl;
+    if (cnt == 0) return;
     int rc = ensure_init();
     if (rc != FH3_OK) { report("fh3_dequant", rc); return; }
     std::lock_guard<std::recursive_mutex> lk(g.mu);
-    const size_t in_bytes = (size_t)nsb * 144u, out_bytes = (size_t)nsb * 256u * sizeof(float);
+    const size_t in_bytes = fh3_row_bytes(type, cnt), out_bytes = (size_t)cnt * sizeof(float);
     if ((rc = grow(g.st_w, in_bytes)) != FH3_OK || (rc = grow(g.st_y, out_bytes)) != FH3_OK) {
         report("fh3_dequant", rc);
         return;
     }
     hipError_t e = hipMemcpy(g.st_w.p, src, in_bytes, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = fh3k_dequant_q4k_f32(g.st_w.p, (int64_t)in_bytes, nsb * 256, 1, (float *)g.st_y.p, g.stream);
+    if (e == hipSuccess) e = fh3k_dequant_f32(type, g.st_w.p, (int64_t)in_bytes, cnt, 1, (float *)g.st_y.p, g.stream);
     if (e == hipSuccess) e = hipStreamSynchronize(g.stream);
     if (e == hipSuccess) e = hipMemcpy(dst, g.st_y.p, out_bytes, hipMemcpyDeviceToHost);
     if (e != hipSuccess) report("fh3_dequant", hip_fail(e, "fh3_dequant"));

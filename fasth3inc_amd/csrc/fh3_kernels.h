@@ -10,9 +10,21 @@
 extern "C" {
 #endif
 
-// Bit-exact fp32 dequantisation of `rows` Q4_K rows (n % 256 == 0).
-hipError_t fh3k_dequant_q4k_f32(const void *src, int64_t row_bytes, int64_t n, int64_t rows,
-                                float *dst, hipStream_t st);
+// Weight type ids (the values of the reference's FH3_QUANT_* enum).
+enum {
+    FH3K_F32 = 0, FH3K_F16 = 1, FH3K_Q8_0 = 8, FH3K_Q2_K = 10, FH3K_Q3_K = 11,
+    FH3K_Q4_K = 12, FH3K_Q5_K = 13, FH3K_Q6_K = 14, FH3K_BF16 = 30
+};
+
+// Elements per block of a decodable type (1 for F32/F16/BF16), 0 otherwise.
+int fh3k_dequant_block_len(int type);
+
+// Bit-exact fp32 dequantisation of `rows` rows of n elements (n a multiple of
+// the block length), source rows row_bytes apart, output dense [rows][n].
+// src 2-byte aligned with row_bytes even (16-byte for Q4_K/Q5_K), dst
+// 16-byte aligned.
+hipError_t fh3k_dequant_f32(int type, const void *src, int64_t row_bytes, int64_t n, int64_t rows,
+                            float *dst, hipStream_t st);
 
 // x[M][K] fp32 -> x16 fragments (Mpad x K fp16, Mpad % 32 == 0, rows >= M zero)
 // and xs_inv[Mpad] (per-row inverse power-of-two scale).

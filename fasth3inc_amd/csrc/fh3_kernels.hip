@@ -6,7 +6,8 @@
 //   group 2c+1 in its high nibbles.  w = (d*sc_g)*q - dmin*m_g.
 //
 // Kernels
-//   k_dequant_q4k_f32   bit-exact fp32 dequantisation (parity / debug path)
+//   k_dequant_blocks<T> bit-exact fp32 dequantisation of Q8_0/Q2_K/Q3_K/Q4_K/Q5_K/Q6_K
+//   k_dequant_half<BF>  bit-exact fp32 from F16 / BF16
 //   k_xprep             fp32 activations -> fp16 MFMA fragments, per-row 2^e scale
 //   k_skinny<TB,C>      small n_tok: one wavefront per 16 weight rows per K slice of
 //                       C super-blocks, exact weights (sc*q in fp16), two
@@ -131,41 +132,158 @@ __device__ __forceinline__ u32x4 ld16(const uint8_t *p) {
 }
 
 // ---------------------------------------------------------------------------
-// Bit-exact fp32 dequantisation.  One thread per (row, super-block, 16-byte
-// quarter of the nibbles): 32 outputs, two groups.
+// Bit-exact fp32 dequantisation of every block format the reference decodes
+// (src/core/fh3_quant.c:58-282).  One thread per 16 consecutive outputs of a
+// block ("piece" G): 16 pieces per 256-weight super-block, 2 per Q8_0 block,
+// so a wavefront writes 4 KiB of contiguous fp32 with 16-byte stores.  Every
+// value is formed with the reference's roundings (__fmul_rn / __fsub_rn keep
+// the compiler from contracting them into an fma): the group scale product
+// first, then the weight product, then the offset subtraction.
+//
+// Block starts are only as aligned as the block size allows (Q5_K 16 B, Q2_K
+// 4 B, Q3_K / Q6_K / Q8_0 2 B), so each format loads with its own guaranteed
+// alignment and never wider.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_dequant_q4k_f32(const uint8_t *__restrict__ src,
-                                                         int64_t row_bytes, int64_t n, int64_t rows,
-                                                         float *__restrict__ dst) {
-    const int64_t nsb = n / 256;
+template <int A>
+__device__ __forceinline__ u32x4 ld16_al(const uint8_t *p) {
+    if constexpr (A >= 16) {
+        return ld16(p);
+    } else if constexpr (A >= 4) {
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(p);
+        return u32x4{q[0], q[1], q[2], q[3]};
+    } else {
+        const uint16_t *q = reinterpret_cast<const uint16_t *>(p);
+        u32x4 r;
+#pragma unroll
+        for (int i = 0; i < 4; i++) r[i] = (uint32_t)q[2 * i] | ((uint32_t)q[2 * i + 1] << 16);
+        return r;
+    }
+}
+
+__device__ __forceinline__ uint32_t byte_of(const u32x4 v, int i) {
+    return (v[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+}
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) {
+    return *reinterpret_cast<const uint16_t *>(p);
+}
+
+// Per-format geometry: block length, block bytes, pieces (threads) per block.
+template <int T> struct Fmt;
+template <> struct Fmt<FH3K_Q8_0> { static constexpr int BL = 32, BB = 34, P = 2; };
+template <> struct Fmt<FH3K_Q2_K> { static constexpr int BL = 256, BB = 84, P = 16; };
+template <> struct Fmt<FH3K_Q3_K> { static constexpr int BL = 256, BB = 110, P = 16; };
+template <> struct Fmt<FH3K_Q4_K> { static constexpr int BL = 256, BB = 144, P = 16; };
+template <> struct Fmt<FH3K_Q5_K> { static constexpr int BL = 256, BB = 176, P = 16; };
+template <> struct Fmt<FH3K_Q6_K> { static constexpr int BL = 256, BB = 210, P = 16; };
+
+// Outputs 16G..16G+15 of one block.
+template <int T>
+__device__ __forceinline__ void deq_piece(const uint8_t *blk, int G, float o[16]) {
+    if constexpr (T == FH3K_Q8_0) {
+        // fh3_quant.c:58-72: d (fp16) then 32 int8; w = q * d
+        const float d = f16_to_f32_exact(ld_u16(blk));
+        const u32x4 q = ld16_al<2>(blk + 2 + 16 * G);
+#pragma unroll
+        for (int l = 0; l < 16; l++) o[l] = __fmul_rn((float)(int8_t)byte_of(q, l), d);
+    } else if constexpr (T == FH3K_Q2_K) {
+        // fh3_quant.c:74-114: bytes 0-15 scale|min<<4 per 16-group, 16-79 two
+        // 32-byte chunks of 2-bit values (chunk G/8, half G%2, bit pair (G/2)%4),
+        // 80 d, 82 dmin; w = (d*sc)*q - dmin*m
+        const float d = f16_to_f32_exact(ld_u16(blk + 80));
+        const float dmin = f16_to_f32_exact(ld_u16(blk + 82));
+        const uint32_t sm = blk[G];
+        const float dl = __fmul_rn(d, (float)(sm & 15u)), ml = __fmul_rn(dmin, (float)(sm >> 4));
+        const u32x4 q = ld16_al<4>(blk + 16 + (G >> 3) * 32 + (G & 1) * 16);
+        const int sh = 2 * ((G >> 1) & 3);
+#pragma unroll
+        for (int l = 0; l < 16; l++)
+            o[l] = __fsub_rn(__fmul_rn(dl, (float)((byte_of(q, l) >> sh) & 3u)), ml);
+    } else if constexpr (T == FH3K_Q3_K) {
+        // fh3_quant.c:116-152: 0-31 high-bit mask, 32-95 2-bit values, 96-107
+        // signed 6-bit scales (low 4 bits from nibbles of bytes 96-103, top 2
+        // from bytes 104-107, minus 32), 108 d.  q = low2 - 4 where the mask
+        // bit G/2 is clear; w = (d*sc)*q
+        const float d = f16_to_f32_exact(ld_u16(blk + 108));
+        const uint32_t lo4 = G < 8 ? (blk[96 + G] & 15u) : (blk[88 + G] >> 4);
+        const uint32_t hi2 = (blk[104 + (G & 3)] >> (2 * (G >> 2))) & 3u;
+        const float dl = __fmul_rn(d, (float)((int)(lo4 | (hi2 << 4)) - 32));
+        const u32x4 q = ld16_al<2>(blk + 32 + (G >> 3) * 32 + (G & 1) * 16);
+        const u32x4 hm = ld16_al<2>(blk + (G & 1) * 16);
+        const int shl = 2 * ((G & 7) >> 1), shh = G >> 1;
+#pragma unroll
+        for (int l = 0; l < 16; l++) {
+            const int v = (int)((byte_of(q, l) >> shl) & 3u) - (((byte_of(hm, l) >> shh) & 1u) ? 0 : 4);
+            o[l] = __fmul_rn(dl, (float)v);
+        }
+    } else if constexpr (T == FH3K_Q4_K || T == FH3K_Q5_K) {
+        // fh3_quant.c:154-236: d, dmin, 12 bytes of packed 6-bit scales/mins;
+        // group g = G/2 has its nibbles in chunk g/2 (low nibble for even g);
+        // Q5_K adds bit g of byte 16 + l' (l' = index inside the group) as the
+        // fifth bit.  w = (d*sc)*q - dmin*m
+        const u32x4 hdr = ld16(blk);
+        const int g = G >> 1, h = G & 1;
+        float D, Mn;
+        q4k_group(hdr, g, D, Mn);
+        constexpr int QS = T == FH3K_Q4_K ? 16 : 48;
+        const u32x4 q = ld16(blk + QS + (g >> 1) * 32 + 16 * h);
+        u32x4 qh = u32x4{0u, 0u, 0u, 0u};
+        if constexpr (T == FH3K_Q5_K) qh = ld16(blk + 16 + 16 * h);
+        const int sh = 4 * (g & 1);
+#pragma unroll
+        for (int l = 0; l < 16; l++) {
+            uint32_t v = (byte_of(q, l) >> sh) & 15u;
+            if constexpr (T == FH3K_Q5_K) v |= ((byte_of(qh, l) >> g) & 1u) << 4;
+            o[l] = __fsub_rn(__fmul_rn(D, (float)v), Mn);
+        }
+    } else {
+        // fh3_quant.c:238-282 (Q6_K): 0-127 low nibbles, 128-191 high bit
+        // pairs, 192-207 int8 scales, 208 d.  Half h = G/8, r = G%8: nibble
+        // r/4 of byte h*64 + (r%4)*16 + l, pair r/2 of byte 128 + h*32 +
+        // (r%2)*16 + l; q = (nibble | pair << 4) - 32; w = (d*sc)*q
+        const float d = f16_to_f32_exact(ld_u16(blk + 208));
+        const int h = G >> 3, r = G & 7;
+        const u32x4 ql = ld16_al<2>(blk + h * 64 + (r & 3) * 16);
+        const u32x4 qh = ld16_al<2>(blk + 128 + h * 32 + (r & 1) * 16);
+        const float dl = __fmul_rn(d, (float)(int8_t)blk[192 + G]);
+        const int shl = 4 * (r >> 2), shh = 2 * (r >> 1);
+#pragma unroll
+        for (int l = 0; l < 16; l++) {
+            const int v = (int)(((byte_of(ql, l) >> shl) & 15u) | (((byte_of(qh, l) >> shh) & 3u) << 4)) - 32;
+            o[l] = __fmul_rn(dl, (float)v);
+        }
+    }
+}
+
+template <int T>
+__global__ __launch_bounds__(256) void k_dequant_blocks(const uint8_t *__restrict__ src, int64_t row_bytes,
+                                                        int64_t nblk, int64_t rows, float *__restrict__ dst) {
+    constexpr int BL = Fmt<T>::BL, BB = Fmt<T>::BB, P = Fmt<T>::P;
+    const int64_t per_row = nblk * P;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= rows * nsb * 8) return;
-    const int64_t row = gid / (nsb * 8);
-    const int64_t rem = gid - row * nsb * 8;
-    const int64_t sb = rem >> 3;
-    const int piece = (int)(rem & 7);
-    const int c = piece >> 1, h = piece & 1;
-    const uint8_t *blk = src + row * row_bytes + sb * 144;
-    const u32x4 hdr = ld16(blk);
-    float Dlo, Mlo, Dhi, Mhi;
-    q4k_group(hdr, 2 * c, Dlo, Mlo);
-    q4k_group(hdr, 2 * c + 1, Dhi, Mhi);
-    const u32x4 qv = ld16(blk + 16 + 32 * c + 16 * h);
-    float *out = dst + row * n + sb * 256;
-    float lo[16], hi[16];
+    if (gid >= rows * per_row) return;
+    const int64_t row = gid / per_row;
+    const int64_t rem = gid - row * per_row;
+    const int64_t b = rem / P;
+    const int G = (int)(rem - b * P);
+    float o[16];
+    deq_piece<T>(src + row * row_bytes + b * BB, G, o);
+    f32x4 *out = reinterpret_cast<f32x4 *>(dst + row * nblk * BL + b * BL + 16 * G);
 #pragma unroll
-    for (int j = 0; j < 16; j++) {
-        const uint32_t byte = (qv[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-        lo[j] = __fsub_rn(__fmul_rn(Dlo, (float)(byte & 15u)), Mlo);
-        hi[j] = __fsub_rn(__fmul_rn(Dhi, (float)(byte >> 4)), Mhi);
-    }
-    f32x4 *olo = reinterpret_cast<f32x4 *>(out + (2 * c) * 32 + 16 * h);
-    f32x4 *ohi = reinterpret_cast<f32x4 *>(out + (2 * c + 1) * 32 + 16 * h);
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        olo[j] = f32x4{lo[4 * j], lo[4 * j + 1], lo[4 * j + 2], lo[4 * j + 3]};
-        ohi[j] = f32x4{hi[4 * j], hi[4 * j + 1], hi[4 * j + 2], hi[4 * j + 3]};
-    }
+    for (int j = 0; j < 4; j++) out[j] = f32x4{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
+}
+
+// F16 (fh3_quant.c:36-49, exact, F16C NaN quieting) and BF16 (:51-56, the bits
+// are the top half of the fp32 word): one thread per element.
+template <bool BF>
+__global__ __launch_bounds__(256) void k_dequant_half(const uint8_t *__restrict__ src, int64_t row_bytes,
+                                                      int64_t n, int64_t rows, float *__restrict__ dst) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= rows * n) return;
+    const int64_t row = gid / n;
+    const int64_t i = gid - row * n;
+    const uint32_t h = ld_u16(src + row * row_bytes + 2 * i);
+    dst[gid] = BF ? __builtin_bit_cast(float, h << 16) : f16_to_f32_exact(h);
 }
 
 // ---------------------------------------------------------------------------
@@ -592,14 +710,53 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
 // ---------------------------------------------------------------------------
 // Launchers (host side, called by fh3_hip.cpp)
 // ---------------------------------------------------------------------------
-extern "C" hipError_t fh3k_dequant_q4k_f32(const void *src, int64_t row_bytes, int64_t n, int64_t rows,
-                                           float *dst, hipStream_t st) {
-    const int64_t threads = rows * (n / 256) * 8;
-    if (threads <= 0) return hipSuccess;
-    const int64_t blocks = (threads + 255) / 256;
-    hipLaunchKernelGGL(k_dequant_q4k_f32, dim3((unsigned)blocks), dim3(256), 0, st,
-                       (const uint8_t *)src, row_bytes, n, rows, dst);
+template <int T>
+static hipError_t launch_dequant_blocks(const void *src, int64_t row_bytes, int64_t n, int64_t rows, float *dst,
+                                        hipStream_t st) {
+    const int64_t nblk = n / Fmt<T>::BL;
+    const int64_t blocks = (rows * nblk * Fmt<T>::P + 255) / 256;
+    if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_dequant_blocks<T>, dim3((unsigned)blocks), dim3(256), 0, st, (const uint8_t *)src,
+                       row_bytes, nblk, rows, dst);
     return hipGetLastError();
+}
+
+extern "C" int fh3k_dequant_block_len(int type) {
+    switch (type) {
+        case FH3K_F32: case FH3K_F16: case FH3K_BF16: return 1;
+        case FH3K_Q8_0: return 32;
+        case FH3K_Q2_K: case FH3K_Q3_K: case FH3K_Q4_K: case FH3K_Q5_K: case FH3K_Q6_K: return 256;
+        default: return 0;
+    }
+}
+
+extern "C" hipError_t fh3k_dequant_f32(int type, const void *src, int64_t row_bytes, int64_t n, int64_t rows,
+                                       float *dst, hipStream_t st) {
+    const int bl = fh3k_dequant_block_len(type);
+    if (bl == 0 || n <= 0 || rows <= 0 || n % bl) return hipErrorInvalidValue;
+    if (type == FH3K_F32) {
+        return hipMemcpy2DAsync(dst, (size_t)n * sizeof(float), src, (size_t)row_bytes, (size_t)n * sizeof(float),
+                                (size_t)rows, hipMemcpyDeviceToDevice, st);
+    }
+    if (type == FH3K_F16 || type == FH3K_BF16) {
+        const int64_t blocks = (rows * n + 255) / 256;
+        if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
+        if (type == FH3K_F16)
+            hipLaunchKernelGGL(k_dequant_half<false>, dim3((unsigned)blocks), dim3(256), 0, st,
+                               (const uint8_t *)src, row_bytes, n, rows, dst);
+        else
+            hipLaunchKernelGGL(k_dequant_half<true>, dim3((unsigned)blocks), dim3(256), 0, st,
+                               (const uint8_t *)src, row_bytes, n, rows, dst);
+        return hipGetLastError();
+    }
+    switch (type) {
+        case FH3K_Q8_0: return launch_dequant_blocks<FH3K_Q8_0>(src, row_bytes, n, rows, dst, st);
+        case FH3K_Q2_K: return launch_dequant_blocks<FH3K_Q2_K>(src, row_bytes, n, rows, dst, st);
+        case FH3K_Q3_K: return launch_dequant_blocks<FH3K_Q3_K>(src, row_bytes, n, rows, dst, st);
+        case FH3K_Q4_K: return launch_dequant_blocks<FH3K_Q4_K>(src, row_bytes, n, rows, dst, st);
+        case FH3K_Q5_K: return launch_dequant_blocks<FH3K_Q5_K>(src, row_bytes, n, rows, dst, st);
+        default: return launch_dequant_blocks<FH3K_Q6_K>(src, row_bytes, n, rows, dst, st);
+    }
 }
 
 extern "C" hipError_t fh3k_xprep(const float *x, int M, int K, int Mpad, void *x16, float *xs_inv,

@@ -79,9 +79,11 @@ typedef struct Fh3LayerView {
 size_t fh3_row_bytes(int type, int64_t n);
 
 /* Dequantise n elements of one row from host memory to host fp32, on the GPU.
- * Q4_K output is bit-identical to the reference.  Q4_K writes n/256 whole
- * super-blocks, as the reference does; other types print "unsupported type"
- * and write nothing.  Replaces src/core/fh3_quant.c:284-318. */
+ * F32, F16, BF16, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K and Q6_K are decoded
+ * bit-identically to the reference; block types write only whole blocks
+ * (n/32 for Q8_0, n/256 for the K types), as the reference does.  Other types
+ * print "unsupported type" and write nothing.  NULL pointers or n <= 0 are a
+ * silent no-op.  Replaces src/core/fh3_quant.c:36-318. */
 void fh3_dequant(int type, const void *src, float *dst, int64_t n);
 
 /* y[n_tok][out] = x[n_tok][in] * W^T (+ bias[out]) on host buffers, computed

@@ -40,9 +40,11 @@ int fh3_hip_memcpy_dtod(void *dst, const void *src, size_t bytes);
 int fh3_hip_memset(void *dptr, int value, size_t bytes);
 int fh3_hip_synchronize(void);
 
-/* Bit-exact fp32 dequantisation of `rows` Q4_K rows of n elements each,
- * rows spaced fh3_row_bytes(type, n) apart in d_src, written densely to d_dst
- * [rows][n].  n % 256 == 0.  Same bits as src/core/fh3_quant.c:154-196. */
+/* Bit-exact fp32 dequantisation of `rows` rows of n elements each, rows
+ * spaced fh3_row_bytes(type, n) apart in d_src, written densely to d_dst
+ * [rows][n].  Types F32, F16, BF16, Q8_0 (n % 32 == 0), Q2_K, Q3_K, Q4_K, Q5_K,
+ * Q6_K (n % 256 == 0); pointers 16-byte aligned.  Same bits as
+ * src/core/fh3_quant.c:36-282.  FH3_E_INVALID for another type or size. */
 int fh3_hip_dequant_dev(int type, const void *d_src, float *d_dst, int64_t rows, int64_t n,
                         void *stream);
 

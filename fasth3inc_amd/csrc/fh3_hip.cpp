@@ -79,9 +79,13 @@ int grow(DevBuf &b, size_t need) {
 
 int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
-int choose_path(int n_tok) {
+// A forced path that cannot take the shape falls back to the automatic choice.
+int choose_path(int n_tok, int64_t in) {
+    const bool g8 = in <= fh3k_max_in() && fh3k_gemv8_fits((int)in, n_tok);
+    if (g.path == FH3_HIP_PATH_GEMV8 && g8) return FH3_HIP_PATH_GEMV8;
     if (g.path == FH3_HIP_PATH_SKINNY && n_tok <= fh3k_skinny_max_tokens()) return FH3_HIP_PATH_SKINNY;
     if (g.path == FH3_HIP_PATH_GEMM) return FH3_HIP_PATH_GEMM;
+    if (g8) return FH3_HIP_PATH_GEMV8;
     return n_tok <= fh3k_skinny_max_tokens() ? FH3_HIP_PATH_SKINNY : FH3_HIP_PATH_GEMM;
 }
 
@@ -287,7 +291,7 @@ extern "C" int fh3_hip_graph_destroy(void *graph_exec) {
 }
 
 extern "C" int fh3_hip_set_path(int path) {
-    if (path < FH3_HIP_PATH_AUTO || path > FH3_HIP_PATH_GEMM)
+    if (path < FH3_HIP_PATH_AUTO || path > FH3_HIP_PATH_GEMV8)
         return set_err(FH3_E_INVALID, "fh3_hip_set_path: bad path %d", path);
     g.path = path;
     return FH3_OK;
@@ -295,7 +299,7 @@ extern "C" int fh3_hip_set_path(int path) {
 
 extern "C" int fh3_hip_skinny_max(void) { return fh3k_skinny_max_tokens(); }
 
-extern "C" int fh3_hip_matmul_path(int n_tok) { return choose_path(n_tok); }
+extern "C" int fh3_hip_matmul_path(int n_tok, int64_t in) { return choose_path(n_tok, in); }
 
 extern "C" int fh3_hip_dequant_dev(int type, const void *d_src, float *d_dst, int64_t rows, int64_t n,
                                    void *stream) {
@@ -342,6 +346,12 @@ extern "C" size_t fh3_hip_prepared_bytes(int n_tok, int64_t in) {
 }
 
 static int prepare(const float *d_x, int n_tok, int64_t in, void *d_prep, int64_t rows, hipStream_t st) {
+    if (choose_path(n_tok, in) == FH3_HIP_PATH_GEMV8) {
+        // that kernel quantises fp32 activations itself: the prepared form is x
+        FH3_HIPCALL(hipMemcpyAsync(d_prep, d_x, (size_t)n_tok * (size_t)in * sizeof(float),
+                                   hipMemcpyDeviceToDevice, st));
+        return FH3_OK;
+    }
     float *xs_inv = (float *)((char *)d_prep + prep_scale_offset(n_tok, in));
     FH3_HIPCALL(fh3k_xprep(d_x, n_tok, (int)in, (int)rows, d_prep, xs_inv, st));
     return FH3_OK;
@@ -361,7 +371,10 @@ static int product(const Fh3W *w, const void *prep, int n_tok, const float *bias
     const int K = (int)w->in, N = (int)w->out;
     const int64_t row_bytes = (int64_t)fh3_row_bytes(w->type, w->in);
     const float *xs_inv = (const float *)((const char *)prep + prep_scale_offset(n_tok, w->in));
-    if (choose_path(n_tok) == FH3_HIP_PATH_SKINNY) {
+    const int path = choose_path(n_tok, w->in);
+    if (path == FH3_HIP_PATH_GEMV8) {
+        FH3_HIPCALL(fh3k_gemv8(w->data, row_bytes, N, K, (const float *)prep, bias, d_y, n_tok, st));
+    } else if (path == FH3_HIP_PATH_SKINNY) {
         FH3_HIPCALL(fh3k_skinny(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, st));
     } else {
         FH3_HIPCALL(fh3k_gemm(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, st));
@@ -391,10 +404,16 @@ extern "C" int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, i
     if ((uintptr_t)d_x & 15u) return set_err(FH3_E_INVALID, "fh3_hip_matmul_dev: x must be 16-byte aligned");
     rc = ensure_init();
     if (rc != FH3_OK) return rc;
-    std::lock_guard<std::recursive_mutex> lk(g.mu);
     hipStream_t st = stream ? (hipStream_t)stream : g.stream;
+    const int path = choose_path(n_tok, w->in);
+    if (path == FH3_HIP_PATH_GEMV8) {  // no preparation and no workspace
+        FH3_HIPCALL(fh3k_gemv8(w->data, (int64_t)fh3_row_bytes(w->type, w->in), (int)w->out, (int)w->in, d_x,
+                               d_bias_or_null, d_y, n_tok, st));
+        return FH3_OK;
+    }
+    std::lock_guard<std::recursive_mutex> lk(g.mu);
     // the small-M kernel only reads round_up(n_tok, 32) prepared rows
-    const int64_t rows = choose_path(n_tok) == FH3_HIP_PATH_SKINNY ? round_up(n_tok, 32) : prep_rows(n_tok);
+    const int64_t rows = path == FH3_HIP_PATH_SKINNY ? round_up(n_tok, 32) : prep_rows(n_tok);
     rc = grow(g.ws, fh3_hip_prepared_bytes(n_tok, w->in));
     if (rc != FH3_OK) return rc;
     rc = prepare(d_x, n_tok, w->in, g.ws.p, rows, st);

@@ -37,6 +37,15 @@ hipError_t fh3k_skinny(const void *W, int64_t row_bytes, int N, int K, const voi
                        const float *xs_inv, const float *bias, float *y, int M, hipStream_t st);
 int fh3k_skinny_max_tokens(void);
 
+// y = x * W^T (+bias) for n_tok = M <= fh3k_gemv8_max_tokens() straight from
+// fp32 x[M][K] (16-byte aligned): activations quantised to int16 inside the
+// kernel, integer MFMA on the raw weights.  fh3k_gemv8_fits(K, M) says whether
+// the kernel takes this shape (its LDS grows with K * M).
+hipError_t fh3k_gemv8(const void *W, int64_t row_bytes, int N, int K, const float *x, const float *bias,
+                      float *y, int M, hipStream_t st);
+int fh3k_gemv8_max_tokens(void);
+int fh3k_gemv8_fits(int K, int M);
+
 // Largest in-dimension (K) the activation preparation handles.
 int fh3k_max_in(void);
 

@@ -560,6 +560,225 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) vo
 }
 
 // ---------------------------------------------------------------------------
+// One- and two-token kernel (k_gemv8): integer MFMA on the raw 4-bit weights,
+// activations quantised inside the kernel (no preparation launch).
+//
+// Activations.  Each wavefront quantises the fp32 activations of its own
+// window of super-blocks: x_q = rne(x * 2^e), e per (token, wavefront) so that
+// max|x| * 2^e lies in [2^13, 2^14), split as x_q = 256*hi + lo with hi, lo
+// signed bytes (two int8 planes).  x * 2^e + (1.5*2^23 + 128) puts
+// x_q + 128 in the low 16 bits of the fp32 result (round to nearest even):
+// byte 1 is hi, byte 0 xor 0x80 is lo.  Non-finite activations in a window make
+// that token's output NaN.
+//
+// Products.  v_mfma_i32_16x16x64_i8, B = 16 weight rows: lane (row r = l%16,
+// k-block qd = l/16) holds 8 bytes of chunk qd of row r as 16 nibbles, the low
+// nibbles (group 2qd) in bytes 0-7 and the high ones (group 2qd+1) in bytes
+// 8-15.  A = "group slots": A row i = (token i/8, group i%8) is non-zero only in
+// the k-block of its group and only in the half that holds that group, so
+// output row i collects sum_k q_k x_k over exactly one group (32 weights) of
+// one token, exact in int32.  Four MFMAs (one per 8-byte piece of the chunks)
+// cover a super-block; each runs on both activation planes, and on B = ones
+// for the group sums of x_q (the dmin*m term).  Per super-block, lane l holds
+// groups 4*((l/16)&1)+v (v = 0..3) of token l/32 for row r:
+//   T = sum_v sc_v * (256*S_hi + S_lo),  Mt = sum_v m_v * (256*X_hi + X_lo)
+// in 24-bit integer multiply-adds (|S| < 2^23, |T| < 2^31), then
+//   acc += d * T - dmin * Mt   in fp32,
+// the reference's w = (d*sc)*q - dmin*m with all integer parts exact.
+//
+// LDS record of (super-block, token, plane): 32 slots of 16 bytes, slot g*4+p
+// holding x_q[32g + 8p .. +7] in its low half (even g) or high half (odd g) and
+// zeros in the other half, then 4 zero slots for lanes whose A operand is zero;
+// every A operand is one ds_read_b128 with a compile-time offset.
+// Workgroup and window split as in k_skinny (NW wavefronts x C super-blocks
+// over 16 weight rows, last window moved inside the row, partial sums added in
+// wave order: deterministic).
+// ---------------------------------------------------------------------------
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int G8_REC = 576;        // bytes of one (super-block, token, plane) record
+constexpr int G8_MAX_TOKENS = 2;
+
+// Maximum over the wavefront (DPP within rows of 16, then row broadcasts),
+// read from lane 63.
+__device__ __forceinline__ float wave_max_f32(float v) {
+    int iv = __builtin_bit_cast(int, v);
+#define FH3_DPP_MAX(ctrl, rows)                                                                 \
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(iv, iv, ctrl, rows, 0xF, false))); \
+    iv = __builtin_bit_cast(int, v);
+    FH3_DPP_MAX(0xB1, 0xF)   // quad_perm [1,0,3,2]
+    FH3_DPP_MAX(0x4E, 0xF)   // quad_perm [2,3,0,1]
+    FH3_DPP_MAX(0x141, 0xF)  // row_half_mirror
+    FH3_DPP_MAX(0x140, 0xF)  // row_mirror
+    FH3_DPP_MAX(0x142, 0xA)  // row_bcast:15 into rows 1, 3
+    FH3_DPP_MAX(0x143, 0xC)  // row_bcast:31 into rows 2, 3
+#undef FH3_DPP_MAX
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 63));
+}
+
+template <int MT, int C, int RMAX = 4>
+__global__ __launch_bounds__(512) void k_gemv8(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int K,
+                                               const float *__restrict__ X, const float *__restrict__ bias,
+                                               float *__restrict__ Y, int M) {
+    constexpr int WAVE_LDS = C * MT * 2 * G8_REC;
+    constexpr int RING = C < RMAX ? C : RMAX;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
+    const int NW = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, qd = lane >> 4;
+    const int o0 = blockIdx.x * 16;
+    const int orow = o0 + r < N ? o0 + r : N - 1;
+    const int nsb = K >> 8;
+    const int own = wave * C;
+    const int s0 = own < nsb - C ? own : nsb - C;
+    const uint8_t *wh = W + (size_t)orow * row_bytes + (size_t)s0 * 144;
+    const uint8_t *wc = wh + 16 + 32 * qd;
+    uint8_t *my = lds8 + wave * WAVE_LDS;
+
+    // activations first: the quantisation waits only for them, not for the
+    // weights issued after them (loads of a wavefront complete in order)
+    f32x4 xv[MT][C];
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        if (t < M) {
+            const f32x4 *xr = reinterpret_cast<const f32x4 *>(X + (size_t)t * K + (size_t)s0 * 256) + lane;
+#pragma unroll
+            for (int i = 0; i < C; i++) xv[t][i] = xr[i * 64];
+        }
+    }
+    u32x4 hv[RING], ca[RING], cb[RING];
+#pragma unroll
+    for (int s = 0; s < RING; s++) {
+        hv[s] = ld16(wh + s * 144);
+        ca[s] = ld16(wc + s * 144);
+        cb[s] = ld16(wc + s * 144 + 16);
+    }
+
+    // quantise into the records: lane l holds k = 4l..4l+3 of a super-block,
+    // group l/8, piece (l%8)/2, bytes 4*(l&1).. of the slot half
+    const int pg = lane >> 3, pp = (lane & 7) >> 1;
+    const int wdat = (pg * 4 + pp) * 16 + (pg & 1) * 8 + 4 * (lane & 1);
+    const int wzero = (pg * 4 + pp) * 16 + (1 - (pg & 1)) * 8 + 4 * (lane & 1);
+    float inv[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        inv[t] = 0.f;
+        if (t < M) {
+            float mx = 0.f, chk = 0.f;
+#pragma unroll
+            for (int i = 0; i < C; i++) {
+                const f32x4 v = xv[t][i];
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+                chk = __builtin_fmaf((v.x + v.y) + (v.z + v.w), 0x1p-64f, chk);  // Inf/NaN survive
+            }
+            mx = wave_max_f32(mx);
+            const bool bad = __builtin_amdgcn_ballot_w64(!__builtin_isfinite(chk)) != 0;
+            int e = 0;
+            if (mx > 0.f) {
+                int E;
+                (void)frexpf(mx, &E);
+                e = 14 - E;
+                e = e > 126 ? 126 : (e < -126 ? -126 : e);
+            }
+            const float sc = ldexpf(1.0f, e);
+            inv[t] = bad ? __builtin_nanf("") : ldexpf(1.0f, -e);
+#pragma unroll
+            for (int i = 0; i < C; i++) {
+                const f32x4 v = xv[t][i];
+                const uint32_t v0 = __builtin_bit_cast(uint32_t, __builtin_fmaf(v.x, sc, 12583040.0f));
+                const uint32_t v1 = __builtin_bit_cast(uint32_t, __builtin_fmaf(v.y, sc, 12583040.0f));
+                const uint32_t v2 = __builtin_bit_cast(uint32_t, __builtin_fmaf(v.z, sc, 12583040.0f));
+                const uint32_t v3 = __builtin_bit_cast(uint32_t, __builtin_fmaf(v.w, sc, 12583040.0f));
+                const uint32_t p01 = __builtin_amdgcn_perm(v1, v0, 0x05040100u);  // v0.b0 v0.b1 v1.b0 v1.b1
+                const uint32_t p23 = __builtin_amdgcn_perm(v3, v2, 0x05040100u);
+                const uint32_t hi4 = __builtin_amdgcn_perm(p23, p01, 0x07050301u);
+                const uint32_t lo4 = __builtin_amdgcn_perm(p23, p01, 0x06040200u) ^ 0x80808080u;
+                uint8_t *rec = my + ((i * MT + t) * 2) * G8_REC;
+                *reinterpret_cast<uint32_t *>(rec + wdat) = hi4;
+                *reinterpret_cast<uint32_t *>(rec + wzero) = 0u;
+                *reinterpret_cast<uint32_t *>(rec + G8_REC + wdat) = lo4;
+                *reinterpret_cast<uint32_t *>(rec + G8_REC + wzero) = 0u;
+            }
+        }
+    }
+    for (int z = lane; z < C * MT * 2 * 4; z += 64)
+        *reinterpret_cast<u32x4 *>(my + (z >> 2) * G8_REC + 512 + 16 * (z & 3)) = u32x4{0u, 0u, 0u, 0u};
+    // the records are read back by other lanes of the same wavefront only:
+    // LDS operations of a wavefront execute in order
+    __builtin_amdgcn_wave_barrier();
+
+    // A operand of lane (row i = r: token r/8, group r%8; k-block qd): the
+    // group's slot when qd == g/2 and the token exists, else a zero slot
+    const int g = r & 7;
+    const bool dl = qd == (g >> 1) && (r >> 3) < MT;
+    const uint8_t *aop = my + (dl ? (r >> 3) * 2 * G8_REC + g * 64 : 512);
+    const int hh = qd & 1;
+    const uint32_t mA = hh ? 0x0F0F0F0Fu : 0x3F3F3F3Fu, mB = hh ? 0x30303030u : 0u;
+    const i32x4 ones = i32x4{0x01010101, 0x01010101, 0x01010101, 0x01010101};
+    float acc = 0.f;
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int i = 0; i < C; i++) {
+        const int s = i % RING;
+        const u32x4 h = hv[s];
+        const uint32_t cw[8] = {ca[s].x, ca[s].y, ca[s].z, ca[s].w, cb[s].x, cb[s].y, cb[s].z, cb[s].w};
+        i32x4 cwh = {0, 0, 0, 0}, cwl = cwh, coh = cwh, col = cwh;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint32_t u0 = cw[2 * p], u1 = cw[2 * p + 1];
+            const i32x4 b = i32x4{(int)(u0 & 0x0F0F0F0Fu), (int)(u1 & 0x0F0F0F0Fu), (int)((u0 >> 4) & 0x0F0F0F0Fu),
+                                  (int)((u1 >> 4) & 0x0F0F0F0Fu)};
+            const int im = i * MT * 2 * G8_REC + 16 * p;
+            const i32x4 ah = *reinterpret_cast<const i32x4 *>(aop + im);
+            const i32x4 al = *reinterpret_cast<const i32x4 *>(aop + im + G8_REC);
+            cwh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, cwh, 0, 0, 0);
+            cwl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, cwl, 0, 0, 0);
+            coh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, ones, coh, 0, 0, 0);
+            col = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, ones, col, 0, 0, 0);
+        }
+        // 6-bit scales and mins of groups 4hh..4hh+3 of row r, one per byte
+        // (reference src/core/fh3_quant.c:168-177)
+        const uint32_t sc4 = ((hh ? h.w : h.y) & mA) | ((h.y >> 2) & mB);
+        const uint32_t m4 = ((hh ? (h.w >> 4) : h.z) & mA) | ((h.z >> 2) & mB);
+        const bool valid = s0 + i >= own;
+        const float d = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xFFFFu)) : 0.f;
+        const float dmin = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x >> 16)) : 0.f;
+        int T = 0, Mt = 0;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int S = (cwh[v] << 8) + cwl[v];
+            const int Xs = (coh[v] << 8) + col[v];
+            T += (int)((sc4 >> (8 * v)) & 63u) * ((S << 8) >> 8);    // 24-bit multiply-add
+            Mt += (int)((m4 >> (8 * v)) & 63u) * ((Xs << 8) >> 8);
+        }
+        acc = __builtin_fmaf(d, (float)T, __builtin_fmaf(-dmin, (float)Mt, acc));
+        if (i + RING < C) {
+            hv[s] = ld16(wh + (i + RING) * 144);
+            ca[s] = ld16(wc + (i + RING) * 144);
+            cb[s] = ld16(wc + (i + RING) * 144 + 16);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // lanes l and l+16 hold the two group halves of (token l/32, row r)
+    float v = acc + __shfl_down(acc, 16);
+    v *= (lane >> 5) ? (MT > 1 ? inv[MT - 1] : 0.f) : inv[0];
+    float *red = reinterpret_cast<float *>(my);  // this wavefront's records are no longer read
+    red[lane] = v;
+    __syncthreads();
+    if (threadIdx.x < 32) {
+        const int tl = threadIdx.x >> 4, rr = threadIdx.x & 15;
+        const int l = tl * 32 + rr;
+        float sum = 0.f;
+        for (int w = 0; w < NW; w++) sum += reinterpret_cast<const float *>(lds8 + w * WAVE_LDS)[l];
+        const int o = o0 + rr;
+        if (tl < M && o < N) Y[(size_t)tl * N + o] = sum + (bias ? bias[o] : 0.f);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Large-M kernel.  Output tile 256 tokens x 128 weight rows, 4 wavefronts, each
 // owning 64 tokens x all 128 rows (2 x 4 tiles of 32x32, 128 fp32 accumulators
 // per lane).  Per K step s of 64 (one Q4_K chunk: groups 2c and 2c+1):
@@ -840,6 +1059,60 @@ extern "C" hipError_t fh3k_skinny(const void *W, int64_t row_bytes, int N, int K
 }
 
 extern "C" int fh3k_skinny_max_tokens(void) { return 64; }
+
+// k_gemv8: same window split as k_skinny; LDS = NW * C * MT * 2 records.
+static const size_t kGemv8MaxLds = 80u << 10;  // two workgroups per CU
+
+static size_t gemv8_lds(int K, int mt, int &C, int &NW) {
+    skinny_split(K / 256, C, NW);
+    return C ? (size_t)NW * C * mt * 2 * G8_REC : 0;
+}
+
+extern "C" int fh3k_gemv8_max_tokens(void) { return G8_MAX_TOKENS; }
+
+extern "C" int fh3k_gemv8_fits(int K, int M) {
+    int C, NW;
+    if (M < 1 || M > G8_MAX_TOKENS || K % 256) return 0;
+    const size_t lds = gemv8_lds(K, M, C, NW);
+    return lds > 0 && lds <= kGemv8MaxLds;
+}
+
+template <int MT, int C>
+static hipError_t launch_gemv8_c(const void *W, int64_t rb, int N, int K, const float *x, const float *bias,
+                                 float *y, int M, int NW, hipStream_t st) {
+    const size_t lds = (size_t)NW * C * MT * 2 * G8_REC;
+    hipLaunchKernelGGL((k_gemv8<MT, C>), dim3((unsigned)((N + 15) / 16)), dim3(NW * 64), lds, st,
+                       (const uint8_t *)W, rb, N, K, x, bias, y, M);
+    return hipGetLastError();
+}
+
+template <int MT>
+static hipError_t launch_gemv8(const void *W, int64_t rb, int N, int K, const float *x, const float *bias, float *y,
+                               int M, hipStream_t st) {
+    int C, NW;
+    gemv8_lds(K, MT, C, NW);
+    switch (C) {
+        case 1: return launch_gemv8_c<MT, 1>(W, rb, N, K, x, bias, y, M, NW, st);
+        case 2: return launch_gemv8_c<MT, 2>(W, rb, N, K, x, bias, y, M, NW, st);
+        case 3: return launch_gemv8_c<MT, 3>(W, rb, N, K, x, bias, y, M, NW, st);
+        case 4: return launch_gemv8_c<MT, 4>(W, rb, N, K, x, bias, y, M, NW, st);
+        case 5: return launch_gemv8_c<MT, 5>(W, rb, N, K, x, bias, y, M, NW, st);
+        case 6: return launch_gemv8_c<MT, 6>(W, rb, N, K, x, bias, y, M, NW, st);
+        case 7: return launch_gemv8_c<MT, 7>(W, rb, N, K, x, bias, y, M, NW, st);
+        case 8: return launch_gemv8_c<MT, 8>(W, rb, N, K, x, bias, y, M, NW, st);
+        case 10: return launch_gemv8_c<MT, 10>(W, rb, N, K, x, bias, y, M, NW, st);
+        case 13: return launch_gemv8_c<MT, 13>(W, rb, N, K, x, bias, y, M, NW, st);
+        case 16: return launch_gemv8_c<MT, 16>(W, rb, N, K, x, bias, y, M, NW, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+extern "C" hipError_t fh3k_gemv8(const void *W, int64_t row_bytes, int N, int K, const float *x, const float *bias,
+                                 float *y, int M, hipStream_t st) {
+    if (!fh3k_gemv8_fits(K, M)) return hipErrorInvalidValue;
+    return M == 1 ? launch_gemv8<1>(W, row_bytes, N, K, x, bias, y, M, st)
+                  : launch_gemv8<2>(W, row_bytes, N, K, x, bias, y, M, st);
+}
 
 extern "C" hipError_t fh3k_gemm(const void *W, int64_t row_bytes, int N, int K, const void *x16,
                                 const float *xs_inv, const float *bias, float *y, int M, hipStream_t st) {

@@ -31,7 +31,7 @@ FH3_E_NOT_FOUND = -6
 FH3_E_NOMEM = -7
 FH3_E_INVALID = -8
 
-PATH_AUTO, PATH_SKINNY, PATH_GEMM = 0, 1, 2
+PATH_AUTO, PATH_SKINNY, PATH_GEMM, PATH_GEMV8 = 0, 1, 2, 3
 
 Q4K_BLOCK_BYTES = 144
 Q4K_BLOCK_WEIGHTS = 256
@@ -151,7 +151,7 @@ SIGNATURES = {
     "fh3_hip_graph_destroy": (_c_int, [_c_void_p]),
     "fh3_hip_set_path": (_c_int, [_c_int]),
     "fh3_hip_skinny_max": (_c_int, []),
-    "fh3_hip_matmul_path": (_c_int, [_c_int]),
+    "fh3_hip_matmul_path": (_c_int, [_c_int, _c_i64]),
     # fh3_synth.h
     "fh3_philox4x32_10": (None, [_c_void_p, _c_void_p, _c_void_p]),
     "fh3_rng_uniform": (None, [_c_u64, _c_u64, _c_void_p, _c_size]),
@@ -268,8 +268,8 @@ def set_path(path):
     _check(lib().fh3_hip_set_path(path), "fh3_hip_set_path")
 
 
-def matmul_path(n_tok):
-    return lib().fh3_hip_matmul_path(n_tok)
+def matmul_path(n_tok, k):
+    return lib().fh3_hip_matmul_path(n_tok, k)
 
 
 class DeviceBuffer:

@@ -51,12 +51,15 @@ int fh3_hip_dequant_dev(int type, const void *d_src, float *d_dst, int64_t rows,
 /* Device-resident fh3_matmul: d_y[n_tok][w->out] = d_x[n_tok][w->in] * W^T
  * (+ d_bias).  w->data is a device pointer to the packed Q4_K rows (16-byte
  * aligned), w->in % 256 == 0.  Work is enqueued on `stream` and the call
- * returns without synchronising.  Activations are converted to fp16 with a
- * per-row power-of-two scale, weights are dequantised exactly in fp32 and
- * rounded once to fp16, products accumulate in fp32 on MFMA.  Deterministic:
- * no atomics, fixed reduction order.  Uses a library-owned workspace of
- * about n_tok * in * 2 bytes; calls that overlap on different streams race
- * on it. */
+ * returns without synchronising.  For one or two tokens (FH3_HIP_PATH_GEMV8
+ * below) activations are quantised to int16 inside the product kernel and
+ * weights enter an integer MFMA exactly; otherwise activations are converted to
+ * fp16 with a per-row power-of-two scale and weights enter an fp16 MFMA (exact
+ * sc*q for n_tok <= 64, dequantised in fp32 and rounded once to fp16 above),
+ * with fp32 accumulation.  Deterministic: no atomics, fixed reduction order.
+ * Non-finite activations give NaN outputs for that token on the GEMV8 path.
+ * Except on the GEMV8 path, uses a library-owned workspace of about
+ * n_tok * in * 2 bytes; calls that overlap on different streams race on it. */
 int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok,
                        const float *d_bias_or_null, void *stream);
 
@@ -68,7 +71,8 @@ int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok,
  *     per row);
  *   fh3_hip_prepare_x_dev: fill d_prep (16-byte aligned) from d_x[n_tok][in];
  *   fh3_hip_matmul_prepared_dev: the product from a prepared buffer; same
- *     results as fh3_hip_matmul_dev, no library workspace. */
+ *     results as fh3_hip_matmul_dev, no library workspace.  (For the
+ *     FH3_HIP_PATH_GEMV8 shapes the prepared form is a copy of x.) */
 size_t fh3_hip_prepared_bytes(int n_tok, int64_t in);
 int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, void *d_prep, void *stream);
 int fh3_hip_matmul_prepared_dev(const Fh3W *w, const void *d_prep, float *d_y, int n_tok,
@@ -84,17 +88,26 @@ int fh3_hip_graph_end(void *stream, void **graph_exec);
 int fh3_hip_graph_launch(void *graph_exec, void *stream);
 int fh3_hip_graph_destroy(void *graph_exec);
 
-/* Kernel selection for fh3_hip_matmul_dev: FH3_HIP_PATH_AUTO picks the
- * wavefront-per-row-block GEMV for n_tok <= fh3_hip_skinny_max() and the
- * LDS-staged MFMA GEMM above it; the other two force one kernel (tests). */
+/* Kernel selection for fh3_hip_matmul_dev: FH3_HIP_PATH_AUTO picks
+ *   - FH3_HIP_PATH_GEMV8 for n_tok <= 2 when its LDS fits (in <= 17920 for one
+ *     token, in <= 8960 for two): activations quantised to int16 (two int8
+ *     planes, one power-of-two scale per token and wavefront window) inside
+ *     the kernel, integer MFMA on the raw 4-bit weights, no preparation launch
+ *     and no workspace;
+ *   - FH3_HIP_PATH_SKINNY (fp16 activations, exact fp16 sc*q weights) for
+ *     n_tok <= fh3_hip_skinny_max();
+ *   - FH3_HIP_PATH_GEMM above.
+ * Setting a path forces it where it can take the shape (tests); prepare and
+ * product of the two-stage API must run under the same setting. */
 #define FH3_HIP_PATH_AUTO   0
 #define FH3_HIP_PATH_SKINNY 1
 #define FH3_HIP_PATH_GEMM   2
+#define FH3_HIP_PATH_GEMV8  3
 int fh3_hip_set_path(int path);
 int fh3_hip_skinny_max(void);
-/* The kernel family fh3_hip_matmul_dev would use for n_tok under the current
- * setting (FH3_HIP_PATH_SKINNY or FH3_HIP_PATH_GEMM). */
-int fh3_hip_matmul_path(int n_tok);
+/* The kernel family fh3_hip_matmul_dev would use for n_tok tokens of in
+ * inputs under the current setting. */
+int fh3_hip_matmul_path(int n_tok, int64_t in);
 
 #ifdef __cplusplus
 }

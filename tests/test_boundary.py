@@ -73,3 +73,26 @@ def test_row_bytes_matches_reference_build(fh3, ref):
     for t in (0, 1, 2, 3, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 30, 99):
         for n in (1, 31, 32, 255, 256, 5120, 13824):
             assert fh3.row_bytes(t, n) == ref.fh3_row_bytes(t, n), (t, n)
+
+
+def test_matmul_path_selection(fh3):
+    """Kernel family per shape (host-side decision, no GPU call): the int8
+    kernel takes one or two tokens while its LDS fits, the fp16 GEMV up to
+    64 tokens, the GEMM above; a forced path that cannot take a shape falls
+    back to the automatic choice."""
+    F = fh3
+    G8, SK, GM = F.PATH_GEMV8, F.PATH_SKINNY, F.PATH_GEMM
+    assert F.matmul_path(1, 5120) == G8 and F.matmul_path(2, 5120) == G8
+    assert F.matmul_path(1, 17920) == G8 and F.matmul_path(1, 18176) == SK
+    assert F.matmul_path(2, 8960) == G8 and F.matmul_path(2, 9216) == SK
+    assert F.matmul_path(3, 5120) == SK and F.matmul_path(64, 5120) == SK
+    assert F.matmul_path(65, 5120) == GM
+    try:
+        F.set_path(SK)
+        assert F.matmul_path(1, 5120) == SK
+        F.set_path(G8)
+        assert F.matmul_path(1, 5120) == G8 and F.matmul_path(3, 5120) == SK
+        F.set_path(GM)
+        assert F.matmul_path(1, 5120) == GM
+    finally:
+        F.set_path(F.PATH_AUTO)

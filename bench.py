@@ -43,8 +43,8 @@ METRIC = "Q4_K GEMM TFLOP/s + GEMV weight GB/s (% roofline); DiT block linear ms
 # FETCH_SIZE = 128 MiB and WRITE_SIZE = 256 MiB.  Summaries:
 # profiles/k_skinny_gemv_m1-16_k5120.md, profiles/k_gemm_dit_attention_m8192_k5120.md,
 # profiles/hbm_counters_copy_256MiB.md.  Re-measure when the kernels change.
-TRAFFIC_SKINNY_MEAN = 33767392      # mean over the six GEMV shapes (algorithmic mean 32899072)
-TRAFFIC_GEMM = {"attn_qkv": 2329190762, "attn_out": 782388133}
+TRAFFIC_GEMV_MEAN = 33597850        # mean over the six GEMV shapes (algorithmic mean 32899072)
+TRAFFIC_GEMM = {"attn_qkv": 2342595929, "attn_out": 781987460}
 
 
 def q4k_bytes(N, K):
@@ -332,9 +332,9 @@ def main():
         log("[bench] GEMV M=%d N=%d kernel %.2f us call %.2f us" % (c.M, c.N, t_k * 1e3, t_c * 1e3))
     achieved = k_bytes / (k_time * 1e-3)
     roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK, 4), "traffic": TRAFFIC_SKINNY_MEAN,
-                "traffic_over_algorithmic": round(TRAFFIC_SKINNY_MEAN / (k_bytes / len(gemv)), 3),
-                "kernel": "k_skinny (fh3_hip_matmul_prepared_dev, n_tok<=64)",
+                "frac": round(achieved / HBM_PEAK, 4), "traffic": TRAFFIC_GEMV_MEAN,
+                "traffic_over_algorithmic": round(TRAFFIC_GEMV_MEAN / (k_bytes / len(gemv)), 3),
+                "kernel": "k_gemv8 (n_tok<=2) and k_skinny (n_tok<=64), fh3_hip_matmul_prepared_dev",
                 "note": "algorithmic bytes N*K/256*144 + 4MK + 4MN per launch over the mean launch time "
                         "(graph of 64 back-to-back launches, rotating weight copies) of the six shapes"}
 

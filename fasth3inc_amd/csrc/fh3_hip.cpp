@@ -30,6 +30,8 @@ struct State {
     int device = -1;
     hipStream_t stream = nullptr;
     DevBuf ws;                      // x16 fragments + per-row scales
+    DevBuf ws2;                     // x16 made from a prepared fp32 copy (other weight types)
+    DevBuf w16;                     // fp16 rows of a weight of another type
     DevBuf st_w, st_x, st_y, st_b;  // staging for the host-pointer wrappers
     int path = FH3_HIP_PATH_AUTO;
     std::recursive_mutex mu;
@@ -193,7 +195,7 @@ extern "C" void fh3_hip_shutdown(void) {
     std::lock_guard<std::recursive_mutex> lk(g.mu);
     if (!g.init) return;
     (void)hipDeviceSynchronize();
-    DevBuf *bufs[] = {&g.ws, &g.st_w, &g.st_x, &g.st_y, &g.st_b};
+    DevBuf *bufs[] = {&g.ws, &g.ws2, &g.w16, &g.st_w, &g.st_x, &g.st_y, &g.st_b};
     for (DevBuf *b : bufs) {
         if (b->p) (void)hipFree(b->p);
         b->p = nullptr;
@@ -322,8 +324,8 @@ extern "C" int fh3_hip_dequant_dev(int type, const void *d_src, float *d_dst, in
 static int check_weights(const Fh3W *w, const char *fn) {
     if (!w || !w->data || w->in <= 0 || w->out <= 0)
         return set_err(FH3_E_INVALID, "%s: NULL weights or non-positive size", fn);
-    if (w->type != FH3_QUANT_Q4_K)
-        return set_err(FH3_E_INVALID, "%s: unsupported weight type %d (Q4_K only)", fn, w->type);
+    if (fh3k_dequant_block_len(w->type) == 0)
+        return set_err(FH3_E_INVALID, "%s: unsupported weight type %d", fn, w->type);
     if (w->in % 256)
         return set_err(FH3_E_INVALID, "%s: in=%lld is not a multiple of 256", fn, (long long)w->in);
     if (w->in > fh3k_max_in() || w->out > 0x7FFFFFFF)
@@ -367,7 +369,44 @@ extern "C" int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, vo
     return prepare(d_x, n_tok, in, d_prep, prep_rows(n_tok), stream ? (hipStream_t)stream : g.stream);
 }
 
+// Weights of another type than Q4_K: fp16 rows (the weight itself for F16,
+// else decoded into the library's w16 buffer), then k_skinny16 / k_gemm16.
+static int path16(int n_tok) {
+    if (g.path == FH3_HIP_PATH_GEMM) return FH3_HIP_PATH_GEMM;
+    return n_tok <= fh3k_skinny_max_tokens() ? FH3_HIP_PATH_SKINNY : FH3_HIP_PATH_GEMM;
+}
+
+static int product16(const Fh3W *w, const void *x16, const float *xs_inv, int n_tok, const float *bias, float *d_y,
+                     hipStream_t st) {
+    const int K = (int)w->in, N = (int)w->out;
+    const void *w16 = w->data;
+    if (w->type != FH3_QUANT_F16) {
+        int rc = grow(g.w16, (size_t)w->out * (size_t)w->in * 2);
+        if (rc != FH3_OK) return rc;
+        FH3_HIPCALL(fh3k_weights_f16(w->type, w->data, (int64_t)fh3_row_bytes(w->type, w->in), K, N, g.w16.p, st));
+        w16 = g.w16.p;
+    }
+    if (path16(n_tok) == FH3_HIP_PATH_SKINNY)
+        FH3_HIPCALL(fh3k_skinny16(w16, N, K, x16, xs_inv, bias, d_y, n_tok, st));
+    else
+        FH3_HIPCALL(fh3k_gemm16(w16, N, K, x16, xs_inv, bias, d_y, n_tok, st));
+    return FH3_OK;
+}
+
 static int product(const Fh3W *w, const void *prep, int n_tok, const float *bias, float *d_y, hipStream_t st) {
+    if (w->type != FH3_QUANT_Q4_K) {
+        std::lock_guard<std::recursive_mutex> lk(g.mu);
+        if (choose_path(n_tok, w->in) == FH3_HIP_PATH_GEMV8) {
+            // the prepared form is then a copy of x: make the fragments here
+            int rc = grow(g.ws2, fh3_hip_prepared_bytes(n_tok, w->in));
+            if (rc != FH3_OK) return rc;
+            float *xs = (float *)((char *)g.ws2.p + prep_scale_offset(n_tok, w->in));
+            FH3_HIPCALL(fh3k_xprep((const float *)prep, n_tok, (int)w->in, (int)prep_rows(n_tok), g.ws2.p, xs, st));
+            return product16(w, g.ws2.p, xs, n_tok, bias, d_y, st);
+        }
+        return product16(w, prep, (const float *)((const char *)prep + prep_scale_offset(n_tok, w->in)), n_tok,
+                         bias, d_y, st);
+    }
     const int K = (int)w->in, N = (int)w->out;
     const int64_t row_bytes = (int64_t)fh3_row_bytes(w->type, w->in);
     const float *xs_inv = (const float *)((const char *)prep + prep_scale_offset(n_tok, w->in));
@@ -405,6 +444,15 @@ extern "C" int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, i
     rc = ensure_init();
     if (rc != FH3_OK) return rc;
     hipStream_t st = stream ? (hipStream_t)stream : g.stream;
+    if (w->type != FH3_QUANT_Q4_K) {
+        std::lock_guard<std::recursive_mutex> lk(g.mu);
+        const int64_t rows = path16(n_tok) == FH3_HIP_PATH_SKINNY ? round_up(n_tok, 32) : prep_rows(n_tok);
+        rc = grow(g.ws, fh3_hip_prepared_bytes(n_tok, w->in));
+        if (rc != FH3_OK) return rc;
+        float *xs = (float *)((char *)g.ws.p + prep_scale_offset(n_tok, w->in));
+        FH3_HIPCALL(fh3k_xprep(d_x, n_tok, (int)w->in, (int)rows, g.ws.p, xs, st));
+        return product16(w, g.ws.p, xs, n_tok, d_bias_or_null, d_y, st);
+    }
     const int path = choose_path(n_tok, w->in);
     if (path == FH3_HIP_PATH_GEMV8) {  // no preparation and no workspace
         FH3_HIPCALL(fh3k_gemv8(w->data, (int64_t)fh3_row_bytes(w->type, w->in), (int)w->out, (int)w->in, d_x,
@@ -481,8 +529,8 @@ extern "C" void fh3_matmul(const Fh3W *w, const float *x, float *y, int n_tok, c
     if (!w || !x || !y || n_tok <= 0 || w->in <= 0 || w->out <= 0) return;
     int rc = ensure_init();
     if (rc != FH3_OK) { report("fh3_matmul", rc); return; }
-    if (w->type != FH3_QUANT_Q4_K || !w->data) {
-        set_err(FH3_E_INVALID, "fh3_matmul: unsupported weight type %d (Q4_K only)", w->type);
+    if (fh3k_dequant_block_len(w->type) == 0 || !w->data) {
+        set_err(FH3_E_INVALID, "fh3_matmul: unsupported weight type %d", w->type);
         report("fh3_matmul", FH3_E_INVALID);
         return;
     }

@@ -924,6 +924,221 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Weights of the other types (the reference's fh3_matmul takes every type its
+// fh3_dequant decodes, src/core/fh3_ops.c:325-333).  They are decoded once per
+// call to fp16 rows W16[N][K] -- the reference's fp32 value rounded once to
+// fp16, as k_gemm rounds Q4_K -- and multiplied by k_skinny16 / k_gemm16, which
+// read those rows directly.  F16 weights are used as they are.
+// ---------------------------------------------------------------------------
+template <int T>
+__global__ __launch_bounds__(256) void k_weights_f16_blocks(const uint8_t *__restrict__ src, int64_t row_bytes,
+                                                            int64_t nblk, int64_t rows, _Float16 *__restrict__ dst) {
+    constexpr int BL = Fmt<T>::BL, BB = Fmt<T>::BB, P = Fmt<T>::P;
+    const int64_t per_row = nblk * P;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= rows * per_row) return;
+    const int64_t row = gid / per_row;
+    const int64_t rem = gid - row * per_row;
+    const int64_t b = rem / P;
+    const int G = (int)(rem - b * P);
+    float o[16];
+    deq_piece<T>(src + row * row_bytes + b * BB, G, o);
+    half8 *out = reinterpret_cast<half8 *>(dst + row * nblk * BL + b * BL + 16 * G);
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        half8 h;
+#pragma unroll
+        for (int e = 0; e < 8; e++) h[e] = (_Float16)o[8 * j + e];
+        out[j] = h;
+    }
+}
+
+// F32 / BF16 rows -> fp16, 8 elements per thread (n % 8 == 0).
+template <bool BF>
+__global__ __launch_bounds__(256) void k_weights_f16_elem(const uint8_t *__restrict__ src, int64_t n8,
+                                                          _Float16 *__restrict__ dst) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= n8) return;
+    half8 h;
+    if (BF) {
+        const u32x4 v = reinterpret_cast<const u32x4 *>(src)[gid];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            h[2 * e] = (_Float16)__builtin_bit_cast(float, v[e] << 16);
+            h[2 * e + 1] = (_Float16)__builtin_bit_cast(float, v[e] & 0xFFFF0000u);
+        }
+    } else {
+        const f32x4 *s = reinterpret_cast<const f32x4 *>(src) + 2 * gid;
+        const f32x4 a = s[0], c = s[1];
+        h = half8{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+                  (_Float16)c.x, (_Float16)c.y, (_Float16)c.z, (_Float16)c.w};
+    }
+    reinterpret_cast<half8 *>(dst)[gid] = h;
+}
+
+// Small M on fp16 rows: the k_skinny work split (NW wavefronts x C windows of
+// 256 k over 16 rows, last window moved inside the row, padding windows
+// skipped), B = 8 fp16 weights of row l%16 at k offset 8*(l/16) of a 32-k
+// window, loaded straight from W16; A = the same k of the X16 fragments.
+// Deterministic: wave partials added in order through LDS.
+template <int TB, int C>
+__global__ __launch_bounds__(512) void k_skinny16(const _Float16 *__restrict__ W16, int N, int K,
+                                                  const half8 *__restrict__ X16, const float *__restrict__ xs_inv,
+                                                  const float *__restrict__ bias, float *__restrict__ Y, int M) {
+    extern __shared__ f32x4 red[];  // [NW][TB][64]
+    const int NW = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = lane & 15, q = lane >> 4;
+    const int o0 = blockIdx.x * 16;
+    const int orow = o0 + j < N ? o0 + j : N - 1;
+    const int nsb = K / 256;
+    const int kf_n = K / 16;
+    const int own = wave * C;
+    const int s0 = own < nsb - C ? own : nsb - C;
+    const half8 *wr = reinterpret_cast<const half8 *>(W16 + (size_t)orow * K + (size_t)s0 * 256) + q;
+    const half8 *xq[TB];
+    f32x4 acc[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++) {
+        acc[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        int t = tb * 16 + j;
+        t = t < M ? t : M - 1;
+        // window m of super-block i: k = 32m + 8q -> fragment 2m + q/2, half q&1
+        xq[tb] = X16 + ((size_t)(t >> 5) * kf_n + (size_t)s0 * 16 + (q >> 1)) * 64 + (t & 31) + 32 * (q & 1);
+    }
+    // weights one window ahead; activations one window ahead for one token
+    // block, loaded at the start of the window otherwise (register budget)
+    constexpr int AB = TB == 1 ? 2 : 1;
+    half8 b[2][8], a[AB][8][TB];
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        b[0][m] = wr[4 * m];
+#pragma unroll
+        for (int tb = 0; tb < TB; tb++) a[0][m][tb] = xq[tb][(2 * m) * 64];
+    }
+#pragma unroll
+    for (int i = 0; i < C; i++) {
+        const int cur = i & 1, ac = AB == 2 ? cur : 0;
+        if (i + 1 < C) {
+#pragma unroll
+            for (int m = 0; m < 8; m++) {
+                b[cur ^ 1][m] = wr[(i + 1) * 32 + 4 * m];
+                if (AB == 2) {
+#pragma unroll
+                    for (int tb = 0; tb < TB; tb++) a[ac ^ 1][m][tb] = xq[tb][((i + 1) * 16 + 2 * m) * 64];
+                }
+            }
+        }
+        if (AB == 1 && i > 0) {
+#pragma unroll
+            for (int m = 0; m < 8; m++)
+#pragma unroll
+                for (int tb = 0; tb < TB; tb++) a[0][m][tb] = xq[tb][(i * 16 + 2 * m) * 64];
+        }
+        if (s0 + i >= own) {
+#pragma unroll
+            for (int m = 0; m < 8; m++)
+#pragma unroll
+                for (int tb = 0; tb < TB; tb++)
+                    acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ac][m][tb], b[cur][m], acc[tb], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++) red[(wave * TB + tb) * 64 + lane] = acc[tb];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < TB * 64; idx += blockDim.x) {
+        const int tb = idx >> 6, l = idx & 63;
+        f32x4 s = red[tb * 64 + l];
+        for (int w = 1; w < NW; w++) s += red[(w * TB + tb) * 64 + l];
+        const int o = o0 + (l & 15);
+        if (o < N) {
+            const float bo = bias ? bias[o] : 0.f;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int t = tb * 16 + 4 * (l >> 4) + v;
+                if (t < M) Y[(size_t)t * N + o] = s[v] * xs_inv[t] + bo;
+            }
+        }
+    }
+}
+
+// Large M on fp16 rows: the k_gemm tile (256 tokens x 128 rows, 4 wavefronts
+// of 64 tokens, v_mfma_f32_32x32x16_f16) with the B fragments copied from W16
+// instead of dequantised: per K step of 64, thread (r, h) moves k 16h..16h+15
+// and 32+16h..32+16h+15 of row r into the same LDS fragment slots k_gemm's
+// dequantisation writes.  Next step's rows and activations are loaded during
+// the current step's MFMAs; one barrier per step.
+__global__ __launch_bounds__(256, 2) void k_gemm16(const _Float16 *__restrict__ W16, int N, int K,
+                                                   const half8 *__restrict__ X16, const float *__restrict__ xs_inv,
+                                                   const float *__restrict__ bias, float *__restrict__ Y, int M,
+                                                   int m_tiles, int n_tiles) {
+    __shared__ half8 lds[2][16][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int total = m_tiles * n_tiles;
+    const int id = blockIdx.x;
+    const int per = total >> 3;
+    const int L = (id < per * 8) ? (id & 7) * per + (id >> 3) : id;
+    const int mt = L / n_tiles, nt = L - mt * n_tiles;
+    const int m0 = mt * GEMM_BM, n0 = nt * GEMM_BN;
+    const int r = tid & 127, h = tid >> 7;
+    int orow = n0 + r;
+    orow = orow < N ? orow : N - 1;
+    const half8 *wrow = reinterpret_cast<const half8 *>(W16 + (size_t)orow * K) + 2 * h;
+    const int wf = (r >> 5) * 4, wl = r & 31;
+    const int kf_n = K / 16;
+    const half8 *xa0 = X16 + ((size_t)(m0 / 32 + 2 * wave) * kf_n) * 64 + lane;
+    const half8 *xa1 = xa0 + (size_t)kf_n * 64;
+    const int S = K / 64;
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[a][c] = f32x16{};
+    half8 wb[4], xc[2][4], xn[2][4];
+    // step s of row r: half8 index 8s + 2h + {0, 1} (k 16h..) and 8s + 4 + 2h + {0, 1} (k 32+16h..)
+    wb[0] = wrow[0], wb[1] = wrow[1], wb[2] = wrow[4], wb[3] = wrow[5];
+    gemm_load_x(xa0, xa1, 0, xc);
+    lds[0][wf + h][wl] = wb[0], lds[0][wf + h][wl + 32] = wb[1];
+    lds[0][wf + 2 + h][wl] = wb[2], lds[0][wf + 2 + h][wl + 32] = wb[3];
+    __syncthreads();
+    for (int s = 0; s < S; s++) {
+        const int cur = s & 1;
+        const bool more = s + 1 < S;
+        if (more) {
+            const half8 *p = wrow + 8 * (s + 1);
+            wb[0] = p[0], wb[1] = p[1], wb[2] = p[4], wb[3] = p[5];
+            gemm_load_x(xa0, xa1, s + 1, xn);
+        }
+        gemm_mfma(lds[cur], lane, xc, acc);
+        if (more) {
+            lds[cur ^ 1][wf + h][wl] = wb[0], lds[cur ^ 1][wf + h][wl + 32] = wb[1];
+            lds[cur ^ 1][wf + 2 + h][wl] = wb[2], lds[cur ^ 1][wf + 2 + h][wl + 32] = wb[3];
+#pragma unroll
+            for (int a = 0; a < 2; a++)
+#pragma unroll
+                for (int k = 0; k < 4; k++) xc[a][k] = xn[a][k];
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int tb = 0; tb < 2; tb++) {
+        const int tbase = m0 + 64 * wave + 32 * tb + 4 * (lane >> 5);
+#pragma unroll
+        for (int ob = 0; ob < 4; ob++) {
+            const int o = n0 + 32 * ob + (lane & 31);
+            if (o >= N) continue;
+            const float bo = bias ? bias[o] : 0.f;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int t = tbase + 8 * (v >> 2) + (v & 3);
+                if (t < M) Y[(size_t)t * N + o] = acc[tb][ob][v] * xs_inv[t] + bo;
+            }
+        }
+    }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -1125,3 +1340,94 @@ extern "C" hipError_t fh3k_gemm(const void *W, int64_t row_bytes, int N, int K, 
 }
 
 extern "C" int fh3k_gemm_row_pad(void) { return GEMM_BM; }
+
+// ---------------------------------------------------------------------------
+// Other weight types: decode to fp16 rows, then k_skinny16 / k_gemm16
+// ---------------------------------------------------------------------------
+template <int T>
+static hipError_t launch_weights_f16_blocks(const void *src, int64_t row_bytes, int64_t n, int64_t rows,
+                                            void *dst, hipStream_t st) {
+    const int64_t nblk = n / Fmt<T>::BL;
+    const int64_t blocks = (rows * nblk * Fmt<T>::P + 255) / 256;
+    if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_weights_f16_blocks<T>, dim3((unsigned)blocks), dim3(256), 0, st, (const uint8_t *)src,
+                       row_bytes, nblk, rows, (_Float16 *)dst);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t fh3k_weights_f16(int type, const void *src, int64_t row_bytes, int K, int N, void *dst,
+                                       hipStream_t st) {
+    const int bl = fh3k_dequant_block_len(type);
+    if (bl == 0 || K <= 0 || N <= 0 || K % 256) return hipErrorInvalidValue;
+    if (type == FH3K_F16)
+        return hipMemcpyAsync(dst, src, (size_t)N * K * 2, hipMemcpyDeviceToDevice, st);
+    if (type == FH3K_F32 || type == FH3K_BF16) {
+        const int64_t n8 = (int64_t)N * K / 8, blocks = (n8 + 255) / 256;
+        if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
+        if (type == FH3K_BF16)
+            hipLaunchKernelGGL(k_weights_f16_elem<true>, dim3((unsigned)blocks), dim3(256), 0, st,
+                               (const uint8_t *)src, n8, (_Float16 *)dst);
+        else
+            hipLaunchKernelGGL(k_weights_f16_elem<false>, dim3((unsigned)blocks), dim3(256), 0, st,
+                               (const uint8_t *)src, n8, (_Float16 *)dst);
+        return hipGetLastError();
+    }
+    switch (type) {
+        case FH3K_Q8_0: return launch_weights_f16_blocks<FH3K_Q8_0>(src, row_bytes, K, N, dst, st);
+        case FH3K_Q2_K: return launch_weights_f16_blocks<FH3K_Q2_K>(src, row_bytes, K, N, dst, st);
+        case FH3K_Q3_K: return launch_weights_f16_blocks<FH3K_Q3_K>(src, row_bytes, K, N, dst, st);
+        case FH3K_Q4_K: return launch_weights_f16_blocks<FH3K_Q4_K>(src, row_bytes, K, N, dst, st);
+        case FH3K_Q5_K: return launch_weights_f16_blocks<FH3K_Q5_K>(src, row_bytes, K, N, dst, st);
+        default: return launch_weights_f16_blocks<FH3K_Q6_K>(src, row_bytes, K, N, dst, st);
+    }
+}
+
+template <int TB, int C>
+static hipError_t launch_skinny16_c(const void *W16, int N, int K, const void *x16, const float *xs_inv,
+                                    const float *bias, float *y, int M, int NW, hipStream_t st) {
+    const size_t lds = (size_t)NW * TB * 64 * sizeof(f32x4);
+    hipLaunchKernelGGL((k_skinny16<TB, C>), dim3((unsigned)((N + 15) / 16)), dim3(NW * 64), lds, st,
+                       (const _Float16 *)W16, N, K, (const half8 *)x16, xs_inv, bias, y, M);
+    return hipGetLastError();
+}
+
+template <int TB>
+static hipError_t launch_skinny16(const void *W16, int N, int K, const void *x16, const float *xs_inv,
+                                  const float *bias, float *y, int M, hipStream_t st) {
+    int C, NW;
+    skinny_split(K / 256, C, NW);
+    switch (C) {
+        case 1: return launch_skinny16_c<TB, 1>(W16, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 2: return launch_skinny16_c<TB, 2>(W16, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 3: return launch_skinny16_c<TB, 3>(W16, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 4: return launch_skinny16_c<TB, 4>(W16, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 5: return launch_skinny16_c<TB, 5>(W16, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 6: return launch_skinny16_c<TB, 6>(W16, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 7: return launch_skinny16_c<TB, 7>(W16, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 8: return launch_skinny16_c<TB, 8>(W16, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 10: return launch_skinny16_c<TB, 10>(W16, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 13: return launch_skinny16_c<TB, 13>(W16, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 16: return launch_skinny16_c<TB, 16>(W16, N, K, x16, xs_inv, bias, y, M, NW, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+extern "C" hipError_t fh3k_skinny16(const void *W16, int N, int K, const void *x16, const float *xs_inv,
+                                    const float *bias, float *y, int M, hipStream_t st) {
+    switch ((M + 15) / 16) {
+        case 1: return launch_skinny16<1>(W16, N, K, x16, xs_inv, bias, y, M, st);
+        case 2: return launch_skinny16<2>(W16, N, K, x16, xs_inv, bias, y, M, st);
+        case 3: return launch_skinny16<3>(W16, N, K, x16, xs_inv, bias, y, M, st);
+        case 4: return launch_skinny16<4>(W16, N, K, x16, xs_inv, bias, y, M, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+extern "C" hipError_t fh3k_gemm16(const void *W16, int N, int K, const void *x16, const float *xs_inv,
+                                  const float *bias, float *y, int M, hipStream_t st) {
+    const int m_tiles = (M + GEMM_BM - 1) / GEMM_BM;
+    const int n_tiles = (N + GEMM_BN - 1) / GEMM_BN;
+    hipLaunchKernelGGL(k_gemm16, dim3((unsigned)(m_tiles * n_tiles)), dim3(256), 0, st, (const _Float16 *)W16, N, K,
+                       (const half8 *)x16, xs_inv, bias, y, M, m_tiles, n_tiles);
+    return hipGetLastError();
+}

@@ -88,10 +88,13 @@ void fh3_dequant(int type, const void *src, float *dst, int64_t n);
 
 /* y[n_tok][out] = x[n_tok][in] * W^T (+ bias[out]) on host buffers, computed
  * on the GPU (inputs are copied in and y out on every call).  NULL pointers or
- * non-positive sizes are a silent no-op, as in the reference.  Q4_K only, with
- * in % 256 == 0.  Results are deterministic run to run; they match the CPU
- * path within rel-Frobenius 2e-3 (fp16 operands, fp32 accumulation).
- * Replaces src/core/fh3_ops.c:317-404. */
+ * non-positive sizes are a silent no-op, as in the reference.  Weight types:
+ * every type fh3_dequant decodes (Q4_K on its own kernels; F32, F16, BF16,
+ * Q8_0, Q2_K, Q3_K, Q5_K, Q6_K decoded per call to fp16 rows), in % 256 == 0;
+ * other types print "unsupported" and leave y unwritten.  Results are
+ * deterministic run to run; they match the CPU path within rel-Frobenius 2e-3
+ * (fp16 or int16 operands, fp32 accumulation).  Replaces
+ * src/core/fh3_ops.c:317-404. */
 void fh3_matmul(const Fh3W *w, const float *x, float *y, int n_tok, const float *bias_or_null);
 
 /* The reference's single-thread variants (src/core/fh3_ops.c:210-315) are

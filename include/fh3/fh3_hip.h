@@ -49,8 +49,12 @@ int fh3_hip_dequant_dev(int type, const void *d_src, float *d_dst, int64_t rows,
                         void *stream);
 
 /* Device-resident fh3_matmul: d_y[n_tok][w->out] = d_x[n_tok][w->in] * W^T
- * (+ d_bias).  w->data is a device pointer to the packed Q4_K rows (16-byte
- * aligned), w->in % 256 == 0.  Work is enqueued on `stream` and the call
+ * (+ d_bias).  w->data is a device pointer to the packed rows (16-byte
+ * aligned), w->in % 256 == 0.  Q4_K runs the kernels described here; the
+ * other types fh3_dequant decodes are first decoded to fp16 rows (the exact
+ * value rounded once; F16 used as it is) into a library buffer of
+ * out * in * 2 bytes, then multiplied with the same activation handling and
+ * fp32 accumulation.  Work is enqueued on `stream` and the call
  * returns without synchronising.  For one or two tokens (FH3_HIP_PATH_GEMV8
  * below) activations are quantised to int16 inside the product kernel and
  * weights enter an integer MFMA exactly; otherwise activations are converted to

@@ -203,7 +203,7 @@ def test_matmul_dev_rejects_bad_arguments(gpu):
     dx = F.DeviceBuffer(4 * 256)
     dy = F.DeviceBuffer(4 * 16)
     with pytest.raises(F.Fh3Error) as e:
-        F.matmul_dev(dw, 256, 16, dx, dy, 1, qtype=F.FH3_QUANT_Q6_K)
+        F.matmul_dev(dw, 256, 16, dx, dy, 1, qtype=2)   # Q4_0: no decoder in the reference
     assert e.value.code == F.FH3_E_INVALID
     with pytest.raises(F.Fh3Error):
         F.matmul_dev(dw, 200, 16, dx, dy, 1)          # in % 256 != 0

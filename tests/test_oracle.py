@@ -224,3 +224,20 @@ def test_matmul_exact_integers(oracle):
     bias = rng.integers(-9, 10, N).astype(np.float32)
     y = H.oracle_matmul(oracle, raw, K, N, x.astype(np.float32), bias)
     assert np.array_equal(y, (x @ wint.T + bias).astype(np.float32))
+
+
+@pytest.mark.parametrize("name", ["F16", "BF16", "Q8_0", "Q2_K", "Q3_K", "Q5_K", "Q6_K"])
+def test_matmul_other_types_bitwise_vs_reference_build(oracle, ref, name):
+    """src/core/fh3_ops.c:317-404 decodes any type through fh3_dequant; the
+    oracle's product must match the reference build bit for bit for each."""
+    t = H.QTYPES[name][0]
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    K, N, M = 512, 70, 5
+    raw = H.random_blocks(rng, name, N, K, scale_lo=-12, scale_hi=-8)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    for b in (None, bias):
+        yo = H.matmul_with(oracle, "fh3_oracle_matmul", raw, K, N, x, b, qtype=t)
+        yr = H.matmul_with(ref, "fh3_matmul", raw, K, N, x, b, qtype=t)
+        assert np.isfinite(yo).all()
+        assert np.array_equal(yo.view(np.uint32), yr.view(np.uint32))

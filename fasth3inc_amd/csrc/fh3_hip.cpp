@@ -393,7 +393,8 @@ static int product16(const Fh3W *w, const void *x16, const float *xs_inv, int n_
     return FH3_OK;
 }
 
-static int product(const Fh3W *w, const void *prep, int n_tok, const float *bias, float *d_y, hipStream_t st) {
+static int product(const Fh3W *w, const void *prep, int n_tok, const float *bias, float *d_y, hipStream_t st,
+                   int epi = FH3_EPI_NONE, const float *aux = nullptr) {
     if (w->type != FH3_QUANT_Q4_K) {
         std::lock_guard<std::recursive_mutex> lk(g.mu);
         if (choose_path(n_tok, w->in) == FH3_HIP_PATH_GEMV8) {
@@ -412,11 +413,11 @@ static int product(const Fh3W *w, const void *prep, int n_tok, const float *bias
     const float *xs_inv = (const float *)((const char *)prep + prep_scale_offset(n_tok, w->in));
     const int path = choose_path(n_tok, w->in);
     if (path == FH3_HIP_PATH_GEMV8) {
-        FH3_HIPCALL(fh3k_gemv8(w->data, row_bytes, N, K, (const float *)prep, bias, d_y, n_tok, st));
+        FH3_HIPCALL(fh3k_gemv8_epi(w->data, row_bytes, N, K, (const float *)prep, bias, d_y, n_tok, epi, aux, st));
     } else if (path == FH3_HIP_PATH_SKINNY) {
-        FH3_HIPCALL(fh3k_skinny(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, st));
+        FH3_HIPCALL(fh3k_skinny_epi(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, epi, aux, st));
     } else {
-        FH3_HIPCALL(fh3k_gemm(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, st));
+        FH3_HIPCALL(fh3k_gemm_epi(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, epi, aux, st));
     }
     return FH3_OK;
 }
@@ -434,13 +435,26 @@ extern "C" int fh3_hip_matmul_prepared_dev(const Fh3W *w, const void *d_prep, fl
     return product(w, d_prep, n_tok, d_bias_or_null, d_y, stream ? (hipStream_t)stream : g.stream);
 }
 
-extern "C" int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok,
-                                  const float *d_bias_or_null, void *stream) {
-    int rc = check_weights(w, "fh3_hip_matmul_dev");
+// Epilogue arguments: Q4_K weights only; SwiGLU needs out % 128 == 0 (val and
+// gate halves of whole 64-row tiles); the gate-residual epilogue needs aux.
+static int check_epi(const Fh3W *w, int epi, const float *aux, const char *fn) {
+    if (epi == FH3_EPI_NONE) return FH3_OK;
+    if (epi != FH3_EPI_GATE_RESIDUAL && epi != FH3_EPI_SWIGLU) return set_err(FH3_E_INVALID, "%s: bad epilogue %d", fn, epi);
+    if (w->type != FH3_QUANT_Q4_K) return set_err(FH3_E_INVALID, "%s: fused epilogues take Q4_K weights", fn);
+    if (epi == FH3_EPI_SWIGLU && w->out % 128)
+        return set_err(FH3_E_INVALID, "%s: SwiGLU needs out %% 128 == 0 (out=%lld)", fn, (long long)w->out);
+    if (epi == FH3_EPI_GATE_RESIDUAL && !aux) return set_err(FH3_E_INVALID, "%s: gate-residual needs the gate", fn);
+    return FH3_OK;
+}
+
+static int matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok, const float *d_bias_or_null,
+                      void *stream, int epi, const float *aux, const char *fn) {
+    int rc = check_weights(w, fn);
     if (rc != FH3_OK) return rc;
+    if ((rc = check_epi(w, epi, aux, fn)) != FH3_OK) return rc;
     if (!d_x || !d_y || n_tok <= 0)
-        return set_err(FH3_E_INVALID, "fh3_hip_matmul_dev: NULL pointer or n_tok <= 0");
-    if ((uintptr_t)d_x & 15u) return set_err(FH3_E_INVALID, "fh3_hip_matmul_dev: x must be 16-byte aligned");
+        return set_err(FH3_E_INVALID, "%s: NULL pointer or n_tok <= 0", fn);
+    if ((uintptr_t)d_x & 15u) return set_err(FH3_E_INVALID, "%s: x must be 16-byte aligned", fn);
     rc = ensure_init();
     if (rc != FH3_OK) return rc;
     hipStream_t st = stream ? (hipStream_t)stream : g.stream;
@@ -455,8 +469,8 @@ extern "C" int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, i
     }
     const int path = choose_path(n_tok, w->in);
     if (path == FH3_HIP_PATH_GEMV8) {  // no preparation and no workspace
-        FH3_HIPCALL(fh3k_gemv8(w->data, (int64_t)fh3_row_bytes(w->type, w->in), (int)w->out, (int)w->in, d_x,
-                               d_bias_or_null, d_y, n_tok, st));
+        FH3_HIPCALL(fh3k_gemv8_epi(w->data, (int64_t)fh3_row_bytes(w->type, w->in), (int)w->out, (int)w->in, d_x,
+                                   d_bias_or_null, d_y, n_tok, epi, aux, st));
         return FH3_OK;
     }
     std::lock_guard<std::recursive_mutex> lk(g.mu);
@@ -466,7 +480,69 @@ extern "C" int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, i
     if (rc != FH3_OK) return rc;
     rc = prepare(d_x, n_tok, w->in, g.ws.p, rows, st);
     if (rc != FH3_OK) return rc;
-    return product(w, g.ws.p, n_tok, d_bias_or_null, d_y, st);
+    return product(w, g.ws.p, n_tok, d_bias_or_null, d_y, st, epi, aux);
+}
+
+extern "C" int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok,
+                                  const float *d_bias_or_null, void *stream) {
+    return matmul_dev(w, d_x, d_y, n_tok, d_bias_or_null, stream, FH3_EPI_NONE, nullptr, "fh3_hip_matmul_dev");
+}
+
+extern "C" int fh3_hip_matmul_epi_dev(const Fh3W *w, const float *d_x, int n_tok, const float *d_bias_or_null,
+                                      int epi, const float *d_aux, float *d_out, void *stream) {
+    return matmul_dev(w, d_x, d_out, n_tok, d_bias_or_null, stream, epi, d_aux, "fh3_hip_matmul_epi_dev");
+}
+
+extern "C" int fh3_hip_matmul_prepared_epi_dev(const Fh3W *w, const void *d_prep, int n_tok,
+                                               const float *d_bias_or_null, int epi, const float *d_aux,
+                                               float *d_out, void *stream) {
+    const char *fn = "fh3_hip_matmul_prepared_epi_dev";
+    int rc = check_weights(w, fn);
+    if (rc != FH3_OK) return rc;
+    if ((rc = check_epi(w, epi, d_aux, fn)) != FH3_OK) return rc;
+    if (!d_prep || !d_out || n_tok <= 0) return set_err(FH3_E_INVALID, "%s: NULL pointer or n_tok <= 0", fn);
+    if ((uintptr_t)d_prep & 15u) return set_err(FH3_E_INVALID, "%s: prepared buffer must be 16-byte aligned", fn);
+    rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    return product(w, d_prep, n_tok, d_bias_or_null, d_out, stream ? (hipStream_t)stream : g.stream, epi, d_aux);
+}
+
+extern "C" int fh3_hip_prepare_x_norm_dev(const float *d_x, int n_tok, int64_t in, const float *d_norm_w, float eps,
+                                          const float *d_shift, const float *d_scale, void *d_prep, void *stream) {
+    const char *fn = "fh3_hip_prepare_x_norm_dev";
+    if (!d_x || !d_prep || !d_norm_w || n_tok <= 0 || in <= 0 || in % 256 || in > fh3k_max_in() ||
+        (d_shift == nullptr) != (d_scale == nullptr))
+        return set_err(FH3_E_INVALID, "%s: bad arguments", fn);
+    if (((uintptr_t)d_x & 15u) || ((uintptr_t)d_prep & 15u) || ((uintptr_t)d_norm_w & 15u) ||
+        ((uintptr_t)d_shift & 15u) || ((uintptr_t)d_scale & 15u))
+        return set_err(FH3_E_INVALID, "%s: pointers must be 16-byte aligned", fn);
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    hipStream_t st = stream ? (hipStream_t)stream : g.stream;
+    if (choose_path(n_tok, in) == FH3_HIP_PATH_GEMV8) {  // prepared form: the normalised fp32 rows
+        FH3_HIPCALL(fh3k_rownorm_f32(d_x, n_tok, (int)in, (float *)d_prep, d_norm_w, eps, d_shift, d_scale, st));
+        return FH3_OK;
+    }
+    float *xs_inv = (float *)((char *)d_prep + prep_scale_offset(n_tok, in));
+    FH3_HIPCALL(fh3k_xprep_norm(d_x, n_tok, (int)in, (int)prep_rows(n_tok), d_prep, xs_inv, d_norm_w, eps, d_shift,
+                                d_scale, st));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_rownorm_dev(const float *d_x, int n_tok, int64_t in, const float *d_norm_w, float eps,
+                                   const float *d_shift, const float *d_scale, float *d_y, void *stream) {
+    const char *fn = "fh3_hip_rownorm_dev";
+    if (!d_x || !d_y || !d_norm_w || n_tok <= 0 || in <= 0 || in % 4 || in > fh3k_max_in() ||
+        (d_shift == nullptr) != (d_scale == nullptr))
+        return set_err(FH3_E_INVALID, "%s: bad arguments", fn);
+    if (((uintptr_t)d_x & 15u) || ((uintptr_t)d_y & 15u) || ((uintptr_t)d_norm_w & 15u) ||
+        ((uintptr_t)d_shift & 15u) || ((uintptr_t)d_scale & 15u))
+        return set_err(FH3_E_INVALID, "%s: pointers must be 16-byte aligned", fn);
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    FH3_HIPCALL(fh3k_rownorm_f32(d_x, n_tok, (int)in, d_y, d_norm_w, eps, d_shift, d_scale,
+                                 stream ? (hipStream_t)stream : g.stream));
+    return FH3_OK;
 }
 
 // ---------------------------------------------------------------------------

@@ -55,6 +55,24 @@ hipError_t fh3k_skinny16(const void *W16, int N, int K, const void *x16, const f
 hipError_t fh3k_gemm16(const void *W16, int N, int K, const void *x16, const float *xs_inv, const float *bias,
                        float *y, int M, hipStream_t st);
 
+// Product epilogues (EPI_* of fh3_kernels.hip; FH3_EPI_* of fh3_hip.h): 0 plain
+// store, 1 y[t][o] += aux[t][o] * product (gate residual), 2 SwiGLU (weight of
+// 2F rows [val | gate], y of width F; N % 128 == 0 for the GEMM, % 16 below).
+hipError_t fh3k_skinny_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16, const float *xs_inv,
+                           const float *bias, float *y, int M, int epi, const float *aux, hipStream_t st);
+hipError_t fh3k_gemv8_epi(const void *W, int64_t row_bytes, int N, int K, const float *x, const float *bias,
+                          float *y, int M, int epi, const float *aux, hipStream_t st);
+hipError_t fh3k_gemm_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16, const float *xs_inv,
+                         const float *bias, float *y, int M, int epi, const float *aux, hipStream_t st);
+
+// fh3k_xprep with the rows first normalised: rmsnorm with weight norm_w and
+// eps, then (shift and scale both set, [M][K]) AdaLN modulate.
+hipError_t fh3k_xprep_norm(const float *x, int M, int K, int Mpad, void *x16, float *xs_inv, const float *norm_w,
+                           float eps, const float *shift, const float *scale, hipStream_t st);
+// The same normalisation into fp32 rows y[M][K] (y may alias x).
+hipError_t fh3k_rownorm_f32(const float *x, int M, int K, float *y, const float *norm_w, float eps,
+                            const float *shift, const float *scale, hipStream_t st);
+
 // Largest in-dimension (K) the activation preparation handles.
 int fh3k_max_in(void);
 

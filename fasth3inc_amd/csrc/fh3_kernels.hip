@@ -298,9 +298,63 @@ __global__ __launch_bounds__(256) void k_dequant_half(const uint8_t *__restrict_
 // ---------------------------------------------------------------------------
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 
+// Optional row normalisation applied before the scaling (the DiT block's
+// rmsnorm + AdaLN modulate in front of its qkv and fc1 products, reference
+// src/model/fh3_dit.c:383-386 and 430-433): when w is set,
+//   x = (x * inv_rms) * w,  inv_rms = 1 / sqrt(sum(x*x) / K + eps)
+// (src/core/fh3_ops.c:410-456), then, when shift is set,
+//   x = fma(x, 1 + scale[t], shift[t])   (src/core/fh3_ops.c:529-557),
+// shift / scale being [M][K] rows.
+struct RowNorm {
+    const float *w;
+    float eps;
+    const float *shift, *scale;
+};
+
+// Sum over the 256 threads of a workgroup, returned to every thread.
+__device__ __forceinline__ float block_sum256(float v, float *s_red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) s_red[wave] = v;
+    __syncthreads();
+    v = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    __syncthreads();
+    return v;
+}
+
+template <int V4>
+__device__ __forceinline__ void row_norm(f32x4 (&v)[V4], const RowNorm &nm, int t, int K, float *s_red) {
+    const int tid = threadIdx.x, n4 = K / 4;
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < V4; i++)
+        ss = __builtin_fmaf(v[i].w, v[i].w, __builtin_fmaf(v[i].z, v[i].z,
+             __builtin_fmaf(v[i].y, v[i].y, __builtin_fmaf(v[i].x, v[i].x, ss))));
+    ss = block_sum256(ss, s_red);
+    const float inv = 1.0f / __builtin_sqrtf(ss / (float)K + nm.eps);
+    const f32x4 *w4 = reinterpret_cast<const f32x4 *>(nm.w);
+    const f32x4 *sh4 = reinterpret_cast<const f32x4 *>(nm.shift ? nm.shift + (size_t)t * K : nullptr);
+    const f32x4 *sc4 = reinterpret_cast<const f32x4 *>(nm.scale ? nm.scale + (size_t)t * K : nullptr);
+#pragma unroll
+    for (int i = 0; i < V4; i++) {
+        const int k4 = tid + 256 * i;
+        if (k4 < n4) {
+            const f32x4 w = w4[k4];
+            f32x4 y = {(v[i].x * inv) * w.x, (v[i].y * inv) * w.y, (v[i].z * inv) * w.z, (v[i].w * inv) * w.w};
+            if (sh4) {
+                const f32x4 a = sh4[k4], c = sc4[k4];
+                y = f32x4{__builtin_fmaf(y.x, 1.0f + c.x, a.x), __builtin_fmaf(y.y, 1.0f + c.y, a.y),
+                          __builtin_fmaf(y.z, 1.0f + c.z, a.z), __builtin_fmaf(y.w, 1.0f + c.w, a.w)};
+            }
+            v[i] = y;
+        }
+    }
+}
+
 template <int V4>
 __global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ X, int M, int K,
-                                               half8 *__restrict__ X16, float *__restrict__ xs_inv) {
+                                               half8 *__restrict__ X16, float *__restrict__ xs_inv, RowNorm nm) {
     __shared__ float s_red[4];
     // Consecutive workgroup ids go to different XCDs; give each XCD a
     // contiguous run of rows instead, so that neighbouring rows, which share
@@ -317,8 +371,11 @@ __global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ X, int 
         const int k4 = tid + 256 * i;
         v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (t < M && k4 < n4) v[i] = xr[k4];
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
     }
+    if (nm.w && t < M) row_norm<V4>(v, nm, t, K, s_red);  // uniform per workgroup
+#pragma unroll
+    for (int i = 0; i < V4; i++)
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
     if (lane == 0) s_red[wave] = mx;
@@ -345,6 +402,52 @@ __global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ X, int 
             dst[(size_t)(k4 >> 2) * 128 + ((k4 >> 1) & 1) * 64 + (k4 & 1)] = h;
         }
     }
+}
+
+// The same normalisation into fp32 rows (the prepared form of the one- and
+// two-token kernel, and the device form of rmsnorm / modulate): one
+// workgroup per row, Y may alias X.
+template <int V4>
+__global__ __launch_bounds__(256) void k_rownorm_f32(const float *X, int K, float *Y,
+                                                     RowNorm nm) {
+    __shared__ float s_red[4];
+    const int t = blockIdx.x, tid = threadIdx.x, n4 = K / 4;
+    const f32x4 *xr = reinterpret_cast<const f32x4 *>(X + (size_t)t * K);
+    f32x4 v[V4];
+#pragma unroll
+    for (int i = 0; i < V4; i++) {
+        const int k4 = tid + 256 * i;
+        v[i] = k4 < n4 ? xr[k4] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    row_norm<V4>(v, nm, t, K, s_red);
+    f32x4 *yr = reinterpret_cast<f32x4 *>(Y + (size_t)t * K);
+#pragma unroll
+    for (int i = 0; i < V4; i++) {
+        const int k4 = tid + 256 * i;
+        if (k4 < n4) yr[k4] = v[i];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Product epilogues (runtime, uniform per launch): the DiT block's operations
+// right after its linears, reference src/model/fh3_dit.c:416, 436, 439.
+//   EPI_NONE      Y[t][o] = y
+//   EPI_GATE_RES  Y[t][o] = fma(aux[t][o], y, Y[t][o])      (fh3_gate_residual,
+//                 src/core/fh3_ops.c:559-585; Y is the residual stream h)
+//   EPI_SWIGLU    the weight has 2F rows [val | gate]; Y[t][j] = val_j * silu(gate_j)
+//                 with Y of width F (fh3_swiglu, src/core/fh3_ops.c:507-527);
+//                 a workgroup then owns output columns and takes rows j and
+//                 F + j together.
+// y is the product value with bias, exactly what fh3_matmul would store.
+// ---------------------------------------------------------------------------
+constexpr int EPI_NONE = 0, EPI_GATE_RES = 1, EPI_SWIGLU = 2;
+
+// silu(g) = g / (1 + exp(-g)), 0 below -80 (src/core/fh3_ops.c:515-520)
+__device__ __forceinline__ float silu_f32(float g) { return g < -80.0f ? 0.0f : g / (1.0f + expf(-g)); }
+
+__device__ __forceinline__ void epi_store(float *Y, const float *aux, int epi, size_t idx, float y) {
+    if (epi == EPI_GATE_RES) Y[idx] = __builtin_fmaf(aux[idx], y, Y[idx]);
+    else Y[idx] = y;
 }
 
 // ---------------------------------------------------------------------------
@@ -480,7 +583,8 @@ __device__ __forceinline__ void skinny_superblock(const u32x4 hv, const u32x4 ca
 template <int TB, int C, int MAXT = 512, int RMAX = (TB == 1 ? 5 : 3)>
 __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_skinny(
     const uint8_t *__restrict__ W, int64_t row_bytes, int N, int K, const half8 *__restrict__ X16,
-    const float *__restrict__ xs_inv, const float *__restrict__ bias, float *__restrict__ Y, int M) {
+    const float *__restrict__ xs_inv, const float *__restrict__ bias, float *__restrict__ Y, int M, int epi,
+    const float *__restrict__ aux) {
     extern __shared__ f32x4 red[];  // [NW][TB][64]
     constexpr int RING = C < RMAX ? C : RMAX;
     constexpr int AB = TB == 1 ? 2 : 1;  // activation buffers
@@ -488,8 +592,10 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) vo
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane & 15, q = lane >> 4;
-    const int o0 = blockIdx.x * 16;
-    const int orow = o0 + j < N ? o0 + j : N - 1;
+    // rows o0..o0+15, or (SwiGLU) rows o0..o0+7 and F+o0..F+o0+7
+    const int F = N >> 1;
+    const int o0 = epi == EPI_SWIGLU ? blockIdx.x * 8 : blockIdx.x * 16;
+    const int orow = epi == EPI_SWIGLU ? (j < 8 ? o0 + j : F + o0 + j - 8) : (o0 + j < N ? o0 + j : N - 1);
     const int nsb = K / 256;
     const int kf_n = K / 16;
     const int own = wave * C;                          // first super-block this wave owns
@@ -545,6 +651,19 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) vo
     // 4*(l/16) + v; the workgroup may have fewer threads than TB*64
     for (int idx = threadIdx.x; idx < TB * 64; idx += blockDim.x) {
         const int tb = idx >> 6, l = idx & 63;
+        if (epi == EPI_SWIGLU) {
+            if ((l & 15) >= 8) continue;  // the gate column of l is l + 8
+            f32x4 sv = red[tb * 64 + l], sg = red[tb * 64 + l + 8];
+            for (int w = 1; w < NW; w++) sv += red[(w * TB + tb) * 64 + l], sg += red[(w * TB + tb) * 64 + l + 8];
+            const int o = o0 + (l & 15);
+            const float bv = bias ? bias[o] : 0.f, bg = bias ? bias[F + o] : 0.f;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int t = tb * 16 + 4 * (l >> 4) + v;
+                if (t < M) Y[(size_t)t * F + o] = (sv[v] * xs_inv[t] + bv) * silu_f32(sg[v] * xs_inv[t] + bg);
+            }
+            continue;
+        }
         f32x4 s = red[tb * 64 + l];
         for (int w = 1; w < NW; w++) s += red[(w * TB + tb) * 64 + l];
         const int o = o0 + (l & 15);
@@ -553,7 +672,7 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) vo
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int t = tb * 16 + 4 * (l >> 4) + v;
-                if (t < M) Y[(size_t)t * N + o] = s[v] * xs_inv[t] + bo;
+                if (t < M) epi_store(Y, aux, epi, (size_t)t * N + o, s[v] * xs_inv[t] + bo);
             }
         }
     }
@@ -619,7 +738,7 @@ __device__ __forceinline__ float wave_max_f32(float v) {
 template <int MT, int C, int RMAX = 4>
 __global__ __launch_bounds__(512) void k_gemv8(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int K,
                                                const float *__restrict__ X, const float *__restrict__ bias,
-                                               float *__restrict__ Y, int M) {
+                                               float *__restrict__ Y, int M, int epi, const float *__restrict__ aux) {
     constexpr int WAVE_LDS = C * MT * 2 * G8_REC;
     constexpr int RING = C < RMAX ? C : RMAX;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
@@ -627,8 +746,9 @@ __global__ __launch_bounds__(512) void k_gemv8(const uint8_t *__restrict__ W, in
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, qd = lane >> 4;
-    const int o0 = blockIdx.x * 16;
-    const int orow = o0 + r < N ? o0 + r : N - 1;
+    const int F = N >> 1;
+    const int o0 = epi == EPI_SWIGLU ? blockIdx.x * 8 : blockIdx.x * 16;
+    const int orow = epi == EPI_SWIGLU ? (r < 8 ? o0 + r : F + o0 + r - 8) : (o0 + r < N ? o0 + r : N - 1);
     const int nsb = K >> 8;
     const int own = wave * C;
     const int s0 = own < nsb - C ? own : nsb - C;
@@ -773,8 +893,18 @@ __global__ __launch_bounds__(512) void k_gemv8(const uint8_t *__restrict__ W, in
         const int l = tl * 32 + rr;
         float sum = 0.f;
         for (int w = 0; w < NW; w++) sum += reinterpret_cast<const float *>(lds8 + w * WAVE_LDS)[l];
-        const int o = o0 + rr;
-        if (tl < M && o < N) Y[(size_t)tl * N + o] = sum + (bias ? bias[o] : 0.f);
+        if (epi == EPI_SWIGLU) {
+            if (rr < 8 && tl < M) {  // gate of column rr is row rr + 8 of this block
+                float sg = 0.f;
+                for (int w = 0; w < NW; w++) sg += reinterpret_cast<const float *>(lds8 + w * WAVE_LDS)[l + 8];
+                const int o = o0 + rr;
+                const float bv = bias ? bias[o] : 0.f, bg = bias ? bias[F + o] : 0.f;
+                Y[(size_t)tl * F + o] = (sum + bv) * silu_f32(sg + bg);
+            }
+        } else {
+            const int o = o0 + rr;
+            if (tl < M && o < N) epi_store(Y, aux, epi, (size_t)tl * N + o, sum + (bias ? bias[o] : 0.f));
+        }
     }
 }
 
@@ -850,7 +980,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
                                                  const float *__restrict__ xs_inv,
                                                  const float *__restrict__ bias,
                                                  float *__restrict__ Y, int M, int m_tiles,
-                                                 int n_tiles) {
+                                                 int n_tiles, int epi, const float *__restrict__ aux) {
     __shared__ half8 lds[2][16][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
@@ -861,9 +991,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
     const int mt = L / n_tiles, nt = L - mt * n_tiles;
     const int m0 = mt * GEMM_BM, n0 = nt * GEMM_BN;
 
-    // weight-loader role
+    // weight-loader role: rows n0..n0+127, or (SwiGLU) 64 val rows from
+    // nt*64 and the 64 gate rows F + nt*64..
     const int r = tid & 127, h = tid >> 7;
+    const int F = N >> 1;
     int orow = n0 + r;
+    if (epi == EPI_SWIGLU) orow = r < 64 ? nt * 64 + r : F + nt * 64 + r - 64;
     orow = orow < N ? orow : N - 1;
     const uint8_t *wrow = W + (size_t)orow * row_bytes;
     const int wf = (r >> 5) * 4;   // first LDS fragment of this row's 32-row block
@@ -907,6 +1040,27 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
 
     // epilogue: 32x32 output D, lane l holds column l%32 (weight row) and rows
     // 8*(v/4) + 4*(l/32) + v%4 (tokens)
+    if (epi == EPI_SWIGLU) {
+        // tiles ob = 0, 1 hold val rows nt*64 + 32*ob + l%32, tiles 2, 3 the
+        // matching gate rows
+#pragma unroll
+        for (int tb = 0; tb < 2; tb++) {
+            const int tbase = m0 + 64 * wave + 32 * tb + 4 * (lane >> 5);
+#pragma unroll
+            for (int ob = 0; ob < 2; ob++) {
+                const int o = nt * 64 + 32 * ob + (lane & 31);
+                const float bv = bias ? bias[o] : 0.f, bg = bias ? bias[F + o] : 0.f;
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const int t = tbase + 8 * (v >> 2) + (v & 3);
+                    if (t < M)
+                        Y[(size_t)t * F + o] = (acc[tb][ob][v] * xs_inv[t] + bv) *
+                                               silu_f32(acc[tb][ob + 2][v] * xs_inv[t] + bg);
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int tb = 0; tb < 2; tb++) {
         const int tbase = m0 + 64 * wave + 32 * tb + 4 * (lane >> 5);
@@ -918,7 +1072,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
 #pragma unroll
             for (int v = 0; v < 16; v++) {
                 const int t = tbase + 8 * (v >> 2) + (v & 3);
-                if (t < M) Y[(size_t)t * N + o] = acc[tb][ob][v] * xs_inv[t] + bo;
+                if (t < M) epi_store(Y, aux, epi, (size_t)t * N + o, acc[tb][ob][v] * xs_inv[t] + bo);
             }
         }
     }
@@ -1193,18 +1347,44 @@ extern "C" hipError_t fh3k_dequant_f32(int type, const void *src, int64_t row_by
     }
 }
 
-extern "C" hipError_t fh3k_xprep(const float *x, int M, int K, int Mpad, void *x16, float *xs_inv,
-                                 hipStream_t st) {
-    if (Mpad % 8 || Mpad < M) return hipErrorInvalidValue;
+extern "C" hipError_t fh3k_xprep_norm(const float *x, int M, int K, int Mpad, void *x16, float *xs_inv,
+                                      const float *norm_w, float eps, const float *shift, const float *scale,
+                                      hipStream_t st) {
+    if (Mpad % 8 || Mpad < M || (shift != nullptr) != (scale != nullptr) || (shift && !norm_w))
+        return hipErrorInvalidValue;
+    const RowNorm nm{norm_w, eps, shift, scale};
     const dim3 grid((unsigned)Mpad), block(256);
     if (K <= 4096)
-        hipLaunchKernelGGL(k_xprep<4>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv);
+        hipLaunchKernelGGL(k_xprep<4>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv, nm);
     else if (K <= 8192)
-        hipLaunchKernelGGL(k_xprep<8>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv);
+        hipLaunchKernelGGL(k_xprep<8>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv, nm);
     else if (K <= 16384)
-        hipLaunchKernelGGL(k_xprep<16>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv);
+        hipLaunchKernelGGL(k_xprep<16>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv, nm);
     else if (K <= 32768)
-        hipLaunchKernelGGL(k_xprep<32>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv);
+        hipLaunchKernelGGL(k_xprep<32>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv, nm);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+extern "C" hipError_t fh3k_xprep(const float *x, int M, int K, int Mpad, void *x16, float *xs_inv,
+                                 hipStream_t st) {
+    return fh3k_xprep_norm(x, M, K, Mpad, x16, xs_inv, nullptr, 0.f, nullptr, nullptr, st);
+}
+
+extern "C" hipError_t fh3k_rownorm_f32(const float *x, int M, int K, float *y, const float *norm_w, float eps,
+                                       const float *shift, const float *scale, hipStream_t st) {
+    if (!norm_w || M <= 0 || K % 4 || (shift != nullptr) != (scale != nullptr)) return hipErrorInvalidValue;
+    const RowNorm nm{norm_w, eps, shift, scale};
+    const dim3 grid((unsigned)M), block(256);
+    if (K <= 4096)
+        hipLaunchKernelGGL(k_rownorm_f32<4>, grid, block, 0, st, x, K, y, nm);
+    else if (K <= 8192)
+        hipLaunchKernelGGL(k_rownorm_f32<8>, grid, block, 0, st, x, K, y, nm);
+    else if (K <= 16384)
+        hipLaunchKernelGGL(k_rownorm_f32<16>, grid, block, 0, st, x, K, y, nm);
+    else if (K <= 32768)
+        hipLaunchKernelGGL(k_rownorm_f32<32>, grid, block, 0, st, x, K, y, nm);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -1230,47 +1410,61 @@ static void skinny_split(int nsb, int &C, int &NW) {
     NW = C ? (nsb + C - 1) / C : 0;
 }
 
+// Workgroups of the 16-row kernels: 16 rows each, or 8 output columns (16
+// weight rows) under SwiGLU.
+static unsigned row_blocks16(int N, int epi) {
+    return (unsigned)(epi == EPI_SWIGLU ? (N / 2) / 8 : (N + 15) / 16);
+}
+
 template <int TB, int C>
 static hipError_t launch_skinny_c(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,
-                                  const float *bias, float *y, int M, int NW, hipStream_t st) {
-    const unsigned blocks = (unsigned)((N + 15) / 16);
+                                  const float *bias, float *y, int M, int NW, int epi, const float *aux,
+                                  hipStream_t st) {
     const size_t lds = (size_t)NW * TB * 64 * sizeof(f32x4);
-    hipLaunchKernelGGL((k_skinny<TB, C>), dim3(blocks), dim3(NW * 64), lds, st, (const uint8_t *)W, rb, N, K,
-                       (const half8 *)x16, xs_inv, bias, y, M);
+    hipLaunchKernelGGL((k_skinny<TB, C>), dim3(row_blocks16(N, epi)), dim3(NW * 64), lds, st, (const uint8_t *)W, rb,
+                       N, K, (const half8 *)x16, xs_inv, bias, y, M, epi, aux);
     return hipGetLastError();
 }
 
 template <int TB>
 static hipError_t launch_skinny(const void *W, int64_t rb, int N, int K, const void *x16,
-                                const float *xs_inv, const float *bias, float *y, int M, hipStream_t st) {
+                                const float *xs_inv, const float *bias, float *y, int M, int epi, const float *aux,
+                                hipStream_t st) {
     int C, NW;
     skinny_split(K / 256, C, NW);
     switch (C) {
-        case 1: return launch_skinny_c<TB, 1>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
-        case 2: return launch_skinny_c<TB, 2>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
-        case 3: return launch_skinny_c<TB, 3>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
-        case 4: return launch_skinny_c<TB, 4>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
-        case 5: return launch_skinny_c<TB, 5>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
-        case 6: return launch_skinny_c<TB, 6>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
-        case 7: return launch_skinny_c<TB, 7>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
-        case 8: return launch_skinny_c<TB, 8>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
-        case 10: return launch_skinny_c<TB, 10>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
-        case 13: return launch_skinny_c<TB, 13>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
-        case 16: return launch_skinny_c<TB, 16>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, st);
+        case 1: return launch_skinny_c<TB, 1>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 2: return launch_skinny_c<TB, 2>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 3: return launch_skinny_c<TB, 3>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 4: return launch_skinny_c<TB, 4>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 5: return launch_skinny_c<TB, 5>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 6: return launch_skinny_c<TB, 6>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 7: return launch_skinny_c<TB, 7>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 8: return launch_skinny_c<TB, 8>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 10: return launch_skinny_c<TB, 10>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 13: return launch_skinny_c<TB, 13>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 16: return launch_skinny_c<TB, 16>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+extern "C" hipError_t fh3k_skinny_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16,
+                                      const float *xs_inv, const float *bias, float *y, int M, int epi,
+                                      const float *aux, hipStream_t st) {
+    if (epi == EPI_SWIGLU && (N % 16)) return hipErrorInvalidValue;
+    const int tb = (M + 15) / 16;
+    switch (tb) {
+        case 1: return launch_skinny<1>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, epi, aux, st);
+        case 2: return launch_skinny<2>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, epi, aux, st);
+        case 3: return launch_skinny<3>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, epi, aux, st);
+        case 4: return launch_skinny<4>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, epi, aux, st);
         default: return hipErrorInvalidValue;
     }
 }
 
 extern "C" hipError_t fh3k_skinny(const void *W, int64_t row_bytes, int N, int K, const void *x16,
                                   const float *xs_inv, const float *bias, float *y, int M, hipStream_t st) {
-    const int tb = (M + 15) / 16;
-    switch (tb) {
-        case 1: return launch_skinny<1>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, st);
-        case 2: return launch_skinny<2>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, st);
-        case 3: return launch_skinny<3>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, st);
-        case 4: return launch_skinny<4>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, st);
-        default: return hipErrorInvalidValue;
-    }
+    return fh3k_skinny_epi(W, row_bytes, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st);
 }
 
 extern "C" int fh3k_skinny_max_tokens(void) { return 64; }
@@ -1294,49 +1488,61 @@ extern "C" int fh3k_gemv8_fits(int K, int M) {
 
 template <int MT, int C>
 static hipError_t launch_gemv8_c(const void *W, int64_t rb, int N, int K, const float *x, const float *bias,
-                                 float *y, int M, int NW, hipStream_t st) {
+                                 float *y, int M, int NW, int epi, const float *aux, hipStream_t st) {
     const size_t lds = (size_t)NW * C * MT * 2 * G8_REC;
-    hipLaunchKernelGGL((k_gemv8<MT, C>), dim3((unsigned)((N + 15) / 16)), dim3(NW * 64), lds, st,
-                       (const uint8_t *)W, rb, N, K, x, bias, y, M);
+    hipLaunchKernelGGL((k_gemv8<MT, C>), dim3(row_blocks16(N, epi)), dim3(NW * 64), lds, st, (const uint8_t *)W, rb,
+                       N, K, x, bias, y, M, epi, aux);
     return hipGetLastError();
 }
 
 template <int MT>
 static hipError_t launch_gemv8(const void *W, int64_t rb, int N, int K, const float *x, const float *bias, float *y,
-                               int M, hipStream_t st) {
+                               int M, int epi, const float *aux, hipStream_t st) {
     int C, NW;
     gemv8_lds(K, MT, C, NW);
     switch (C) {
-        case 1: return launch_gemv8_c<MT, 1>(W, rb, N, K, x, bias, y, M, NW, st);
-        case 2: return launch_gemv8_c<MT, 2>(W, rb, N, K, x, bias, y, M, NW, st);
-        case 3: return launch_gemv8_c<MT, 3>(W, rb, N, K, x, bias, y, M, NW, st);
-        case 4: return launch_gemv8_c<MT, 4>(W, rb, N, K, x, bias, y, M, NW, st);
-        case 5: return launch_gemv8_c<MT, 5>(W, rb, N, K, x, bias, y, M, NW, st);
-        case 6: return launch_gemv8_c<MT, 6>(W, rb, N, K, x, bias, y, M, NW, st);
-        case 7: return launch_gemv8_c<MT, 7>(W, rb, N, K, x, bias, y, M, NW, st);
-        case 8: return launch_gemv8_c<MT, 8>(W, rb, N, K, x, bias, y, M, NW, st);
-        case 10: return launch_gemv8_c<MT, 10>(W, rb, N, K, x, bias, y, M, NW, st);
-        case 13: return launch_gemv8_c<MT, 13>(W, rb, N, K, x, bias, y, M, NW, st);
-        case 16: return launch_gemv8_c<MT, 16>(W, rb, N, K, x, bias, y, M, NW, st);
+        case 1: return launch_gemv8_c<MT, 1>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
+        case 2: return launch_gemv8_c<MT, 2>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
+        case 3: return launch_gemv8_c<MT, 3>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
+        case 4: return launch_gemv8_c<MT, 4>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
+        case 5: return launch_gemv8_c<MT, 5>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
+        case 6: return launch_gemv8_c<MT, 6>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
+        case 7: return launch_gemv8_c<MT, 7>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
+        case 8: return launch_gemv8_c<MT, 8>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
+        case 10: return launch_gemv8_c<MT, 10>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
+        case 13: return launch_gemv8_c<MT, 13>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
+        case 16: return launch_gemv8_c<MT, 16>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
         default: return hipErrorInvalidValue;
     }
 }
 
+extern "C" hipError_t fh3k_gemv8_epi(const void *W, int64_t row_bytes, int N, int K, const float *x,
+                                     const float *bias, float *y, int M, int epi, const float *aux, hipStream_t st) {
+    if (!fh3k_gemv8_fits(K, M) || (epi == EPI_SWIGLU && (N % 16))) return hipErrorInvalidValue;
+    return M == 1 ? launch_gemv8<1>(W, row_bytes, N, K, x, bias, y, M, epi, aux, st)
+                  : launch_gemv8<2>(W, row_bytes, N, K, x, bias, y, M, epi, aux, st);
+}
+
 extern "C" hipError_t fh3k_gemv8(const void *W, int64_t row_bytes, int N, int K, const float *x, const float *bias,
                                  float *y, int M, hipStream_t st) {
-    if (!fh3k_gemv8_fits(K, M)) return hipErrorInvalidValue;
-    return M == 1 ? launch_gemv8<1>(W, row_bytes, N, K, x, bias, y, M, st)
-                  : launch_gemv8<2>(W, row_bytes, N, K, x, bias, y, M, st);
+    return fh3k_gemv8_epi(W, row_bytes, N, K, x, bias, y, M, EPI_NONE, nullptr, st);
+}
+
+extern "C" hipError_t fh3k_gemm_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16,
+                                    const float *xs_inv, const float *bias, float *y, int M, int epi,
+                                    const float *aux, hipStream_t st) {
+    if (epi == EPI_SWIGLU && (N % 128)) return hipErrorInvalidValue;
+    const int m_tiles = (M + GEMM_BM - 1) / GEMM_BM;
+    const int n_tiles = epi == EPI_SWIGLU ? (N / 2) / 64 : (N + GEMM_BN - 1) / GEMM_BN;
+    hipLaunchKernelGGL(k_gemm, dim3((unsigned)(m_tiles * n_tiles)), dim3(256), 0, st,
+                       (const uint8_t *)W, row_bytes, N, K, (const half8 *)x16, xs_inv, bias, y, M,
+                       m_tiles, n_tiles, epi, aux);
+    return hipGetLastError();
 }
 
 extern "C" hipError_t fh3k_gemm(const void *W, int64_t row_bytes, int N, int K, const void *x16,
                                 const float *xs_inv, const float *bias, float *y, int M, hipStream_t st) {
-    const int m_tiles = (M + GEMM_BM - 1) / GEMM_BM;
-    const int n_tiles = (N + GEMM_BN - 1) / GEMM_BN;
-    hipLaunchKernelGGL(k_gemm, dim3((unsigned)(m_tiles * n_tiles)), dim3(256), 0, st,
-                       (const uint8_t *)W, row_bytes, N, K, (const half8 *)x16, xs_inv, bias, y, M,
-                       m_tiles, n_tiles);
-    return hipGetLastError();
+    return fh3k_gemm_epi(W, row_bytes, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st);
 }
 
 extern "C" int fh3k_gemm_row_pad(void) { return GEMM_BM; }

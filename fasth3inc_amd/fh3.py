@@ -145,6 +145,14 @@ SIGNATURES = {
     "fh3_hip_prepare_x_dev": (_c_int, [_c_void_p, _c_int, _c_i64, _c_void_p, _c_void_p]),
     "fh3_hip_matmul_prepared_dev": (_c_int, [ctypes.POINTER(Fh3W), _c_void_p, _c_void_p, _c_int, _c_void_p,
                                              _c_void_p]),
+    "fh3_hip_prepare_x_norm_dev": (_c_int, [_c_void_p, _c_int, _c_i64, _c_void_p, ctypes.c_float, _c_void_p,
+                                            _c_void_p, _c_void_p, _c_void_p]),
+    "fh3_hip_rownorm_dev": (_c_int, [_c_void_p, _c_int, _c_i64, _c_void_p, ctypes.c_float, _c_void_p, _c_void_p,
+                                     _c_void_p, _c_void_p]),
+    "fh3_hip_matmul_epi_dev": (_c_int, [ctypes.POINTER(Fh3W), _c_void_p, _c_int, _c_void_p, _c_int, _c_void_p,
+                                        _c_void_p, _c_void_p]),
+    "fh3_hip_matmul_prepared_epi_dev": (_c_int, [ctypes.POINTER(Fh3W), _c_void_p, _c_int, _c_void_p, _c_int,
+                                                 _c_void_p, _c_void_p, _c_void_p]),
     "fh3_hip_graph_begin": (_c_int, [_c_void_p]),
     "fh3_hip_graph_end": (_c_int, [_c_void_p, ctypes.POINTER(_c_void_p)]),
     "fh3_hip_graph_launch": (_c_int, [_c_void_p, _c_void_p]),
@@ -340,6 +348,36 @@ def matmul_prepared_dev(d_w, K, N, d_prep, d_y, n_tok, d_bias=None, stream_ptr=N
     w = Fh3W(qtype, K, N, _ptr_of(d_w))
     _check(lib().fh3_hip_matmul_prepared_dev(ctypes.byref(w), _ptr_of(d_prep), _ptr_of(d_y), n_tok,
                                              _ptr_of(d_bias), stream_ptr), "fh3_hip_matmul_prepared_dev")
+
+
+EPI_NONE, EPI_GATE_RESIDUAL, EPI_SWIGLU = 0, 1, 2
+
+
+def prepare_x_norm_dev(d_x, n_tok, K, d_norm_w, eps, d_prep, d_shift=None, d_scale=None, stream_ptr=None):
+    """fh3_hip_prepare_x_norm_dev: rmsnorm (+ modulate) fused into the activation prep."""
+    _check(lib().fh3_hip_prepare_x_norm_dev(_ptr_of(d_x), n_tok, K, _ptr_of(d_norm_w), eps, _ptr_of(d_shift),
+                                            _ptr_of(d_scale), _ptr_of(d_prep), stream_ptr),
+           "fh3_hip_prepare_x_norm_dev")
+
+
+def rownorm_dev(d_x, n_tok, K, d_norm_w, eps, d_y, d_shift=None, d_scale=None, stream_ptr=None):
+    _check(lib().fh3_hip_rownorm_dev(_ptr_of(d_x), n_tok, K, _ptr_of(d_norm_w), eps, _ptr_of(d_shift),
+                                     _ptr_of(d_scale), _ptr_of(d_y), stream_ptr), "fh3_hip_rownorm_dev")
+
+
+def matmul_epi_dev(d_w, K, N, d_x, n_tok, epi, d_out, d_aux=None, d_bias=None, stream_ptr=None,
+                   qtype=FH3_QUANT_Q4_K):
+    w = Fh3W(qtype, K, N, _ptr_of(d_w))
+    _check(lib().fh3_hip_matmul_epi_dev(ctypes.byref(w), _ptr_of(d_x), n_tok, _ptr_of(d_bias), epi,
+                                        _ptr_of(d_aux), _ptr_of(d_out), stream_ptr), "fh3_hip_matmul_epi_dev")
+
+
+def matmul_prepared_epi_dev(d_w, K, N, d_prep, n_tok, epi, d_out, d_aux=None, d_bias=None, stream_ptr=None,
+                            qtype=FH3_QUANT_Q4_K):
+    w = Fh3W(qtype, K, N, _ptr_of(d_w))
+    _check(lib().fh3_hip_matmul_prepared_epi_dev(ctypes.byref(w), _ptr_of(d_prep), n_tok, _ptr_of(d_bias), epi,
+                                                 _ptr_of(d_aux), _ptr_of(d_out), stream_ptr),
+           "fh3_hip_matmul_prepared_epi_dev")
 
 
 class Graph:

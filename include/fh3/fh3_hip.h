@@ -82,6 +82,40 @@ int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, void *d_prep,
 int fh3_hip_matmul_prepared_dev(const Fh3W *w, const void *d_prep, float *d_y, int n_tok,
                                 const float *d_bias_or_null, void *stream);
 
+/* The DiT block around its linears (reference src/model/fh3_dit.c:383-439),
+ * fused on the device.
+ *
+ * Prologue: fh3_hip_prepare_x_norm_dev fills a prepared buffer (as
+ * fh3_hip_prepare_x_dev) from rows first normalised by rmsnorm with weight
+ * d_norm_w[in] and eps (src/core/fh3_ops.c:410-456), then, when d_shift and
+ * d_scale ([n_tok][in]) are both set, AdaLN-modulated
+ * x*(1+scale)+shift (src/core/fh3_ops.c:529-557): one launch in place of
+ * fh3_rmsnorm + fh3_modulate + the activation preparation.  Sums run in a
+ * different order than the CPU's (fp32), then the usual fp16 / int16
+ * conversion.  fh3_hip_rownorm_dev writes the same normalised rows as fp32
+ * (d_y may equal d_x): the device form of fh3_rmsnorm (+ fh3_modulate).
+ *
+ * Epilogues, Q4_K weights, on the product fh3_hip_matmul_dev would compute
+ * (bias included):
+ *   FH3_EPI_GATE_RESIDUAL  d_out[n_tok][out] += d_aux[n_tok][out] * y
+ *                          (fh3_gate_residual, src/core/fh3_ops.c:559-585);
+ *   FH3_EPI_SWIGLU         the weight's rows are [val (F) | gate (F)],
+ *                          out = 2F with out % 128 == 0;
+ *                          d_out[n_tok][F] = val * silu(gate)
+ *                          (fh3_swiglu, src/core/fh3_ops.c:507-527).
+ * Each replaces a product and an elementwise pass over its output. */
+#define FH3_EPI_NONE          0
+#define FH3_EPI_GATE_RESIDUAL 1
+#define FH3_EPI_SWIGLU        2
+int fh3_hip_prepare_x_norm_dev(const float *d_x, int n_tok, int64_t in, const float *d_norm_w, float eps,
+                               const float *d_shift, const float *d_scale, void *d_prep, void *stream);
+int fh3_hip_rownorm_dev(const float *d_x, int n_tok, int64_t in, const float *d_norm_w, float eps,
+                        const float *d_shift, const float *d_scale, float *d_y, void *stream);
+int fh3_hip_matmul_epi_dev(const Fh3W *w, const float *d_x, int n_tok, const float *d_bias_or_null, int epi,
+                           const float *d_aux, float *d_out, void *stream);
+int fh3_hip_matmul_prepared_epi_dev(const Fh3W *w, const void *d_prep, int n_tok, const float *d_bias_or_null,
+                                    int epi, const float *d_aux, float *d_out, void *stream);
+
 /* HIP graph capture of work enqueued on a stream (NULL = the compute
  * stream), for launch-bound loops such as small-M text-encoder layers:
  * begin, enqueue fh3_hip_* calls on that stream, end -> an executable graph

@@ -1,7 +1,8 @@
 /*
- * fh3_oracle.c -- CPU restatement of fh3's Q4_K linear layer and of every
- * block decoder of src/core/fh3_quant.c (F32, F16, BF16, Q8_0, Q2_K, Q3_K,
- * Q4_K, Q5_K, Q6_K).  TEST INFRASTRUCTURE ONLY (see fh3_oracle.h): the checker
+ * fh3_oracle.c -- CPU restatement of fh3's linear layer (any decodable weight
+ * type), of every block decoder of src/core/fh3_quant.c (F32, F16, BF16, Q8_0,
+ * Q2_K, Q3_K, Q4_K, Q5_K, Q6_K) and of the DiT block's elementwise ops around
+ * the layer (rmsnorm, modulate, swiglu, gate_residual).  TEST INFRASTRUCTURE ONLY (see fh3_oracle.h): the checker
  * and CPU baseline for the HIP product.
  *
  * Build flags follow the reference (CMakeLists.txt:15-26): -O3 -mavx2 -mfma
@@ -349,3 +350,58 @@ void fh3_oracle_matmul(const Fh3OracleW *w, const float *x, float *y,
 }
 
 int fh3_oracle_threads(void) { return omp_get_max_threads(); }
+
+/* ------------------------------------------------------------------------ */
+/* The DiT block's elementwise ops around the linear layer                   */
+/* (src/core/fh3_ops.c:410-585), as the reference's AVX2/FMA build computes   */
+/* them: rmsnorm sums x*x in 8 fmaf lanes (element d in lane d%8) reduced by  */
+/* the fixed tree, then a scalar fmaf tail; modulate and gate_residual fuse   */
+/* their multiply-add on the 8-wide part of each 1024-element chunk.          */
+/* ------------------------------------------------------------------------ */
+void fh3_oracle_rmsnorm(float *x, const float *w, int n, int dim, float eps) {
+    if (!x || !w || n <= 0 || dim <= 0) return;
+    const int64_t d8 = dim - (dim % 8);
+    for (int i = 0; i < n; i++) {
+        float *row = x + (size_t)i * (size_t)dim;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int64_t d = 0; d < d8; d++) acc[d % 8] = fmaf(row[d], row[d], acc[d % 8]);
+        float sum = oracle_tree8(acc);
+        for (int64_t d = d8; d < dim; d++) sum = fmaf(row[d], row[d], sum);
+        const float inv_rms = 1.0f / sqrtf(sum / (float)dim + eps);
+        for (int64_t d = 0; d < dim; d++) row[d] = row[d] * inv_rms * w[d];
+    }
+}
+
+/* src/core/fh3_ops.c:529-557: x = x*(1+scale) + shift, fused on the 8-wide
+ * part, two roundings on a chunk's tail (the build has -ffp-contract=off). */
+void fh3_oracle_modulate(float *x, const float *shift, const float *scale, int n, int dim) {
+    if (!x || !shift || !scale || n <= 0 || dim <= 0) return;
+    const int64_t total = (int64_t)n * (int64_t)dim;
+    for (int64_t k0 = 0; k0 < total; k0 += 1024) {
+        const int64_t k1 = k0 + 1024 <= total ? k0 + 1024 : total;
+        const int64_t kv = k0 + ((k1 - k0) / 8) * 8;
+        for (int64_t k = k0; k < kv; k++) x[k] = fmaf(x[k], 1.0f + scale[k], shift[k]);
+        for (int64_t k = kv; k < k1; k++) x[k] = x[k] * (1.0f + scale[k]) + shift[k];
+    }
+}
+
+/* src/core/fh3_ops.c:507-527: out[j] = val[j] * silu(gate[j]), the input row
+ * being [val (F) | gate (F)]; silu(g) = g / (1 + expf(-g)), 0 below -80. */
+void fh3_oracle_swiglu(const float *in, float *out, int n, int F) {
+    if (!in || !out || n <= 0 || F <= 0) return;
+    for (int i = 0; i < n; i++) {
+        const float *val = in + (size_t)i * 2 * (size_t)F, *gate = val + F;
+        for (int j = 0; j < F; j++) {
+            const float g = gate[j];
+            const float s = g < -80.0f ? 0.0f : g / (1.0f + expf(-g));
+            out[(size_t)i * (size_t)F + j] = val[j] * s;
+        }
+    }
+}
+
+/* src/core/fh3_ops.c:559-585: h = fmaf(gate, y, h) element by element. */
+void fh3_oracle_gate_residual(float *h, const float *gate, const float *y, int n, int dim) {
+    if (!h || !gate || !y || n <= 0 || dim <= 0) return;
+    const int64_t total = (int64_t)n * (int64_t)dim;
+    for (int64_t k = 0; k < total; k++) h[k] = fmaf(gate[k], y[k], h[k]);
+}

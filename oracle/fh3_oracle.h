@@ -62,6 +62,15 @@ void fh3_oracle_matmul_rows(const Fh3OracleW *w, const float *x, float *y,
 /* Number of OpenMP threads the oracle runs with (omp_get_max_threads()). */
 int fh3_oracle_threads(void);
 
+/* The DiT block's elementwise ops around the linear layer, as the reference's
+ * AVX2/FMA build computes them (bitwise):
+ *   src/core/fh3_ops.c:410-456 rmsnorm, :529-557 modulate, :507-527 swiglu,
+ *   :559-585 gate_residual. */
+void fh3_oracle_rmsnorm(float *x, const float *w, int n, int dim, float eps);
+void fh3_oracle_modulate(float *x, const float *shift, const float *scale, int n, int dim);
+void fh3_oracle_swiglu(const float *in, float *out, int n, int F);
+void fh3_oracle_gate_residual(float *h, const float *gate, const float *y, int n, int dim);
+
 #ifdef __cplusplus
 }
 #endif

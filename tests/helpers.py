@@ -50,7 +50,17 @@ def load_oracle():
     lib.fh3_oracle_matmul_rows.argtypes = [ctypes.POINTER(OracleW), ctypes.c_void_p, ctypes.c_void_p,
                                            ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64]
     lib.fh3_oracle_threads.restype = ctypes.c_int
+    _bind_elementwise(lib, "fh3_oracle_")
     return lib
+
+
+def _bind_elementwise(lib, prefix):
+    P, I, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+    for name, args in (("rmsnorm", [P, P, I, I, F]), ("modulate", [P, P, P, I, I]), ("swiglu", [P, P, I, I]),
+                       ("gate_residual", [P, P, P, I, I])):
+        f = getattr(lib, prefix + name)
+        f.restype = None
+        f.argtypes = args
 
 
 def load_ref():
@@ -68,7 +78,15 @@ def load_ref():
     lib.fh3_row_bytes.argtypes = [ctypes.c_int, ctypes.c_int64]
     lib.fh3_rng_normal.restype = None
     lib.fh3_rng_normal.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_size_t]
+    _bind_elementwise(lib, "fh3_")
     return lib
+
+
+def elementwise(lib, prefix, op, *arrays_and_sizes):
+    """Call <prefix><op> on numpy arrays (passed by pointer) and ints/floats;
+    arrays are modified in place as the C function does."""
+    args = [a.ctypes.data_as(ctypes.c_void_p) if isinstance(a, np.ndarray) else a for a in arrays_and_sizes]
+    getattr(lib, prefix + op)(*args)
 
 
 def oracle_dequant(lib, raw, n_rows, n_cols, qtype=Q4_K, fn="fh3_oracle_dequant"):

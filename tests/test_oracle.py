@@ -241,3 +241,55 @@ def test_matmul_other_types_bitwise_vs_reference_build(oracle, ref, name):
         yr = H.matmul_with(ref, "fh3_matmul", raw, K, N, x, b, qtype=t)
         assert np.isfinite(yo).all()
         assert np.array_equal(yo.view(np.uint32), yr.view(np.uint32))
+
+
+# --------------------------------------------------------------------------
+# The DiT block's elementwise ops (src/core/fh3_ops.c:410-585) vs the build
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("n,dim", [(3, 5120), (2, 1000), (5, 13), (1, 7)])
+def test_elementwise_ops_bitwise_vs_reference_build(oracle, ref, n, dim):
+    rng = np.random.default_rng(n * 100 + dim)
+    x = (rng.standard_normal((n, dim)) * 3).astype(np.float32)
+    w = rng.standard_normal(dim).astype(np.float32)
+    shift = rng.standard_normal((n, dim)).astype(np.float32)
+    scale = (rng.standard_normal((n, dim)) * 0.3).astype(np.float32)
+    gate = rng.standard_normal((n, dim)).astype(np.float32)
+    res = []
+    for lib, pre in ((oracle, "fh3_oracle_"), (ref, "fh3_")):
+        a = x.copy()
+        H.elementwise(lib, pre, "rmsnorm", a, w, n, dim, 1e-6)
+        b = a.copy()
+        H.elementwise(lib, pre, "modulate", b, shift, scale, n, dim)
+        h = x.copy()
+        H.elementwise(lib, pre, "gate_residual", h, gate, b, n, dim)
+        F = dim // 2 if dim % 2 == 0 else dim
+        sw_in = np.ascontiguousarray(np.concatenate([x, gate], axis=1)[:, : 2 * F] * 10).astype(np.float32)
+        sw = np.zeros((n, F), np.float32)
+        H.elementwise(lib, pre, "swiglu", sw_in, sw, n, F)
+        res.append((a, b, h, sw))
+    for o, r in zip(res[0], res[1]):
+        assert np.array_equal(o.view(np.uint32), r.view(np.uint32))
+
+
+def test_elementwise_closed_forms(oracle):
+    """rmsnorm of a constant row is w; modulate by (shift 0, scale 0) is the
+    identity; swiglu of gate 0 is 0 and of a very negative gate is exactly 0;
+    gate_residual with gate 0 leaves h."""
+    dim = 64
+    x = np.full((1, dim), 3.0, np.float32)
+    w = np.arange(dim, dtype=np.float32) / 7
+    H.elementwise(oracle, "fh3_oracle_", "rmsnorm", x, w, 1, dim, 0.0)
+    assert np.allclose(x[0], w, rtol=1e-6)
+    y = np.random.default_rng(0).standard_normal((2, dim)).astype(np.float32)
+    z = y.copy()
+    H.elementwise(oracle, "fh3_oracle_", "modulate", z, np.zeros_like(y), np.zeros_like(y), 2, dim)
+    assert np.array_equal(z, y)
+    sw_in = np.zeros((1, 2 * dim), np.float32)
+    sw_in[0, :dim] = 5.0
+    sw_in[0, dim:] = np.linspace(-100, 0, dim, dtype=np.float32)
+    out = np.ones((1, dim), np.float32)
+    H.elementwise(oracle, "fh3_oracle_", "swiglu", sw_in, out, 1, dim)
+    assert out[0, -1] == 0.0 and (out[0, sw_in[0, dim:] < -80] == 0.0).all()
+    h = y.copy()
+    H.elementwise(oracle, "fh3_oracle_", "gate_residual", h, np.zeros_like(y), z, 2, dim)
+    assert np.array_equal(h, y)

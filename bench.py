@@ -155,7 +155,10 @@ def dit_blocks_streamed(ev, st, n_blocks=8, M=16384, passes=2):
     through two device slots (hipMemcpyAsync on the upload stream), M = 16384
     tokens.  Per block: acquire_dev(L), prefetch_dev(L+1), the four
     fh3_hip_matmul_dev calls.  Timed beside the same blocks resident in HBM,
-    and beside the uploads alone."""
+    beside the uploads alone, and streamed as the block's fused sequence
+    (norm1+modulate prep -> qkv; out-proj with the gate residual into h;
+    norm2+modulate prep -> fc1 with SwiGLU -> fc2 with the gate residual),
+    the attention output standing in for its input."""
     import tempfile
     from fasth3inc_amd import pack as P
     hidden, qkv, mlp = 5120, 15360, 13824
@@ -172,10 +175,24 @@ def dit_blocks_streamed(ev, st, n_blocks=8, M=16384, passes=2):
         xa = F.DeviceBuffer.from_array(F.synth_x("outliers", 5, 1, M, hidden))
         xm = F.DeviceBuffer.from_array(F.synth_x("silu_gated", 5, 2, M, mlp))
         ys = [F.DeviceBuffer(M * n * 4) for n in (qkv, hidden, 2 * mlp, hidden)]
+        h = F.DeviceBuffer.from_array(F.synth_x("normal", 5, 3, M, hidden))
+        mods = [F.DeviceBuffer.from_array(0.1 * F.synth_x("normal", 5, 10 + i, M, hidden)) for i in range(3)]
+        prep = F.DeviceBuffer(F.prepared_bytes(M, hidden))
+        act = F.DeviceBuffer(M * mlp * 4)
         res = {"blocks": n_blocks, "M": M, "block_weight_bytes": block_wbytes, "block_flop": block_flop,
                "shapes": "qkv 5120->15360, out 5120->5120, fc1 (up|gate) 5120->27648, fc2 (down) 13824->5120"}
 
-        def run_pass(tr, compute=True):
+        shift, scale, gate = mods
+
+        def fused_block(v):
+            F.prepare_x_norm_dev(h, M, hidden, v.norm1.data, 1e-6, prep, shift, scale)
+            F.matmul_prepared_dev(v.qkv.data, hidden, qkv, prep, ys[0], M)
+            F.matmul_epi_dev(v.out.data, hidden, hidden, xa, M, F.EPI_GATE_RESIDUAL, h, gate)
+            F.prepare_x_norm_dev(h, M, hidden, v.norm2.data, 1e-6, prep, shift, scale)
+            F.matmul_prepared_epi_dev(v.fc1.data, hidden, 2 * mlp, prep, M, F.EPI_SWIGLU, act)
+            F.matmul_epi_dev(v.fc2.data, mlp, hidden, act, M, F.EPI_GATE_RESIDUAL, h, gate)
+
+        def run_pass(tr, compute=True, fused=False):
             for L in range(n_blocks):
                 d = tr.acquire_dev(L)
                 if d is None:
@@ -184,24 +201,33 @@ def dit_blocks_streamed(ev, st, n_blocks=8, M=16384, passes=2):
                 if not compute:
                     continue
                 v = tr.layer(L, d)
+                if fused:
+                    fused_block(v)
+                    continue
                 for w, x, y in ((v.qkv, xa, ys[0]), (v.out, xa, ys[1]), (v.fc1, xa, ys[2]), (v.fc2, xm, ys[3])):
                     F.matmul_dev(w.data, w.in_, w.out, x, y, M)
 
-        for label, dev_budget, compute in (("streamed", 0, True), ("resident", 1 << 40, True),
-                                           ("uploads_only", 0, False)):
+        for label, dev_budget, compute, fused in (("streamed", 0, True, False), ("resident", 1 << 40, True, False),
+                                                  ("uploads_only", 0, False, False),
+                                                  ("streamed_fused_block", 0, True, True)):
             with F.Trunk(path, 1 << 40) as tr:
+                a0 = time.perf_counter()
                 tr.attach_device(dev_budget)
-                run_pass(tr, compute)
+                attach_s = time.perf_counter() - a0
+                run_pass(tr, compute, fused)
                 F.synchronize()
                 u0 = tr.dev_stats().uploads
                 w0 = time.perf_counter()
-                ms = ev.time_ms(lambda i: run_pass(tr, compute), passes, st)
+                ms = ev.time_ms(lambda i: run_pass(tr, compute, fused), passes, st)
                 F.synchronize()
                 wall = (time.perf_counter() - w0) / passes
                 ups = tr.dev_stats().uploads - u0
             per_block = ms / n_blocks
             entry = {"ms_per_block": round(per_block, 3), "wall_ms_per_block": round(wall * 1e3 / n_blocks, 3),
                      "uploads_per_pass": ups // passes}
+            if dev_budget:
+                entry["attach_s"] = round(attach_s, 3)
+                entry["attach_GBps"] = round(n_blocks * block_wbytes / attach_s / 1e9, 1)
             if compute:
                 entry["TFLOPs"] = round(block_flop / (per_block * 1e-3) / 1e12, 1)
             else:
@@ -210,7 +236,9 @@ def dit_blocks_streamed(ev, st, n_blocks=8, M=16384, passes=2):
             log("[bench] DiT blocks %s: %.3f ms/block %s" % (label, per_block, entry))
         res["unhidden_upload_ms_per_block"] = round(res["streamed"]["ms_per_block"] -
                                                     res["resident"]["ms_per_block"], 3)
-        for b in [xa, xm] + ys:
+        res["fused_ops_ms_per_block"] = round(res["streamed_fused_block"]["ms_per_block"] -
+                                              res["streamed"]["ms_per_block"], 3)
+        for b in [xa, xm, h, prep, act] + ys + mods:
             b.close()
         return res
     finally:

@@ -2,8 +2,9 @@
  * fh3_oracle.c -- CPU restatement of fh3's linear layer (any decodable weight
  * type), of every block decoder of src/core/fh3_quant.c (F32, F16, BF16, Q8_0,
  * Q2_K, Q3_K, Q4_K, Q5_K, Q6_K) and of the DiT block's elementwise ops around
- * the layer (rmsnorm, modulate, swiglu, gate_residual).  TEST INFRASTRUCTURE ONLY (see fh3_oracle.h): the checker
- * and CPU baseline for the HIP product.
+ * the layer (rmsnorm, modulate, swiglu, gate_residual) and of its attention
+ * branch (rope3, dense online-softmax attention).  TEST INFRASTRUCTURE ONLY
+ * (see fh3_oracle.h): the checker and CPU baseline for the HIP product.
  *
  * Build flags follow the reference (CMakeLists.txt:15-26): -O3 -mavx2 -mfma
  * -mf16c -ffp-contract=off -fopenmp.  -ffp-contract=off matters: the
@@ -404,4 +405,103 @@ void fh3_oracle_gate_residual(float *h, const float *gate, const float *y, int n
     if (!h || !gate || !y || n <= 0 || dim <= 0) return;
     const int64_t total = (int64_t)n * (int64_t)dim;
     for (int64_t k = 0; k < total; k++) h[k] = fmaf(gate[k], y[k], h[k]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* The attention branch's ops (src/core/fh3_ops.c:458-505,587-695).          */
+/* ------------------------------------------------------------------------ */
+
+/* src/core/fh3_ops.c:458-505: rotate the first rot_dim channels of each head
+ * vector in halves, v0 = x[j], v1 = x[rot/2 + j]:
+ *   x[j]         = v0*cos[j] - v1*sin[j]
+ *   x[rot/2 + j] = v1*cos[rot/2 + j] + v0*sin[rot/2 + j]
+ * every product and the add/sub rounded separately; cos/sin are [n][rot_dim]
+ * (one row per token, shared by the heads); channels >= rot_dim untouched. */
+void fh3_oracle_rope3(float *x, const float *cos, const float *sin, int n, int heads, int head_dim,
+                      int rot_dim) {
+    if (!x || !cos || !sin || n <= 0 || heads <= 0 || head_dim <= 0 || rot_dim <= 0 || rot_dim > head_dim ||
+        (rot_dim % 2) != 0)
+        return;
+    const int half = rot_dim / 2;
+    for (int i = 0; i < n; i++) {
+        const float *c = cos + (size_t)i * (size_t)rot_dim, *s = sin + (size_t)i * (size_t)rot_dim;
+        for (int h = 0; h < heads; h++) {
+            float *v = x + ((size_t)i * (size_t)heads + (size_t)h) * (size_t)head_dim;
+            for (int j = 0; j < half; j++) {
+                const float v0 = v[j], v1 = v[half + j];
+                const float a = v0 * c[j], b = v1 * s[j];
+                const float e = v1 * c[half + j], f = v0 * s[half + j];
+                v[j] = a - b;
+                v[half + j] = e + f;
+            }
+        }
+    }
+}
+
+/* The reference's dot_product_avx2 (src/core/fh3_ops.c:50-65): 8 fmaf lanes,
+ * the fixed tree, an fmaf tail. */
+static float oracle_dot(const float *x, const float *w, int64_t n) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const int64_t n8 = n - (n % 8);
+    for (int64_t k = 0; k < n8; k++) acc[k % 8] = fmaf(x[k], w[k], acc[k % 8]);
+    float s = oracle_tree8(acc);
+    for (int64_t k = n8; k < n; k++) s = fmaf(x[k], w[k], s);
+    return s;
+}
+
+#define ORACLE_ATTN_TILE 64 /* src/core/fh3_ops.c:587 */
+
+/* src/core/fh3_ops.c:589-695, one query at a time: q/o rows [nq][heads][hd],
+ * k/v rows [nk][heads][hd] (the reference has nq = nk = n; a query's result
+ * depends only on its own row, so a subset of queries is exact).  Scores
+ * s = dot(q, k)*(1/sqrtf(hd)) over key tiles of 64; per tile m_new =
+ * max(m, tile max), alpha = expf(m - m_new), l *= alpha, acc *= alpha, then
+ * for each key p = expf(s - m_new), l += p, acc = fmaf(p, v, acc); finally
+ * o = acc * (l > 0 ? 1/l : 0).  m starts at -1e30. */
+void fh3_oracle_attention_rows(const float *q, int nq, const float *k, const float *v, int nk, float *o,
+                               int heads, int hd) {
+    if (!q || !k || !v || !o || nq <= 0 || nk <= 0 || heads <= 0 || hd <= 0) return;
+    const float scale = 1.0f / sqrtf((float)hd);
+    #pragma omp parallel
+    {
+        float *acc = (float *)malloc((size_t)hd * sizeof(float));
+        float sc[ORACLE_ATTN_TILE];
+        #pragma omp for collapse(2) schedule(static)
+        for (int h = 0; h < heads; h++) {
+            for (int i = 0; i < nq; i++) {
+                if (!acc) continue;
+                const float *qi = q + ((size_t)i * (size_t)heads + (size_t)h) * (size_t)hd;
+                float *oi = o + ((size_t)i * (size_t)heads + (size_t)h) * (size_t)hd;
+                float m = -1e30f, l = 0.0f;
+                memset(acc, 0, (size_t)hd * sizeof(float));
+                for (int j0 = 0; j0 < nk; j0 += ORACLE_ATTN_TILE) {
+                    const int B = j0 + ORACLE_ATTN_TILE <= nk ? ORACLE_ATTN_TILE : nk - j0;
+                    float mt = -INFINITY;
+                    for (int t = 0; t < B; t++) {
+                        const float *kj = k + ((size_t)(j0 + t) * (size_t)heads + (size_t)h) * (size_t)hd;
+                        sc[t] = oracle_dot(qi, kj, hd) * scale;
+                        if (t == 0 || sc[t] > mt) mt = sc[t];
+                    }
+                    const float mn = m > mt ? m : mt;
+                    const float alpha = expf(m - mn);
+                    l *= alpha;
+                    for (int d = 0; d < hd; d++) acc[d] *= alpha;
+                    for (int t = 0; t < B; t++) {
+                        const float *vj = v + ((size_t)(j0 + t) * (size_t)heads + (size_t)h) * (size_t)hd;
+                        const float p = expf(sc[t] - mn);
+                        l += p;
+                        for (int d = 0; d < hd; d++) acc[d] = fmaf(p, vj[d], acc[d]);
+                    }
+                    m = mn;
+                }
+                const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+                for (int d = 0; d < hd; d++) oi[d] = acc[d] * inv;
+            }
+        }
+        free(acc);
+    }
+}
+
+void fh3_oracle_attention(const float *q, const float *k, const float *v, float *o, int n, int heads, int hd) {
+    fh3_oracle_attention_rows(q, n, k, v, n, o, heads, hd);
 }

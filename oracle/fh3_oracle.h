@@ -71,6 +71,16 @@ void fh3_oracle_modulate(float *x, const float *shift, const float *scale, int n
 void fh3_oracle_swiglu(const float *in, float *out, int n, int F);
 void fh3_oracle_gate_residual(float *h, const float *gate, const float *y, int n, int dim);
 
+/* Attention branch (src/core/fh3_ops.c:458-505,587-695): rope3 in place on
+ * x[n][heads][head_dim] with cos/sin [n][rot_dim]; dense attention over
+ * [n][heads][hd] rows.  fh3_oracle_attention_rows computes nq queries
+ * against nk keys (the reference's result for those query rows). */
+void fh3_oracle_rope3(float *x, const float *cos, const float *sin, int n, int heads, int head_dim,
+                      int rot_dim);
+void fh3_oracle_attention(const float *q, const float *k, const float *v, float *o, int n, int heads, int hd);
+void fh3_oracle_attention_rows(const float *q, int nq, const float *k, const float *v, int nk, float *o,
+                               int heads, int hd);
+
 #ifdef __cplusplus
 }
 #endif

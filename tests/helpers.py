@@ -57,10 +57,69 @@ def load_oracle():
 def _bind_elementwise(lib, prefix):
     P, I, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
     for name, args in (("rmsnorm", [P, P, I, I, F]), ("modulate", [P, P, P, I, I]), ("swiglu", [P, P, I, I]),
-                       ("gate_residual", [P, P, P, I, I])):
+                       ("gate_residual", [P, P, P, I, I]), ("rope3", [P, P, P, I, I, I, I]),
+                       ("attention", [P, P, P, P, I, I, I])):
         f = getattr(lib, prefix + name)
         f.restype = None
         f.argtypes = args
+    if hasattr(lib, prefix + "attention_rows"):
+        f = getattr(lib, prefix + "attention_rows")
+        f.restype = None
+        f.argtypes = [P, I, P, P, I, P, I, I]
+
+
+OPS_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ops")
+
+
+def read_ops_fixture(name):
+    """The reference's op fixtures copied by tests/golden/make_ops_fixtures.py:
+    a dict of header fields and float32 arrays."""
+    raw = open(os.path.join(OPS_DIR, name + ".bin"), "rb").read()
+    u32 = lambda i: int(np.frombuffer(raw, "<u4", 1, 4 * i)[0])
+    f32 = lambda off, cnt: np.frombuffer(raw, "<f4", cnt, off).copy()
+    if name == "rmsnorm":
+        n, dim = u32(0), u32(1)
+        eps = float(np.frombuffer(raw, "<f4", 1, 8)[0])
+        o = 12
+        x = f32(o, n * dim).reshape(n, dim); o += 4 * n * dim
+        w = f32(o, dim); o += 4 * dim
+        return dict(n=n, dim=dim, eps=eps, x=x, w=w, ref=f32(o, n * dim).reshape(n, dim))
+    if name in ("modulate", "gate_residual"):
+        n, dim = u32(0), u32(1)
+        arrs = [f32(8 + 4 * n * dim * i, n * dim).reshape(n, dim) for i in range(4)]
+        keys = ("x", "shift", "scale", "ref") if name == "modulate" else ("h", "gate", "y", "ref")
+        return dict(n=n, dim=dim, **dict(zip(keys, arrs)))
+    if name == "swiglu":
+        n, F = u32(0), u32(1)
+        return dict(n=n, F=F, inp=f32(8, n * 2 * F).reshape(n, 2 * F),
+                    ref=f32(8 + 8 * n * F, n * F).reshape(n, F))
+    if name == "rope3":
+        n, heads, hd, rot = u32(0), u32(1), u32(2), u32(3)
+        cx, cr = n * heads * hd, n * rot
+        o = 16
+        x = f32(o, cx).reshape(n, heads, hd); o += 4 * cx
+        c = f32(o, cr).reshape(n, rot); o += 4 * cr
+        sn = f32(o, cr).reshape(n, rot); o += 4 * cr
+        return dict(n=n, heads=heads, hd=hd, rot=rot, x=x, cos=c, sin=sn, ref=f32(o, cx).reshape(n, heads, hd))
+    if name == "attention_sub":
+        n, heads, hd, nq = u32(0), u32(1), u32(2), u32(3)
+        o = 16
+        hidx = np.frombuffer(raw, "<i4", heads, o).copy(); o += 4 * heads
+        qidx = np.frombuffer(raw, "<i4", nq, o).copy(); o += 4 * nq
+        out = dict(n=n, heads=heads, hd=hd, nq=nq, head_idx=hidx, q_idx=qidx)
+        for key, rows in (("q", nq), ("k", n), ("v", n), ("ref", nq)):
+            cnt = rows * heads * hd
+            out[key] = f32(o, cnt).reshape(rows, heads, hd)
+            o += 4 * cnt
+        return out
+    raise ValueError(name)
+
+
+def check_close(actual, ref):
+    """The reference's test_ops.c check_close metric: max |a - r| / max(|r|, 1)."""
+    a = np.asarray(actual, np.float64).ravel()
+    r = np.asarray(ref, np.float64).ravel()
+    return float(np.max(np.abs(a - r) / np.maximum(np.abs(r), 1.0)))
 
 
 def load_ref():

@@ -293,3 +293,99 @@ def test_elementwise_closed_forms(oracle):
     h = y.copy()
     H.elementwise(oracle, "fh3_oracle_", "gate_residual", h, np.zeros_like(y), z, 2, dim)
     assert np.array_equal(h, y)
+
+
+# --------------------------------------------------------------------------
+# The reference's own op fixtures (tests/unit/test_ops.c: check_close <= 1e-5)
+# --------------------------------------------------------------------------
+def test_elementwise_fixtures(oracle):
+    f = H.read_ops_fixture("rmsnorm")
+    x = f["x"].copy()
+    H.elementwise(oracle, "fh3_oracle_", "rmsnorm", x, f["w"], f["n"], f["dim"], f["eps"])
+    assert H.check_close(x, f["ref"]) <= 1e-5
+    f = H.read_ops_fixture("modulate")
+    x = f["x"].copy()
+    H.elementwise(oracle, "fh3_oracle_", "modulate", x, f["shift"], f["scale"], f["n"], f["dim"])
+    assert H.check_close(x, f["ref"]) <= 1e-5
+    # the plausible slip x*scale + shift fails it (test_ops.c's own invariant)
+    assert H.check_close(f["x"] * f["scale"] + f["shift"], f["ref"]) > 1.0
+    f = H.read_ops_fixture("gate_residual")
+    h = f["h"].copy()
+    H.elementwise(oracle, "fh3_oracle_", "gate_residual", h, f["gate"], f["y"], f["n"], f["dim"])
+    assert H.check_close(h, f["ref"]) <= 1e-5
+    f = H.read_ops_fixture("swiglu")
+    out = np.zeros_like(f["ref"])
+    H.elementwise(oracle, "fh3_oracle_", "swiglu", f["inp"], out, f["n"], f["F"])
+    assert H.check_close(out, f["ref"]) <= 1e-5
+    swapped = np.ascontiguousarray(np.concatenate([f["inp"][:, f["F"]:], f["inp"][:, :f["F"]]], axis=1))
+    H.elementwise(oracle, "fh3_oracle_", "swiglu", swapped, out, f["n"], f["F"])
+    assert H.check_close(out, f["ref"]) > 1.0
+
+
+def test_rope3_fixture(oracle):
+    f = H.read_ops_fixture("rope3")
+    n, heads, hd, rot = f["n"], f["heads"], f["hd"], f["rot"]
+    x = f["x"].copy()
+    H.elementwise(oracle, "fh3_oracle_", "rope3", x, f["cos"], f["sin"], n, heads, hd, rot)
+    assert H.check_close(x, f["ref"]) <= 1e-5
+    assert np.array_equal(x[..., rot:], f["x"][..., rot:])      # channels past rot_dim untouched
+    # rotating all 128 channels (cos 1, sin 0 past 96) must fail, as test_ops.c checks
+    c = np.concatenate([f["cos"], np.ones((n, hd - rot), np.float32)], axis=1)
+    s = np.concatenate([f["sin"], np.zeros((n, hd - rot), np.float32)], axis=1)
+    xb = f["x"].copy()
+    H.elementwise(oracle, "fh3_oracle_", "rope3", xb, np.ascontiguousarray(c), np.ascontiguousarray(s),
+                  n, heads, hd, hd)
+    assert np.abs(xb - f["ref"]).max() > 1.0
+
+
+def test_attention_fixture(oracle):
+    """attention.bin (n = 777: not a multiple of the 64-key tile), reduced to
+    heads 0 and 3 and every fourth query by make_ops_fixtures.py."""
+    f = H.read_ops_fixture("attention_sub")
+    o = np.zeros_like(f["ref"])
+    oracle.fh3_oracle_attention_rows(H._ptr(f["q"]), f["nq"], H._ptr(f["k"]), H._ptr(f["v"]), f["n"],
+                                     H._ptr(o), f["heads"], f["hd"])
+    assert H.check_close(o, f["ref"]) <= 1e-5
+    assert f["q_idx"][-1] == f["n"] - 1          # the last query row is covered
+
+
+@pytest.mark.parametrize("n,heads,hd", [(130, 2, 128), (70, 3, 75), (1, 1, 8), (64, 1, 64)])
+def test_attention_rope3_bitwise_vs_reference_build(oracle, ref, n, heads, hd):
+    rng = np.random.default_rng(n + hd)
+    q, k, v = ((rng.standard_normal((n, heads, hd)) * 1.5).astype(np.float32) for _ in range(3))
+    outs = []
+    for lib, pre in ((oracle, "fh3_oracle_"), (ref, "fh3_")):
+        o = np.zeros_like(q)
+        H.elementwise(lib, pre, "attention", q, k, v, o, n, heads, hd)
+        outs.append(o)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    rot = hd - hd % 4 if hd >= 4 else 2
+    cos = rng.standard_normal((n, rot)).astype(np.float32)
+    sin = rng.standard_normal((n, rot)).astype(np.float32)
+    xs = []
+    for lib, pre in ((oracle, "fh3_oracle_"), (ref, "fh3_")):
+        x = q.copy()
+        H.elementwise(lib, pre, "rope3", x, cos, sin, n, heads, hd, rot)
+        xs.append(x)
+    assert np.array_equal(xs[0].view(np.uint32), xs[1].view(np.uint32))
+
+
+def test_attention_closed_forms(oracle):
+    """One key: o = v exactly.  Identical keys: uniform weights, o = mean(v).
+    A key whose score dominates by far: o = its v."""
+    hd, heads = 64, 2
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((1, heads, hd)).astype(np.float32)
+    v1 = rng.standard_normal((1, heads, hd)).astype(np.float32)
+    o = np.zeros_like(q)
+    oracle.fh3_oracle_attention_rows(H._ptr(q), 1, H._ptr(q), H._ptr(v1), 1, H._ptr(o), heads, hd)
+    assert np.array_equal(o, v1)
+    n = 150
+    kk = np.repeat(rng.standard_normal((1, heads, hd)).astype(np.float32), n, axis=0)
+    vv = rng.standard_normal((n, heads, hd)).astype(np.float32)
+    oracle.fh3_oracle_attention_rows(H._ptr(q), 1, H._ptr(kk), H._ptr(vv), n, H._ptr(o), heads, hd)
+    assert np.allclose(o[0], vv.mean(axis=0), rtol=1e-5, atol=1e-6)
+    kd = rng.standard_normal((n, heads, hd)).astype(np.float32) * 0.01
+    kd[97] = q[0] * 50.0
+    oracle.fh3_oracle_attention_rows(H._ptr(q), 1, H._ptr(kd), H._ptr(vv), n, H._ptr(o), heads, hd)
+    assert np.allclose(o[0], vv[97], rtol=1e-6, atol=1e-6)

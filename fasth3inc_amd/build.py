@@ -27,7 +27,7 @@ HIPCC = os.environ.get("HIPCC", "hipcc")
 CC = os.environ.get("CC", "gcc")
 
 C_SOURCES = ["fh3_synth.c", "fh3_pack.c", "fh3_trunk.c"]
-HIP_SOURCES = ["fh3_kernels.hip", "fh3_hip.cpp"]
+HIP_SOURCES = ["fh3_kernels.hip", "fh3_attn.hip", "fh3_hip.cpp"]
 
 C_FLAGS = ["-std=gnu99", "-O3", "-fPIC", "-fopenmp", "-Wall", "-Wextra", "-D_GNU_SOURCE",
            "-ffp-contract=off", "-I" + INC, "-I" + CSRC]

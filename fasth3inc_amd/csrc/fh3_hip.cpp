@@ -32,6 +32,7 @@ struct State {
     DevBuf ws;                      // x16 fragments + per-row scales
     DevBuf ws2;                     // x16 made from a prepared fp32 copy (other weight types)
     DevBuf w16;                     // fp16 rows of a weight of another type
+    DevBuf attn;                    // fp16 attention operands (Qp, Kp, Vt)
     DevBuf st_w, st_x, st_y, st_b;  // staging for the host-pointer wrappers
     int path = FH3_HIP_PATH_AUTO;
     std::recursive_mutex mu;
@@ -195,7 +196,7 @@ extern "C" void fh3_hip_shutdown(void) {
     std::lock_guard<std::recursive_mutex> lk(g.mu);
     if (!g.init) return;
     (void)hipDeviceSynchronize();
-    DevBuf *bufs[] = {&g.ws, &g.ws2, &g.w16, &g.st_w, &g.st_x, &g.st_y, &g.st_b};
+    DevBuf *bufs[] = {&g.ws, &g.ws2, &g.w16, &g.attn, &g.st_w, &g.st_x, &g.st_y, &g.st_b};
     for (DevBuf *b : bufs) {
         if (b->p) (void)hipFree(b->p);
         b->p = nullptr;
@@ -546,6 +547,49 @@ extern "C" int fh3_hip_rownorm_dev(const float *d_x, int n_tok, int64_t in, cons
 }
 
 // ---------------------------------------------------------------------------
+// Attention (fh3_attn.hip)
+// ---------------------------------------------------------------------------
+static int attention_dev(const float *q, const float *k, const float *v, int64_t ld, int n, int heads, int hd,
+                         const float *qn_w, const float *kn_w, float eps, const float *cs, const float *sn, int rot,
+                         float *d_o, void *stream, const char *fn) {
+    if (!q || !k || !v || !d_o || n <= 0 || heads <= 0 || hd <= 0)
+        return set_err(FH3_E_INVALID, "%s: NULL pointer or non-positive size", fn);
+    if (!fh3k_attn_head_dim_ok(hd))
+        return set_err(FH3_E_INVALID, "%s: head_dim %d is not supported (64 or 128)", fn, hd);
+    if ((cs == nullptr) != (sn == nullptr) || (cs && (rot <= 0 || rot > hd || rot % 2)))
+        return set_err(FH3_E_INVALID, "%s: rope needs cos and sin with an even rot_dim <= head_dim", fn);
+    if ((uintptr_t)q & 15u || (uintptr_t)k & 15u || (uintptr_t)v & 15u || (uintptr_t)d_o & 15u)
+        return set_err(FH3_E_INVALID, "%s: q, k, v and o must be 16-byte aligned", fn);
+    if ((int64_t)heads * hd > ((int64_t)1 << 30) || (int64_t)n > ((int64_t)1 << 30) / heads)
+        return set_err(FH3_E_INVALID, "%s: n * heads too large", fn);
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    std::lock_guard<std::recursive_mutex> lk(g.mu);
+    if ((rc = grow(g.attn, fh3k_attn_ws_bytes(n, heads, hd))) != FH3_OK) return rc;
+    FH3_HIPCALL(fh3k_attention(q, k, v, ld, n, heads, hd, qn_w, kn_w, eps, cs, sn, cs ? rot : 0, g.attn.p, d_o,
+                               (int64_t)heads * hd, stream ? (hipStream_t)stream : g.stream));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_attention_dev(const float *d_q, const float *d_k, const float *d_v, float *d_o, int n,
+                                     int heads, int hd, void *stream) {
+    return attention_dev(d_q, d_k, d_v, (int64_t)heads * hd, n, heads, hd, nullptr, nullptr, 0.f, nullptr, nullptr,
+                         0, d_o, stream, "fh3_hip_attention_dev");
+}
+
+extern "C" int fh3_hip_attention_qkv_dev(const float *d_qkv, int n, int heads, int hd, const float *d_qnorm_w,
+                                         const float *d_knorm_w, float eps, const float *d_cos, const float *d_sin,
+                                         int rot_dim, float *d_o, void *stream) {
+    const char *fn = "fh3_hip_attention_qkv_dev";
+    if (!d_qkv) return set_err(FH3_E_INVALID, "%s: NULL qkv", fn);
+    if ((d_qnorm_w == nullptr) != (d_knorm_w == nullptr))
+        return set_err(FH3_E_INVALID, "%s: give both q and k norm weights or neither", fn);
+    const int64_t inner = (int64_t)heads * hd;
+    return attention_dev(d_qkv, d_qkv + inner, d_qkv + 2 * inner, 3 * inner, n, heads, hd, d_qnorm_w, d_knorm_w, eps,
+                         d_cos, d_sin, rot_dim, d_o, stream, fn);
+}
+
+// ---------------------------------------------------------------------------
 // fh3.h host-pointer wrappers
 // ---------------------------------------------------------------------------
 extern "C" size_t fh3_row_bytes(int type, int64_t n) {
@@ -632,6 +676,25 @@ extern "C" void fh3_matmul(const Fh3W *w, const float *x, float *y, int n_tok, c
     e = hipStreamSynchronize(g.stream);
     if (e == hipSuccess) e = hipMemcpy(y, g.st_y.p, yb, hipMemcpyDeviceToHost);
     if (e != hipSuccess) report("fh3_matmul", hip_fail(e, "fh3_matmul download"));
+}
+
+extern "C" void fh3_attention(const float *q, const float *k, const float *v, float *o, int n, int heads, int hd) {
+    if (!q || !k || !v || !o || n <= 0 || heads <= 0 || hd <= 0) return;
+    int rc = ensure_init();
+    if (rc != FH3_OK) { report("fh3_attention", rc); return; }
+    std::lock_guard<std::recursive_mutex> lk(g.mu);
+    const size_t b = (size_t)n * (size_t)heads * (size_t)hd * sizeof(float);
+    if ((rc = grow(g.st_w, 3 * b)) || (rc = grow(g.st_y, b))) { report("fh3_attention", rc); return; }
+    float *dq = (float *)g.st_w.p, *dk = dq + b / 4, *dv = dk + b / 4;
+    hipError_t e = hipMemcpy(dq, q, b, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dk, k, b, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dv, v, b, hipMemcpyHostToDevice);
+    if (e != hipSuccess) { report("fh3_attention", hip_fail(e, "fh3_attention upload")); return; }
+    rc = fh3_hip_attention_dev(dq, dk, dv, (float *)g.st_y.p, n, heads, hd, nullptr);
+    if (rc != FH3_OK) { report("fh3_attention", rc); return; }
+    e = hipStreamSynchronize(g.stream);
+    if (e == hipSuccess) e = hipMemcpy(o, g.st_y.p, b, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) report("fh3_attention", hip_fail(e, "fh3_attention download"));
 }
 
 extern "C" void fh3_matmul_scalar(const Fh3W *w, const float *x, float *y, int n_tok, const float *bias_or_null) {

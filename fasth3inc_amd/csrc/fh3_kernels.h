@@ -73,6 +73,19 @@ hipError_t fh3k_xprep_norm(const float *x, int M, int K, int Mpad, void *x16, fl
 hipError_t fh3k_rownorm_f32(const float *x, int M, int K, float *y, const float *norm_w, float eps,
                             const float *shift, const float *scale, hipStream_t st);
 
+// Attention (fh3_attn.hip).  q, k, v: fp32 rows [n][heads][hd] at token
+// stride ld (16-byte aligned, ld % 4 == 0), e.g. read in place from a qkv
+// projection output; o: [n][heads][hd] at token stride o_ld.  Optional
+// per-head rmsnorm of q and k (weights [hd], eps) and rope3 on their first rot
+// channels (cos/sin [n][rot]).  ws holds fh3k_attn_ws_bytes(n, heads, hd).
+// hd must pass fh3k_attn_head_dim_ok.
+int64_t fh3k_attn_pad(int n);
+size_t fh3k_attn_ws_bytes(int n, int heads, int hd);
+int fh3k_attn_head_dim_ok(int hd);
+hipError_t fh3k_attention(const float *q, const float *k, const float *v, int64_t ld, int n, int heads, int hd,
+                          const float *qn_w, const float *kn_w, float eps, const float *cosb, const float *sinb,
+                          int rot, void *ws, float *o, int64_t o_ld, hipStream_t st);
+
 // Largest in-dimension (K) the activation preparation handles.
 int fh3k_max_in(void);
 

@@ -127,6 +127,7 @@ SIGNATURES = {
     "fh3_matmul_scalar": (None, [ctypes.POINTER(Fh3W), _c_void_p, _c_void_p, _c_int, _c_void_p]),
     "fh3_matmul_avx2": (None, [ctypes.POINTER(Fh3W), _c_void_p, _c_void_p, _c_int, _c_void_p]),
     "fh3_rng_normal": (None, [_c_u64, _c_u64, _c_void_p, _c_size]),
+    "fh3_attention": (None, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int]),
     # fh3_hip.h
     "fh3_hip_init": (_c_int, [_c_int]),
     "fh3_hip_shutdown": (None, []),
@@ -153,6 +154,10 @@ SIGNATURES = {
                                         _c_void_p, _c_void_p]),
     "fh3_hip_matmul_prepared_epi_dev": (_c_int, [ctypes.POINTER(Fh3W), _c_void_p, _c_int, _c_void_p, _c_int,
                                                  _c_void_p, _c_void_p, _c_void_p]),
+    "fh3_hip_attention_dev": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+                                       _c_void_p]),
+    "fh3_hip_attention_qkv_dev": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_void_p, ctypes.c_float,
+                                           _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p]),
     "fh3_hip_graph_begin": (_c_int, [_c_void_p]),
     "fh3_hip_graph_end": (_c_int, [_c_void_p, ctypes.POINTER(_c_void_p)]),
     "fh3_hip_graph_launch": (_c_int, [_c_void_p, _c_void_p]),
@@ -378,6 +383,30 @@ def matmul_prepared_epi_dev(d_w, K, N, d_prep, n_tok, epi, d_out, d_aux=None, d_
     _check(lib().fh3_hip_matmul_prepared_epi_dev(ctypes.byref(w), _ptr_of(d_prep), n_tok, _ptr_of(d_bias), epi,
                                                  _ptr_of(d_aux), _ptr_of(d_out), stream_ptr),
            "fh3_hip_matmul_prepared_epi_dev")
+
+
+def attention_dev(d_q, d_k, d_v, d_o, n, heads, hd, stream_ptr=None):
+    """fh3_hip_attention_dev: dense attention over [n][heads][hd] device rows."""
+    _check(lib().fh3_hip_attention_dev(_ptr_of(d_q), _ptr_of(d_k), _ptr_of(d_v), _ptr_of(d_o), n, heads, hd,
+                                       stream_ptr), "fh3_hip_attention_dev")
+
+
+def attention_qkv_dev(d_qkv, n, heads, hd, d_o, d_qnorm_w=None, d_knorm_w=None, eps=1e-5, d_cos=None, d_sin=None,
+                      rot_dim=0, stream_ptr=None):
+    """fh3_hip_attention_qkv_dev: q/k rmsnorm + rope3 + attention read in place
+    from a qkv projection output [n][3*heads*hd]."""
+    _check(lib().fh3_hip_attention_qkv_dev(_ptr_of(d_qkv), n, heads, hd, _ptr_of(d_qnorm_w), _ptr_of(d_knorm_w),
+                                           eps, _ptr_of(d_cos), _ptr_of(d_sin), rot_dim, _ptr_of(d_o), stream_ptr),
+           "fh3_hip_attention_qkv_dev")
+
+
+def attention_host(q, k, v):
+    """fh3_attention on host arrays [n][heads][hd] (staged through the GPU)."""
+    q, k, v = (np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v))
+    o = np.full_like(q, np.nan)
+    n, heads, hd = q.shape
+    lib().fh3_attention(_p(q), _p(k), _p(v), _p(o), n, heads, hd)
+    return o
 
 
 class Graph:

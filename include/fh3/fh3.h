@@ -102,6 +102,16 @@ void fh3_matmul(const Fh3W *w, const float *x, float *y, int n_tok, const float 
 void fh3_matmul_scalar(const Fh3W *w, const float *x, float *y, int n_tok, const float *bias_or_null);
 void fh3_matmul_avx2(const Fh3W *w, const float *x, float *y, int n_tok, const float *bias_or_null);
 
+/* Dense attention on host buffers q, k, v, o [n][heads][hd], computed on the
+ * GPU (copied in and out on every call): softmax(q.k^T / sqrt(hd)) v over all
+ * n keys per head, no mask.  NULL pointers or non-positive sizes are a silent
+ * no-op, as in the reference; head dims other than 64 and 128 print
+ * "not supported" and leave o unwritten.  fp16 operands with fp32
+ * accumulation and an fp32 online softmax: within rel-Frobenius 2e-3 of the
+ * CPU result.  Replaces src/core/fh3_ops.c:589-695 (declared at
+ * include/fh3/fh3.h:117 there). */
+void fh3_attention(const float *q, const float *k, const float *v, float *o, int n, int heads, int hd);
+
 /* Seeded N(0,1) fp32 generator: Philox4x32-10 (Salmon et al., SC'11) with
  * Box-Muller, one counter per 4 outputs.  Same stream layout as the
  * reference's fh3_rng_normal (src/model/fh3_sched.c:110-159); used to build

@@ -116,6 +116,30 @@ int fh3_hip_matmul_epi_dev(const Fh3W *w, const float *d_x, int n_tok, const flo
 int fh3_hip_matmul_prepared_epi_dev(const Fh3W *w, const void *d_prep, int n_tok, const float *d_bias_or_null,
                                     int epi, const float *d_aux, float *d_out, void *stream);
 
+/* The DiT block's attention branch (reference src/model/fh3_dit.c:390-411)
+ * on the device.
+ *
+ * fh3_hip_attention_dev: dense attention over device arrays q, k, v, o
+ * [n][heads][hd] (fh3_attention, src/core/fh3_ops.c:589-695).
+ *
+ * fh3_hip_attention_qkv_dev: the same, reading q, k and v in place from the
+ * qkv projection's output d_qkv [n][3 * heads * hd] (no split copies, cf.
+ * fh3_dit.c:390-395), with q and k first rmsnorm'ed per head by d_qnorm_w /
+ * d_knorm_w [hd] and eps (both or neither; fh3_dit.c:397-398) and rotated by
+ * rope3 on their first rot_dim channels with d_cos / d_sin [n][rot_dim] (both
+ * or neither; fh3_rope3, src/core/fh3_ops.c:458-505; fh3_dit.c:400-401).
+ *
+ * hd must be 64 or 128; pointers 16-byte aligned.  Operands are fp16 with
+ * fp32 accumulation and an fp32 online softmax (rel-Frobenius <= 2e-3 against
+ * the CPU sequence).  The fp16 operands live in a library workspace
+ * (6 * heads * round_up(n, 128) * hd bytes): calls that overlap on different
+ * streams must not share it. */
+int fh3_hip_attention_dev(const float *d_q, const float *d_k, const float *d_v, float *d_o, int n, int heads,
+                          int hd, void *stream);
+int fh3_hip_attention_qkv_dev(const float *d_qkv, int n, int heads, int hd, const float *d_qnorm_w,
+                              const float *d_knorm_w, float eps, const float *d_cos, const float *d_sin, int rot_dim,
+                              float *d_o, void *stream);
+
 /* HIP graph capture of work enqueued on a stream (NULL = the compute
  * stream), for launch-bound loops such as small-M text-encoder layers:
  * begin, enqueue fh3_hip_* calls on that stream, end -> an executable graph

@@ -245,6 +245,43 @@ def dit_blocks_streamed(ev, st, n_blocks=8, M=16384, passes=2):
         os.unlink(path)
 
 
+def dit_attention(ev, st, n=16384, heads=40, hd=128, rot=96):
+    """The DiT block's attention branch at the block shapes (hidden 5120 = 40
+    heads of 128, n = 16384 tokens): fh3_hip_attention_qkv_dev reading q, k,
+    v in place from a qkv projection output, with per-head q/k rmsnorm and
+    rope3 on 96 channels (k_attn_prep), then the online-softmax product
+    (k_attn_fwd).  FLOP = 4 n^2 hd heads (Q K^T and P V)."""
+    inner = heads * hd
+    qkv = F.DeviceBuffer.from_array(F.synth_x("normal", 3, 600, n, 3 * inner))
+    w = F.DeviceBuffer.from_array(np.ones(hd, np.float32))
+    ang = np.outer(np.arange(n, dtype=np.float64), 1e-2 * np.arange(1, rot // 2 + 1))
+    ang = np.concatenate([ang, ang], axis=1)
+    cs = F.DeviceBuffer.from_array(np.cos(ang).astype(np.float32))
+    sn = F.DeviceBuffer.from_array(np.sin(ang).astype(np.float32))
+    o = F.DeviceBuffer(n * inner * 4)
+    try:
+        def call(i):
+            F.attention_qkv_dev(qkv, n, heads, hd, o, w, w, 1e-5, cs, sn, rot)
+        for i in range(3):
+            call(i)
+        F.synchronize()
+        ms = ev.time_ms(call, 5, st)
+        flop = 4.0 * n * n * hd * heads
+        ach = flop / (ms * 1e-3)
+        res = {"n": n, "heads": heads, "head_dim": hd, "rot_dim": rot, "call_ms": round(ms, 4),
+               "TFLOPs": round(ach / 1e12, 1)}
+        roof = {"bound": "mfma", "achieved": round(ach / 1e12, 1), "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
+                "frac": round(ach / MFMA_F16_PEAK, 4), "traffic": None,
+                "kernel": "k_attn_prep + k_attn_fwd (fh3_hip_attention_qkv_dev)",
+                "note": "4*n^2*hd*heads per call over the call time (both launches); fp16 operands, fp32 "
+                        "accumulation and softmax; peak is dense fp16 MFMA"}
+        log("[bench] DiT attention n=%d heads=%d: %.3f ms (%.1f TFLOP/s)" % (n, heads, ms, ach / 1e12))
+        return res, roof
+    finally:
+        for b in (qkv, w, cs, sn, o):
+            b.close()
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline
 # ---------------------------------------------------------------------------
@@ -433,6 +470,14 @@ def main():
         extra["dit_mlp_linears_ms"] = round(sum(g["call_ms"] for g in mlp), 4)
     extra["gemv"] = per_gemv
 
+    # ---------------- DiT attention branch ---------------------------------
+    roofline_attn = None
+    try:
+        extra["dit_attention"], roofline_attn = dit_attention(ev, st)
+    except Exception as e:  # keep the headline line when this leg fails
+        log("[bench] DiT attention failed: %r" % (e,))
+        extra["dit_attention"] = {"error": repr(e)}
+
     # ---------------- DiT blocks streamed through the trunk ----------------
     if not args.no_stream:
         try:
@@ -460,6 +505,7 @@ def main():
                                "device copies", "parallelism": "single GPU"},
         "roofline": roofline,
         "roofline_gemm": roofline_gemm,
+        "roofline_attention": roofline_attn,
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -28,12 +28,18 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 constexpr int ATT_KT = 64;   // keys per tile
 constexpr int ATT_QW = 32;   // queries per wavefront
 constexpr int ATT_NW = 4;    // wavefronts per workgroup
 constexpr int ATT_QB = ATT_QW * ATT_NW;
 constexpr int ATT_PREP_T = 64;  // slots per prep workgroup
+// The softmax offset m of a query is only raised when a tile's maximum
+// exceeds it by more than ATT_TAU (log2 units), so p = exp2(s - m) <= 2^8 and
+// the rescale of the accumulators is skipped on almost every tile.  Any offset
+// gives the same o = sum(p v) / sum(p); fp16 holds p up to 65504.
+constexpr float ATT_TAU = 8.0f;
 
 // Order of the keys inside each 16-key block of Vt.  The P^T operand of the
 // PV product is taken straight from the S^T accumulator, where lane half hf
@@ -91,7 +97,25 @@ __global__ __launch_bounds__(256) void k_attn_prep(const float *__restrict__ q, 
             for (int i = 0; i < DPT; i++) sx[r][d0 + i] = x[i];
             __syncthreads();
             const int half = rot >> 1;
-            if (tok >= 0) {
+            if (tok >= 0 && (rot & 7) == 0) {
+                // 4-element chunks never straddle half or rot: one region
+                // test, and 16-byte reads of the tables and the partner chunk
+                const float *cr = cosb + (size_t)tok * rot, *sr = sinb + (size_t)tok * rot;
+#pragma unroll
+                for (int i = 0; i < DPT / 4; i++) {
+                    const int d = d0 + 4 * i;
+                    if (d < rot) {
+                        const bool lo = d < half;
+                        const f32x4 cv = *(const f32x4 *)(cr + d), sv = *(const f32x4 *)(sr + d);
+                        const f32x4 pv = *(const f32x4 *)&sx[r][lo ? d + half : d - half];
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const float a = x[4 * i + e] * cv[e], b = pv[e] * sv[e];
+                            x[4 * i + e] = lo ? a - b : a + b;
+                        }
+                    }
+                }
+            } else if (tok >= 0) {
                 const float *cr = cosb + (size_t)tok * rot, *sr = sinb + (size_t)tok * rot;
 #pragma unroll
                 for (int i = 0; i < DPT; i++) {
@@ -248,29 +272,37 @@ __global__ __launch_bounds__(256, 2) void k_attn_fwd(const _Float16 *__restrict_
 #pragma unroll
         for (int v = 0; v < 16; v++) mt = fmaxf(mt, s[1][v]);
         mt = wave_swap_max(mt);
-        const float mn = fmaxf(m, mt);
-        const float alpha = __builtin_amdgcn_exp2f(m - mn);
-        m = mn;
-        float ps = 0.f;
+        const bool grow = mt > m + ATT_TAU;
+        if (__ballot(grow)) {  // wave-uniform: some query's offset must rise
+            const float mn = grow ? mt : m;
+            const float alpha = __builtin_amdgcn_exp2f(m - mn);
+            m = mn;
+            lsum *= alpha;
+#pragma unroll
+            for (int i = 0; i < DB; i++) o[i] *= alpha;
+        }
 #pragma unroll
         for (int st = 0; st < 2; st++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                s[st][v] = __builtin_amdgcn_exp2f(s[st][v] - mn);
-                ps += s[st][v];
-            }
-        lsum = lsum * alpha + ps;
-#pragma unroll
-        for (int i = 0; i < DB; i++) o[i] *= alpha;
+            for (int v = 0; v < 16; v++) s[st][v] = __builtin_amdgcn_exp2f(s[st][v] - m);
 
         // P^T fragments: 16-key step t = values 4g..4g+7 of accumulator t/2,
-        // g = 2 (t % 2); they pair with V^T stored in the vt_key order
+        // g = 2 (t % 2); they pair with V^T stored in the vt_key order.  The
+        // row sum is taken over the same fp16 values the product uses.
         half8 pf[4];
 #pragma unroll
         for (int tt = 0; tt < 4; tt++) {
 #pragma unroll
             for (int e = 0; e < 8; e++) pf[tt][e] = (_Float16)s[tt >> 1][8 * (tt & 1) + e];
         }
+        float ps[2] = {0.f, 0.f};
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                ps[e & 1] = __builtin_amdgcn_fdot2(half2v{pf[tt][2 * e], pf[tt][2 * e + 1]}, half2v{1, 1},
+                                                   ps[e & 1], false);
+        lsum += ps[0] + ps[1];
 #pragma unroll
         for (int db = 0; db < DB; db++) {
 #pragma unroll

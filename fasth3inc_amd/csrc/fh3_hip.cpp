@@ -558,8 +558,9 @@ static int attention_dev(const float *q, const float *k, const float *v, int64_t
         return set_err(FH3_E_INVALID, "%s: head_dim %d is not supported (64 or 128)", fn, hd);
     if ((cs == nullptr) != (sn == nullptr) || (cs && (rot <= 0 || rot > hd || rot % 2)))
         return set_err(FH3_E_INVALID, "%s: rope needs cos and sin with an even rot_dim <= head_dim", fn);
-    if ((uintptr_t)q & 15u || (uintptr_t)k & 15u || (uintptr_t)v & 15u || (uintptr_t)d_o & 15u)
-        return set_err(FH3_E_INVALID, "%s: q, k, v and o must be 16-byte aligned", fn);
+    if ((uintptr_t)q & 15u || (uintptr_t)k & 15u || (uintptr_t)v & 15u || (uintptr_t)d_o & 15u ||
+        (uintptr_t)cs & 15u || (uintptr_t)sn & 15u)
+        return set_err(FH3_E_INVALID, "%s: q, k, v, o, cos and sin must be 16-byte aligned", fn);
     if ((int64_t)heads * hd > ((int64_t)1 << 30) || (int64_t)n > ((int64_t)1 << 30) / heads)
         return set_err(FH3_E_INVALID, "%s: n * heads too large", fn);
     int rc = ensure_init();

@@ -12,9 +12,15 @@ Workloads (each launch sequence is preceded by one untimed warmup launch):
          fh3_hip_matmul_prepared_dev -> k_gemm, and the activation prep k_xprep
   copy   hipMemcpy device-to-device of 256 MiB: a copy of known size that
          calibrates FETCH_SIZE / WRITE_SIZE against the bytes moved
+  attn   the DiT attention branch at n = 16384 tokens, 40 heads of 128
+         (hidden 5120): fh3_hip_attention_qkv_dev from a qkv projection
+         output with q/k rmsnorm and rope3 on 96 channels -> k_attn_prep,
+         k_attn_fwd
 """
 import argparse
 import sys
+
+import numpy as np
 
 from . import fh3 as F
 
@@ -66,9 +72,26 @@ def copy(reps):
     print("copy %d bytes: %d launches" % (n, reps), flush=True)
 
 
+def attn(reps, n=16384, heads=40, hd=128, rot=96):
+    inner = heads * hd
+    qkv = F.DeviceBuffer.from_array(F.synth_x("normal", 2, 500, n, 3 * inner))
+    w = F.DeviceBuffer.from_array(np.ones(hd, np.float32))
+    ang = np.outer(np.arange(n, dtype=np.float64), 1e-2 * np.arange(1, rot // 2 + 1))
+    ang = np.concatenate([ang, ang], axis=1)
+    cs = F.DeviceBuffer.from_array(np.cos(ang).astype(np.float32))
+    sn = F.DeviceBuffer.from_array(np.sin(ang).astype(np.float32))
+    o = F.DeviceBuffer(n * inner * 4)
+    for _ in range(reps + 1):
+        F.attention_qkv_dev(qkv, n, heads, hd, o, w, w, 1e-5, cs, sn, rot)
+    F.synchronize()
+    print("attn n=%d heads=%d hd=%d: %d launches" % (n, heads, hd, reps), flush=True)
+    for b in (qkv, w, cs, sn, o):
+        b.close()
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("workload", choices=("gemv", "gemm", "copy", "all"))
+    ap.add_argument("workload", choices=("gemv", "gemm", "copy", "attn", "all"))
     ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args(argv)
     F.init(0)

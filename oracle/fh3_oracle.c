@@ -505,3 +505,233 @@ void fh3_oracle_attention_rows(const float *q, int nq, const float *k, const flo
 void fh3_oracle_attention(const float *q, const float *k, const float *v, float *o, int n, int heads, int hd) {
     fh3_oracle_attention_rows(q, n, k, v, n, o, heads, hd);
 }
+
+/* ------------------------------------------------------------------------ */
+/* Video sparse attention (src/core/fh3_vsa.c:31-507).                       */
+/* ------------------------------------------------------------------------ */
+
+/* Tile geometry (src/core/fh3_vsa.c:31-163): text tokens, then audio tokens,
+ * in runs of `tile`; then the video grid (gt, gh, gw) in 4x4x4 cubes, t-major,
+ * tokens of a cube in (t, h, w) order.  Modalities that do not sum to n make
+ * every token video; a grid that does not match the video count becomes
+ * 1 x 1 x V.  Writes tile_tok[n] (token of each position), tile_off[T + 1]
+ * and returns T (or -1); *n_prefix gets the number of text + audio tiles. */
+int fh3_oracle_vsa_geometry(int n, int num_text, int num_audio, int num_video, int grid_t, int grid_h,
+                            int grid_w, int tile, int *tile_tok, int *tile_off, int max_tiles, int *n_prefix) {
+    if (n <= 0) return -1;
+    if (tile <= 0) tile = 64;
+    int T = num_text > 0 ? num_text : 0, A = num_audio > 0 ? num_audio : 0, V = num_video > 0 ? num_video : 0;
+    if (T + A + V != n) T = 0, A = 0, V = n;
+    int gt = grid_t, gh = grid_h, gw = grid_w;
+    if (gt <= 0 || gh <= 0 || gw <= 0 || gt * gh * gw != V) gt = 1, gh = 1, gw = V;
+    int nt = 0, pos = 0;
+    tile_off[0] = 0;
+    const int seg_len[2] = {T, A}, seg_start[2] = {0, T};
+    for (int sgi = 0; sgi < 2; sgi++) {
+        for (int s0 = 0; s0 < seg_len[sgi]; s0 += tile) {
+            const int sz = seg_len[sgi] - s0 < tile ? seg_len[sgi] - s0 : tile;
+            if (nt >= max_tiles) return -1;
+            for (int e = 0; e < sz; e++) tile_tok[pos++] = seg_start[sgi] + s0 + e;
+            tile_off[++nt] = pos;
+        }
+    }
+    *n_prefix = nt;
+    if (V > 0) {
+        const int base = T + A;
+        for (int t0 = 0; t0 < gt; t0 += 4)
+            for (int h0 = 0; h0 < gh; h0 += 4)
+                for (int w0 = 0; w0 < gw; w0 += 4) {
+                    if (nt >= max_tiles) return -1;
+                    for (int t = t0; t < gt && t < t0 + 4; t++)
+                        for (int h = h0; h < gh && h < h0 + 4; h++)
+                            for (int w = w0; w < gw && w < w0 + 4; w++)
+                                tile_tok[pos++] = base + (t * gh + h) * gw + w;
+                    tile_off[++nt] = pos;
+                }
+    }
+    return nt;
+}
+
+typedef struct {
+    float s;
+    int j;
+} OracleTileScore;
+
+/* descending score, then ascending tile index (src/core/fh3_vsa.c:178-184) */
+static int oracle_tile_cmp(const void *a, const void *b) {
+    const OracleTileScore *x = (const OracleTileScore *)a, *y = (const OracleTileScore *)b;
+    if (x->s > y->s) return -1;
+    if (x->s < y->s) return 1;
+    return x->j < y->j ? -1 : (x->j > y->j ? 1 : 0);
+}
+
+/* src/core/fh3_vsa.c:186-507 on [n][heads][hd] rows.  Per tile: mean-pooled
+ * q, k (and v with a gate) accumulated as pool += x * (1/count) in tile order;
+ * tile scores dot(qpool, kpool) * (1/sqrtf(hd)) with separate roundings.
+ * Query tiles of text/audio attend to every tile; a video query tile attends
+ * to every prefix tile plus its top ceil((1 - sparsity) * video tiles) video
+ * tiles (all of them when sparsity <= 0 or that count covers them).  Fine
+ * attention per query over the selected tiles' tokens in tile order: max,
+ * sum of expf, weights p * (1/sum), out += w * v.  With a gate, each tile's
+ * softmax over all tile scores mixes the pooled v, and
+ * o = fine + coarse * gate.  Returns 0, or -1 when the geometry fails. */
+int fh3_oracle_vsa_attention(int tile, float sparsity, const float *q, const float *k, const float *v,
+                             const float *gate, float *o, int n, int num_text, int num_audio, int num_video,
+                             int grid_t, int grid_h, int grid_w, int heads, int hd) {
+    if (!q || !k || !v || !o || n <= 0 || heads <= 0 || hd <= 0) return -1;
+    if (tile <= 0) tile = 64;
+    const int max_tiles = n + 8;
+    int *tok = (int *)malloc((size_t)n * sizeof(int));
+    int *off = (int *)malloc((size_t)(max_tiles + 1) * sizeof(int));
+    int P = 0;
+    const int T = tok && off ? fh3_oracle_vsa_geometry(n, num_text, num_audio, num_video, grid_t, grid_h, grid_w,
+                                                       tile, tok, off, max_tiles, &P)
+                             : -1;
+    if (T <= 0) {
+        free(tok);
+        free(off);
+        return -1;
+    }
+    const int NV = T - P;
+    const size_t TD = (size_t)T * (size_t)hd, HTD = (size_t)heads * TD;
+    float *qp = (float *)calloc(HTD, sizeof(float)), *kp = (float *)calloc(HTD, sizeof(float));
+    float *vp = gate ? (float *)calloc(HTD, sizeof(float)) : NULL;
+    float *sc = (float *)malloc((size_t)heads * (size_t)T * (size_t)T * sizeof(float));
+    uint8_t *sel = (uint8_t *)calloc((size_t)heads * (size_t)T * (size_t)T, 1);
+    float *fine = (float *)calloc((size_t)n * (size_t)heads * (size_t)hd, sizeof(float));
+    int rc = (qp && kp && (!gate || vp) && sc && sel && fine) ? 0 : -1;
+    const float scale = 1.0f / sqrtf((float)hd);
+    if (rc == 0) {
+        /* pooling */
+        for (int i = 0; i < T; i++) {
+            const int cnt = off[i + 1] - off[i];
+            const float inv = 1.0f / (float)cnt;
+            for (int r = 0; r < cnt; r++) {
+                const int t = tok[off[i] + r];
+                for (int h = 0; h < heads; h++) {
+                    const size_t src = ((size_t)t * heads + h) * hd, dst = (size_t)h * TD + (size_t)i * hd;
+                    for (int d = 0; d < hd; d++) {
+                        qp[dst + d] += q[src + d] * inv;
+                        kp[dst + d] += k[src + d] * inv;
+                        if (gate) vp[dst + d] += v[src + d] * inv;
+                    }
+                }
+            }
+        }
+        /* tile scores */
+        for (int h = 0; h < heads; h++)
+            for (int i = 0; i < T; i++)
+                for (int j = 0; j < T; j++) {
+                    const float *a = qp + (size_t)h * TD + (size_t)i * hd, *b = kp + (size_t)h * TD + (size_t)j * hd;
+                    float dot = 0.0f;
+                    for (int d = 0; d < hd; d++) dot += a[d] * b[d];
+                    sc[((size_t)h * T + i) * T + j] = dot * scale;
+                }
+        /* tile selection */
+        int kv = 0;
+        if (NV > 0) {
+            kv = (int)ceilf((1.0f - sparsity) * (float)NV);
+            if (kv < 1) kv = 1;
+            if (kv > NV) kv = NV;
+        }
+        const int all = sparsity <= 0.0f || kv == NV;
+        OracleTileScore *cand = (OracleTileScore *)malloc((size_t)(NV > 0 ? NV : 1) * sizeof(OracleTileScore));
+        if (!cand) rc = -1;
+        for (int h = 0; h < heads && rc == 0; h++)
+            for (int i = 0; i < T; i++) {
+                uint8_t *row = sel + ((size_t)h * T + i) * T;
+                if (i < P || all) {
+                    memset(row, 1, (size_t)T);
+                    continue;
+                }
+                memset(row, 1, (size_t)P);
+                for (int j = 0; j < NV; j++) {
+                    cand[j].s = sc[((size_t)h * T + i) * T + P + j];
+                    cand[j].j = P + j;
+                }
+                qsort(cand, (size_t)NV, sizeof(OracleTileScore), oracle_tile_cmp);
+                for (int e = 0; e < kv; e++) row[cand[e].j] = 1;
+            }
+        free(cand);
+    }
+    if (rc == 0) {
+        /* fine attention */
+        int *kt = (int *)malloc((size_t)n * sizeof(int));
+        float *s = (float *)malloc((size_t)n * sizeof(float)), *p = (float *)malloc((size_t)n * sizeof(float));
+        if (!kt || !s || !p) rc = -1;
+        for (int h = 0; h < heads && rc == 0; h++)
+            for (int i = 0; i < T; i++) {
+                const uint8_t *row = sel + ((size_t)h * T + i) * T;
+                int nk = 0;
+                for (int j = 0; j < T; j++)
+                    if (row[j])
+                        for (int e = off[j]; e < off[j + 1]; e++) kt[nk++] = tok[e];
+                for (int e = off[i]; e < off[i + 1] && nk > 0; e++) {
+                    const int tq = tok[e];
+                    const float *qi = q + ((size_t)tq * heads + h) * hd;
+                    float mx = -1e30f;
+                    for (int m = 0; m < nk; m++) {
+                        const float *kj = k + ((size_t)kt[m] * heads + h) * hd;
+                        float dot = 0.0f;
+                        for (int d = 0; d < hd; d++) dot += qi[d] * kj[d];
+                        s[m] = dot * scale;
+                        if (s[m] > mx) mx = s[m];
+                    }
+                    float sum = 0.0f;
+                    for (int m = 0; m < nk; m++) {
+                        p[m] = expf(s[m] - mx);
+                        sum += p[m];
+                    }
+                    const float inv = 1.0f / sum;
+                    float *out = fine + ((size_t)tq * heads + h) * hd;
+                    for (int m = 0; m < nk; m++) {
+                        const float w = p[m] * inv;
+                        const float *vj = v + ((size_t)kt[m] * heads + h) * hd;
+                        for (int d = 0; d < hd; d++) out[d] += w * vj[d];
+                    }
+                }
+            }
+        free(kt);
+        free(s);
+        free(p);
+    }
+    if (rc == 0) {
+        const size_t total = (size_t)n * (size_t)heads * (size_t)hd;
+        if (!gate) {
+            memcpy(o, fine, total * sizeof(float));
+        } else {
+            float *oc = (float *)malloc((size_t)hd * sizeof(float));
+            if (!oc) rc = -1;
+            for (int i = 0; i < T && rc == 0; i++)
+                for (int h = 0; h < heads; h++) {
+                    const float *srow = sc + ((size_t)h * T + i) * T;
+                    float mx = -1e30f;
+                    for (int j = 0; j < T; j++)
+                        if (srow[j] > mx) mx = srow[j];
+                    float sum = 0.0f;
+                    for (int j = 0; j < T; j++) sum += expf(srow[j] - mx);
+                    const float inv = 1.0f / sum;
+                    memset(oc, 0, (size_t)hd * sizeof(float));
+                    for (int j = 0; j < T; j++) {
+                        const float w = expf(srow[j] - mx) * inv;
+                        const float *pv = vp + (size_t)h * TD + (size_t)j * hd;
+                        for (int d = 0; d < hd; d++) oc[d] += w * pv[d];
+                    }
+                    for (int e = off[i]; e < off[i + 1]; e++) {
+                        const size_t at = ((size_t)tok[e] * heads + h) * hd;
+                        for (int d = 0; d < hd; d++) o[at + d] = fine[at + d] + oc[d] * gate[at + d];
+                    }
+                }
+            free(oc);
+        }
+    }
+    free(tok);
+    free(off);
+    free(qp);
+    free(kp);
+    free(vp);
+    free(sc);
+    free(sel);
+    free(fine);
+    return rc;
+}

@@ -81,6 +81,15 @@ void fh3_oracle_attention(const float *q, const float *k, const float *v, float 
 void fh3_oracle_attention_rows(const float *q, int nq, const float *k, const float *v, int nk, float *o,
                                int heads, int hd);
 
+/* Video sparse attention (src/core/fh3_vsa.c): the tile geometry and the
+ * whole call.  The sequence is given by its counts and video grid (the fields
+ * of the reference's Fh3Seq that the call reads). */
+int fh3_oracle_vsa_geometry(int n, int num_text, int num_audio, int num_video, int grid_t, int grid_h,
+                            int grid_w, int tile, int *tile_tok, int *tile_off, int max_tiles, int *n_prefix);
+int fh3_oracle_vsa_attention(int tile, float sparsity, const float *q, const float *k, const float *v,
+                             const float *gate, float *o, int n, int num_text, int num_audio, int num_video,
+                             int grid_t, int grid_h, int grid_w, int heads, int hd);
+
 #ifdef __cplusplus
 }
 #endif

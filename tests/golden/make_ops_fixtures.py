@@ -20,6 +20,13 @@ its own q row and all k/v rows of its head.  attention_sub.bin holds
   <IIII> n (keys), heads (2), hd, nq; int32 head_idx[2]; int32 q_idx[nq];
   q[nq][2][hd], k[n][2][hd], v[n][2][hd], ref[nq][2][hd]
 
+The VSA fixtures (reference tests/fixtures/vsa/*.bin: a 44-byte header
+<IIIIIIIIIfI> n, num_text, num_audio, num_video, grid_t, grid_h, grid_w,
+heads, head_dim, sparsity, has_gate; then q, k, v, [gate], ref, each
+[n][heads][head_dim]) are cut to heads 0 and 3 (heads are independent in
+every step of the call) and written to tests/golden/vsa/<name>.bin with the
+same header (heads = 2).
+
     python tests/golden/make_ops_fixtures.py [/root/reference]
 """
 import os
@@ -33,6 +40,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 COPY = ("rmsnorm", "modulate", "swiglu", "gate_residual", "rope3")
 HEADS = (0, 3)
 QSTEP = 4
+VSA = ("vsa_n784", "vsa_padded", "vsa_sparsity0")
 
 
 def main(ref):
@@ -55,6 +63,21 @@ def main(ref):
             f.write(np.ascontiguousarray(a, dtype="<f4").tobytes())
     print("copied %d fixtures and attention_sub.bin (%d queries, heads %s) into %s"
           % (len(COPY), len(qi), HEADS, dst))
+    vsrc = os.path.join(ref, "tests", "fixtures", "vsa")
+    vdst = os.path.join(HERE, "vsa")
+    os.makedirs(vdst, exist_ok=True)
+    for name in VSA:
+        with open(os.path.join(vsrc, name + ".bin"), "rb") as f:
+            hdr = list(struct.unpack("<IIIIIIIIIfI", f.read(44)))
+            n, heads, hd, has_gate = hdr[0], hdr[7], hdr[8], hdr[10]
+            cnt = 5 if has_gate else 4
+            arr = np.frombuffer(f.read(), dtype="<f4").reshape(cnt, n, heads, hd)
+        hdr[7] = len(HEADS)
+        with open(os.path.join(vdst, name + ".bin"), "wb") as f:
+            f.write(struct.pack("<IIIIIIIIIfI", *hdr))
+            for a in arr:
+                f.write(np.ascontiguousarray(a[:, list(HEADS)], dtype="<f4").tobytes())
+    print("wrote %d VSA fixtures (heads %s) into %s" % (len(VSA), HEADS, vdst))
 
 
 if __name__ == "__main__":

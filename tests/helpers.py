@@ -115,6 +115,71 @@ def read_ops_fixture(name):
     raise ValueError(name)
 
 
+VSA_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "vsa")
+
+
+def read_vsa_fixture(name):
+    """A VSA fixture cut to two heads by tests/golden/make_ops_fixtures.py."""
+    raw = open(os.path.join(VSA_DIR, name + ".bin"), "rb").read()
+    h = struct.unpack("<IIIIIIIIIfI", raw[:44])
+    keys = ("n", "num_text", "num_audio", "num_video", "grid_t", "grid_h", "grid_w", "heads", "head_dim",
+            "sparsity", "has_gate")
+    out = dict(zip(keys, h))
+    n, heads, hd = out["n"], out["heads"], out["head_dim"]
+    cnt = n * heads * hd
+    names = ("q", "k", "v", "gate", "ref") if out["has_gate"] else ("q", "k", "v", "ref")
+    for i, key in enumerate(names):
+        out[key] = np.frombuffer(raw, "<f4", cnt, 44 + 4 * cnt * i).reshape(n, heads, hd).copy()
+    if not out["has_gate"]:
+        out["gate"] = None
+    return out
+
+
+class VsaCfg(ctypes.Structure):      # reference include/fh3/fh3.h:41-44
+    _fields_ = [("tile", ctypes.c_int), ("sparsity", ctypes.c_float)]
+
+
+class Seq(ctypes.Structure):         # reference src/model/fh3_seq.h:32-45
+    _fields_ = [("seq_len", ctypes.c_int), ("num_text", ctypes.c_int), ("num_audio", ctypes.c_int),
+                ("num_video", ctypes.c_int), ("grid_t", ctypes.c_int), ("grid_h", ctypes.c_int),
+                ("grid_w", ctypes.c_int), ("tags", ctypes.c_void_p), ("pair_index", ctypes.c_void_p),
+                ("pos", ctypes.c_void_p), ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p)]
+
+
+def _vsa_args(q, k, v, gate):
+    return [_ptr(np.ascontiguousarray(a, dtype=np.float32)) if a is not None else None for a in (q, k, v, gate)]
+
+
+def vsa_oracle(oracle, q, k, v, gate, seq, sparsity=0.8, tile=64):
+    """fh3_oracle_vsa_attention; seq = (n, num_text, num_audio, num_video, gt, gh, gw)."""
+    q, k, v = (np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v))
+    g = None if gate is None else np.ascontiguousarray(gate, dtype=np.float32)
+    o = np.full_like(q, np.nan)
+    n, heads, hd = q.shape
+    f = oracle.fh3_oracle_vsa_attention
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_int, ctypes.c_float] + [ctypes.c_void_p] * 5 + [ctypes.c_int] * 9
+    rc = f(tile, sparsity, _ptr(q), _ptr(k), _ptr(v), None if g is None else _ptr(g), _ptr(o), *seq, heads, hd)
+    assert rc == 0
+    return o
+
+
+def vsa_ref(ref, q, k, v, gate, seq, sparsity=0.8, tile=64):
+    """The reference build's fh3_vsa_attention."""
+    q, k, v = (np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v))
+    g = None if gate is None else np.ascontiguousarray(gate, dtype=np.float32)
+    o = np.full_like(q, np.nan)
+    n, heads, hd = q.shape
+    cfg = VsaCfg(tile, sparsity)
+    sq = Seq(*seq, None, None, None, None, None)
+    f = ref.fh3_vsa_attention
+    f.restype = None
+    f.argtypes = [ctypes.POINTER(VsaCfg)] + [ctypes.c_void_p] * 5 + [ctypes.POINTER(Seq), ctypes.c_int, ctypes.c_int]
+    f(ctypes.byref(cfg), _ptr(q), _ptr(k), _ptr(v), None if g is None else _ptr(g), _ptr(o), ctypes.byref(sq),
+      heads, hd)
+    return o
+
+
 def check_close(actual, ref):
     """The reference's test_ops.c check_close metric: max |a - r| / max(|r|, 1)."""
     a = np.asarray(actual, np.float64).ravel()

@@ -389,3 +389,73 @@ def test_attention_closed_forms(oracle):
     kd[97] = q[0] * 50.0
     oracle.fh3_oracle_attention_rows(H._ptr(q), 1, H._ptr(kd), H._ptr(vv), n, H._ptr(o), heads, hd)
     assert np.allclose(o[0], vv[97], rtol=1e-6, atol=1e-6)
+
+
+# --------------------------------------------------------------------------
+# Video sparse attention (src/core/fh3_vsa.c; tests/unit/test_vsa.c)
+# --------------------------------------------------------------------------
+def _fix_seq(f):
+    return (f["n"], f["num_text"], f["num_audio"], f["num_video"], f["grid_t"], f["grid_h"], f["grid_w"])
+
+
+@pytest.mark.parametrize("name", ["vsa_n784", "vsa_padded", "vsa_sparsity0"])
+def test_vsa_fixtures(oracle, name):
+    """The reference's three VSA fixtures (rel-L2 <= 1e-5, as test_vsa.c),
+    cut to two heads."""
+    f = H.read_vsa_fixture(name)
+    o = H.vsa_oracle(oracle, f["q"], f["k"], f["v"], f["gate"], _fix_seq(f), f["sparsity"])
+    assert H.rel_fro(o, f["ref"]) <= 1e-5
+
+
+def test_vsa_sparsity0_without_gate_is_dense(oracle):
+    """test_vsa.c's structural check: sparsity 0 and no gate equals dense attention."""
+    f = H.read_vsa_fixture("vsa_sparsity0")
+    o = H.vsa_oracle(oracle, f["q"], f["k"], f["v"], None, _fix_seq(f), 0.0)
+    d = np.zeros_like(o)
+    H.elementwise(oracle, "fh3_oracle_", "attention", f["q"], f["k"], f["v"], d, f["n"], f["heads"], f["head_dim"])
+    assert H.rel_fro(o, d) <= 1e-5
+
+
+VSA_CASES = [
+    # (n, text, audio, video, gt, gh, gw, heads, hd, sparsity, gate)
+    (784, 0, 0, 784, 7, 8, 14, 2, 64, 0.8, True),
+    (268, 35, 23, 210, 5, 6, 7, 3, 64, 0.8, False),
+    (300, 100, 0, 200, 2, 10, 10, 2, 128, 0.5, True),
+    (130, 0, 0, 130, 0, 0, 0, 1, 32, 0.9, True),      # no grid: 1 x 1 x V
+    (90, 40, 10, 41, 2, 2, 10, 2, 16, 0.8, True),     # counts do not sum to n: all video
+    (512, 64, 64, 384, 6, 8, 8, 2, 64, 0.0, True),
+    (1000, 16, 24, 960, 6, 10, 16, 1, 64, 0.95, True),
+]
+
+
+@pytest.mark.parametrize("case", VSA_CASES)
+def test_vsa_bitwise_vs_reference_build(oracle, ref, case):
+    n, T, A, V, gt, gh, gw, heads, hd, sp, has_gate = case
+    rng = np.random.default_rng(n + heads * 10 + hd)
+    q, k, v, g = ((rng.standard_normal((n, heads, hd)) * 0.7).astype(np.float32) for _ in range(4))
+    gate = g if has_gate else None
+    seq = (n, T, A, V, gt, gh, gw)
+    a = H.vsa_oracle(oracle, q, k, v, gate, seq, sp)
+    b = H.vsa_ref(ref, q, k, v, gate, seq, sp)
+    assert np.isfinite(a).all()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_vsa_geometry_closed_form(oracle):
+    """Tiles partition the sequence; text and audio runs come first in runs of
+    64; a full 4x4x4 video cube is 64 consecutive-in-(t,h,w) tokens."""
+    import ctypes
+    n, T, A, gt, gh, gw = 35 + 70 + 8 * 8 * 8, 35, 70, 8, 8, 8
+    tok = np.zeros(n, np.int32)
+    off = np.zeros(n + 9, np.int32)
+    npre = ctypes.c_int()
+    f = oracle.fh3_oracle_vsa_geometry
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_int] * 8 + [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
+    nt = f(n, T, A, n - T - A, gt, gh, gw, 64, H._ptr(tok), H._ptr(off), n + 8, ctypes.byref(npre))
+    assert npre.value == 1 + 2 and nt == 3 + 8
+    assert sorted(tok.tolist()) == list(range(n))
+    assert list(off[:4]) == [0, 35, 99, 105]
+    cube = tok[off[3]:off[4]] - (T + A)
+    t, h, w = cube // 64, (cube // 8) % 8, cube % 8
+    assert (t < 4).all() and (h < 4).all() and (w < 4).all() and len(cube) == 64

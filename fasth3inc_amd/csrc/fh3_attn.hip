@@ -50,15 +50,19 @@ __device__ __forceinline__ int vt_key(int p) {
     return (p & ~15) + ((b & 3) | ((b & 4) << 1) | ((b & 8) >> 1));
 }
 
-template <int HD>
+// F32OUT: write the normalised / rotated q and k as fp32 rows
+// Qf/Kf[slot][h][d] (token order, stride heads * HD) instead of the fp16
+// operands, and leave v alone -- the inputs of the VSA tile statistics.
+template <int HD, bool F32OUT>
 __global__ __launch_bounds__(256) void k_attn_prep(const float *__restrict__ q, const float *__restrict__ k,
-                                                   const float *__restrict__ v, int64_t ld, int n,
+                                                   const float *__restrict__ v, int64_t ld, int64_t ldv, int n,
                                                    const int *__restrict__ gather,
                                                    const float *__restrict__ qn_w, const float *__restrict__ kn_w,
                                                    float eps, const float *__restrict__ cosb,
                                                    const float *__restrict__ sinb, int rot, float qscale,
                                                    int n_pad, _Float16 *__restrict__ Qp, _Float16 *__restrict__ Kp,
-                                                   _Float16 *__restrict__ Vt) {
+                                                   _Float16 *__restrict__ Vt, float *__restrict__ Qf,
+                                                   float *__restrict__ Kf, int heads) {
     constexpr int DPT = HD / 4;
     __shared__ float sx[ATT_PREP_T][HD + 4];
     const int t = threadIdx.x, r = t >> 2, c = t & 3;
@@ -130,6 +134,14 @@ __global__ __launch_bounds__(256) void k_attn_prep(const float *__restrict__ q, 
                 }
             }
         }
+        if (F32OUT) {
+            if (tok >= 0) {
+                f32x4 *dst = (f32x4 *)((which ? Kf : Qf) + ((size_t)tok * heads + h) * HD + d0);
+#pragma unroll
+                for (int i = 0; i < DPT / 4; i++) dst[i] = f32x4{x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]};
+            }
+            continue;
+        }
         if (!which) {
 #pragma unroll
             for (int i = 0; i < DPT; i++) x[i] *= qscale;
@@ -144,10 +156,11 @@ __global__ __launch_bounds__(256) void k_attn_prep(const float *__restrict__ q, 
         }
     }
 
+    if (F32OUT) return;
     // v: through LDS, written transposed in the vt_key order
     __syncthreads();
     if (tok >= 0) {
-        const f32x4 *p = (const f32x4 *)(v + (size_t)tok * ld + (size_t)h * HD + d0);
+        const f32x4 *p = (const f32x4 *)(v + (size_t)tok * ldv + (size_t)h * HD + d0);
 #pragma unroll
         for (int i = 0; i < DPT / 4; i++) {
             const f32x4 u = p[i];
@@ -174,11 +187,30 @@ __global__ __launch_bounds__(256) void k_attn_prep(const float *__restrict__ q, 
 
 __device__ __forceinline__ float wave_swap_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
 
-template <int HD>
+// Block-sparse mode (video sparse attention).  Slots are tile-ordered: tile i
+// owns slots 64 i .. 64 i + cnt[i] - 1 and gather[slot] names the token there
+// (-1 for the empty rest of the tile).  The workgroup of query block qb holds
+// query tiles 2 qb (wavefronts 0, 1) and 2 qb + 1 (wavefronts 2, 3); it walks
+// the union of their selected key tiles, lists[(h * nqb + qb) * T + e] =
+// key tile | (bit 14: tile 2 qb selects it) | (bit 15: tile 2 qb + 1 does),
+// e < list_len[h * nqb + qb], and each pair of wavefronts skips the tiles its
+// query tile did not select.  The output row of a slot goes to its token,
+// plus coarse[h][tile][d] * gate[token][h][d] when a gate is given.
+struct Sparse {
+    const uint16_t *lists;
+    const int *list_len;
+    const int *cnt;
+    const int *gather;
+    const float *coarse;
+    const float *gate;
+    int T;
+};
+
+template <int HD, bool SPARSE>
 __global__ __launch_bounds__(256, 2) void k_attn_fwd(const _Float16 *__restrict__ Qp,
                                                      const _Float16 *__restrict__ Kp,
                                                      const _Float16 *__restrict__ Vt, int n, int n_pad,
-                                                     int heads, float *__restrict__ O, int64_t o_ld) {
+                                                     int heads, float *__restrict__ O, int64_t o_ld, Sparse sp) {
     constexpr int KS = HD / 16;            // 16-wide steps of the S product
     constexpr int DB = HD / 32;            // 32-row blocks of O^T
     constexpr int KROW = HD + 8;           // LDS row of K (halfs), padded against bank conflicts
@@ -212,6 +244,15 @@ __global__ __launch_bounds__(256, 2) void k_attn_fwd(const _Float16 *__restrict_
         for (int kk = 0; kk < KS; kk++) qf[kk] = qp[2 * kk];
     }
 
+    // key tiles to visit: 0 .. nkt-1 (dense) or the block's list (sparse)
+    const uint16_t *lst = nullptr;
+    int nkt = (n + ATT_KT - 1) / ATT_KT;
+    if (SPARSE) {
+        lst = sp.lists + (size_t)L * sp.T;
+        nkt = sp.list_len[L];
+    }
+    auto tile_of = [&](int e) { return SPARSE ? (int)(lst[e] & 0x3FFF) : e; };
+
     half8 rk[KCH], rv[KCH];
     auto load_tile = [&](int j) {
 #pragma unroll
@@ -239,97 +280,323 @@ __global__ __launch_bounds__(256, 2) void k_attn_fwd(const _Float16 *__restrict_
     for (int i = 0; i < DB; i++) o[i] = f32x16{};
     float m = -INFINITY, lsum = 0.f;
 
-    const int nkt = (n + ATT_KT - 1) / ATT_KT;
-    load_tile(0);
-    store_tile(0);
+    if (nkt > 0) {
+        load_tile(tile_of(0));
+        store_tile(0);
+    }
     __syncthreads();
-    for (int j = 0; j < nkt; j++) {
-        const int b = j & 1;
-        if (j + 1 < nkt) load_tile(j + 1);
-
-        // S^T[key][query] for the 64 keys: two 32-key accumulators
-        f32x16 s[2] = {f32x16{}, f32x16{}};
+    for (int e = 0; e < nkt; e++) {
+        const int b = e & 1;
+        const int j = tile_of(e);
+        if (e + 1 < nkt) load_tile(tile_of(e + 1));
+        // valid keys in this tile (>= 1); in sparse mode, whether this pair of
+        // wavefronts' query tile selected it (wave-uniform)
+        const int kv = SPARSE ? sp.cnt[j] : n - j * ATT_KT;
+        const bool active = SPARSE ? ((lst[e] >> (14 + (wave >> 1))) & 1) != 0 : true;
+        if (active) {
+            // S^T[key][query] for the 64 keys: two 32-key accumulators
+            f32x16 s[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-        for (int kk = 0; kk < KS; kk++) {
+            for (int kk = 0; kk < KS; kk++) {
 #pragma unroll
-            for (int st = 0; st < 2; st++) {
-                const half8 a = *(const half8 *)&sk[b][32 * st + l32][16 * kk + 8 * hf];
-                s[st] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kk], s[st], 0, 0, 0);
+                for (int st = 0; st < 2; st++) {
+                    const half8 a = *(const half8 *)&sk[b][32 * st + l32][16 * kk + 8 * hf];
+                    s[st] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kk], s[st], 0, 0, 0);
+                }
             }
-        }
-        // lane holds keys 32 st + 8 (v/4) + 4 hf + v%4 of query q0 + l32
-        const int kv = n - j * ATT_KT;  // valid keys in this tile (>= 1)
-        if (kv < ATT_KT) {
+            // lane holds keys 32 st + 8 (v/4) + 4 hf + v%4 of query q0 + l32
+            if (kv < ATT_KT) {
+#pragma unroll
+                for (int st = 0; st < 2; st++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++)
+                        if (32 * st + 8 * (v >> 2) + 4 * hf + (v & 3) >= kv) s[st][v] = -INFINITY;
+            }
+            float mt = s[0][0];
+#pragma unroll
+            for (int v = 1; v < 16; v++) mt = fmaxf(mt, s[0][v]);
+#pragma unroll
+            for (int v = 0; v < 16; v++) mt = fmaxf(mt, s[1][v]);
+            mt = wave_swap_max(mt);
+            const bool grow = mt > m + ATT_TAU;
+            if (__ballot(grow)) {  // wave-uniform: some query's offset must rise
+                const float mn = grow ? mt : m;
+                const float alpha = __builtin_amdgcn_exp2f(m - mn);
+                m = mn;
+                lsum *= alpha;
+#pragma unroll
+                for (int i = 0; i < DB; i++) o[i] *= alpha;
+            }
 #pragma unroll
             for (int st = 0; st < 2; st++)
 #pragma unroll
-                for (int v = 0; v < 16; v++)
-                    if (32 * st + 8 * (v >> 2) + 4 * hf + (v & 3) >= kv) s[st][v] = -INFINITY;
-        }
-        float mt = s[0][0];
-#pragma unroll
-        for (int v = 1; v < 16; v++) mt = fmaxf(mt, s[0][v]);
-#pragma unroll
-        for (int v = 0; v < 16; v++) mt = fmaxf(mt, s[1][v]);
-        mt = wave_swap_max(mt);
-        const bool grow = mt > m + ATT_TAU;
-        if (__ballot(grow)) {  // wave-uniform: some query's offset must rise
-            const float mn = grow ? mt : m;
-            const float alpha = __builtin_amdgcn_exp2f(m - mn);
-            m = mn;
-            lsum *= alpha;
-#pragma unroll
-            for (int i = 0; i < DB; i++) o[i] *= alpha;
-        }
-#pragma unroll
-        for (int st = 0; st < 2; st++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) s[st][v] = __builtin_amdgcn_exp2f(s[st][v] - m);
+                for (int v = 0; v < 16; v++) s[st][v] = __builtin_amdgcn_exp2f(s[st][v] - m);
 
-        // P^T fragments: 16-key step t = values 4g..4g+7 of accumulator t/2,
-        // g = 2 (t % 2); they pair with V^T stored in the vt_key order.  The
-        // row sum is taken over the same fp16 values the product uses.
-        half8 pf[4];
-#pragma unroll
-        for (int tt = 0; tt < 4; tt++) {
-#pragma unroll
-            for (int e = 0; e < 8; e++) pf[tt][e] = (_Float16)s[tt >> 1][8 * (tt & 1) + e];
-        }
-        float ps[2] = {0.f, 0.f};
-#pragma unroll
-        for (int tt = 0; tt < 4; tt++)
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                ps[e & 1] = __builtin_amdgcn_fdot2(half2v{pf[tt][2 * e], pf[tt][2 * e + 1]}, half2v{1, 1},
-                                                   ps[e & 1], false);
-        lsum += ps[0] + ps[1];
-#pragma unroll
-        for (int db = 0; db < DB; db++) {
+            // P^T fragments: 16-key step t = values 4g..4g+7 of accumulator
+            // t/2, g = 2 (t % 2); they pair with V^T stored in the vt_key
+            // order.  The row sum is taken over the same fp16 values the
+            // product uses.
+            half8 pf[4];
 #pragma unroll
             for (int tt = 0; tt < 4; tt++) {
-                const half8 a = *(const half8 *)&sv[b][32 * db + l32][16 * tt + 8 * hf];
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[tt], o[db], 0, 0, 0);
+#pragma unroll
+                for (int q = 0; q < 8; q++) pf[tt][q] = (_Float16)s[tt >> 1][8 * (tt & 1) + q];
+            }
+            float ps[2] = {0.f, 0.f};
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    ps[q & 1] = __builtin_amdgcn_fdot2(half2v{pf[tt][2 * q], pf[tt][2 * q + 1]}, half2v{1, 1},
+                                                       ps[q & 1], false);
+            lsum += ps[0] + ps[1];
+#pragma unroll
+            for (int db = 0; db < DB; db++) {
+#pragma unroll
+                for (int tt = 0; tt < 4; tt++) {
+                    const half8 a = *(const half8 *)&sv[b][32 * db + l32][16 * tt + 8 * hf];
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[tt], o[db], 0, 0, 0);
+                }
             }
         }
-        if (j + 1 < nkt) store_tile(b ^ 1);
+        if (e + 1 < nkt) store_tile(b ^ 1);
         __syncthreads();
     }
 
     const float l = lsum + __shfl_xor(lsum, 32);
     const float inv = 1.0f / l;
-    const int qq = q0 + l32;
-    if (qq < n) {
-        float *orow = O + (size_t)qq * o_ld + (size_t)h * HD;
+    const int slot = q0 + l32;
+    int row = slot < n ? slot : -1;
+    int tile = 0;
+    if (SPARSE) {
+        tile = slot / ATT_KT;
+        row = (tile < sp.T && slot - tile * ATT_KT < sp.cnt[tile]) ? sp.gather[slot] : -1;
+    }
+    if (row >= 0) {
+        float *orow = O + (size_t)row * o_ld + (size_t)h * HD;
+        const float *crow = SPARSE && sp.coarse ? sp.coarse + ((size_t)h * sp.T + tile) * HD : nullptr;
+        const float *grow_ = crow ? sp.gate + (size_t)row * o_ld + (size_t)h * HD : nullptr;
 #pragma unroll
         for (int db = 0; db < DB; db++)
 #pragma unroll
             for (int g = 0; g < 4; g++) {
+                const int d = 32 * db + 8 * g + 4 * hf;
                 f32x4 w;
 #pragma unroll
-                for (int e = 0; e < 4; e++) w[e] = o[db][4 * g + e] * inv;
-                *(f32x4 *)(orow + 32 * db + 8 * g + 4 * hf) = w;
+                for (int q = 0; q < 4; q++) w[q] = o[db][4 * g + q] * inv;
+                if (crow) {
+                    const f32x4 cv = *(const f32x4 *)(crow + d), gv = *(const f32x4 *)(grow_ + d);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float t = cv[q] * gv[q];
+                        w[q] = w[q] + t;
+                    }
+                }
+                *(f32x4 *)(orow + d) = w;
             }
     }
+}
+
+// ---------------------------------------------------------------------------
+// Video sparse attention (src/core/fh3_vsa.c:186-507).  The tile statistics
+// are computed in the reference's exact order and roundings (one thread per
+// output, products and sums rounded separately), so the tile scores -- and
+// with them the top-k tile choice -- are bit-identical to the CPU's; the fine
+// attention then runs on k_attn_fwd over each query tile's selected tiles.
+// ---------------------------------------------------------------------------
+
+// pool[h][i][d] = sum over the tile's tokens in order of x[tok][h][d] * inv[i]
+template <int HD>
+__global__ __launch_bounds__(HD) void k_vsa_pool(const float *__restrict__ q, const float *__restrict__ k,
+                                                 const float *__restrict__ v, int64_t ld, int64_t ldv, int heads,
+                                                 const int *__restrict__ tok, const int *__restrict__ off,
+                                                 const float *__restrict__ inv, int T, float *__restrict__ qp,
+                                                 float *__restrict__ kp, float *__restrict__ vp) {
+    const int i = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+    const float w = inv[i];
+    float aq = 0.f, ak = 0.f, av = 0.f;
+    for (int r = off[i]; r < off[i + 1]; r++) {
+        const size_t t = (size_t)tok[r], at = t * ld + (size_t)h * HD + d;
+        aq = aq + q[at] * w;
+        ak = ak + k[at] * w;
+        if (vp) av = av + v[t * ldv + (size_t)h * HD + d] * w;
+    }
+    const size_t o = ((size_t)h * T + i) * HD + d;
+    qp[o] = aq;
+    kp[o] = ak;
+    if (vp) vp[o] = av;
+}
+
+// scores[h][i][j] = (sum_d qp[h][i][d] * kp[h][j][d], in order) * scale
+template <int HD>
+__global__ __launch_bounds__(256) void k_vsa_scores(const float *__restrict__ qp, const float *__restrict__ kp,
+                                                    int T, float scale, float *__restrict__ sc) {
+    __shared__ float qrow[HD];
+    const int i = blockIdx.x, h = blockIdx.y;
+    if (threadIdx.x < HD) qrow[threadIdx.x] = qp[((size_t)h * T + i) * HD + threadIdx.x];
+    __syncthreads();
+    for (int j = threadIdx.x; j < T; j += blockDim.x) {
+        const float *kr = kp + ((size_t)h * T + j) * HD;
+        float dot = 0.f;
+        for (int d = 0; d < HD; d++) dot = dot + qrow[d] * kr[d];
+        sc[((size_t)h * T + i) * T + j] = dot * scale;
+    }
+}
+
+// The selection of query tile i as flags sel[j] (LDS): every tile for prefix
+// query tiles or when all are kept; otherwise the prefix tiles and the kv
+// video tiles of largest score, ties to the lower tile index (the order of
+// the reference's qsort comparator, src/core/fh3_vsa.c:178-184).  The kv-th
+// largest score is found by a 4-pass radix select on order-preserving keys.
+__device__ void vsa_select_row(const float *__restrict__ srow, int T, int P, int kv, bool all, int i,
+                               uint32_t *keys, uint8_t *sel, int *hist, int *scal) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    if (i < P || all) {
+        for (int j = tid; j < T; j += nt) sel[j] = 1;
+        __syncthreads();
+        return;
+    }
+    const int NV = T - P;
+    for (int j = tid; j < T; j += nt) {
+        sel[j] = j < P;
+        if (j >= P) {
+            float f = srow[j];
+            f = f == 0.f ? 0.f : f;  // -0 ties with +0, as in the comparator
+            const uint32_t u = __float_as_uint(f);
+            keys[j - P] = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+        }
+    }
+    uint32_t prefix = 0, mask = 0;
+    int want = kv;
+    for (int pass = 0; pass < 4; pass++) {
+        const int shift = 24 - 8 * pass;
+        for (int b = tid; b < 256; b += nt) hist[b] = 0;
+        __syncthreads();
+        for (int j = tid; j < NV; j += nt)
+            if ((keys[j] & mask) == prefix) atomicAdd(&hist[(keys[j] >> shift) & 255], 1);
+        __syncthreads();
+        if (tid == 0) {
+            int above = 0, b = 255;
+            for (; b > 0; b--) {
+                if (above + hist[b] >= want) break;
+                above += hist[b];
+            }
+            scal[0] = b;
+            scal[1] = want - above;
+        }
+        __syncthreads();
+        prefix |= (uint32_t)scal[0] << shift;
+        mask |= 0xFFu << shift;
+        want = scal[1];
+        __syncthreads();
+    }
+    // keys above the threshold are in; of those equal to it, the first `want`
+    // by tile index (a block-wide running count over j in order)
+    if (tid == 0) scal[2] = 0;
+    __syncthreads();
+    for (int j0 = 0; j0 < NV; j0 += nt) {
+        const int j = j0 + tid;
+        const bool eq = j < NV && keys[j] == prefix;
+        const uint64_t bal = __ballot(eq);
+        const int wave = tid >> 6, lane = tid & 63;
+        if (lane == 0) hist[wave] = __popcll(bal);
+        __syncthreads();
+        int before = scal[2];
+        for (int w = 0; w < wave; w++) before += hist[w];
+        before += __popcll(bal & ((lane ? (~0ull >> (64 - lane)) : 0ull)));
+        if (j < NV) sel[P + j] = keys[j] > prefix || (eq && before < want);
+        __syncthreads();
+        if (tid == 0) {
+            int tot = 0;
+            for (int w = 0; w < (nt >> 6); w++) tot += hist[w];
+            scal[2] += tot;
+        }
+        __syncthreads();
+    }
+}
+
+// Union tile lists of query-tile pairs (2 qb, 2 qb + 1) for k_attn_fwd.
+__global__ __launch_bounds__(256) void k_vsa_lists(const float *__restrict__ sc, int T, int P, int kv, int all,
+                                                   int nqb, uint16_t *__restrict__ lists,
+                                                   int *__restrict__ list_len) {
+    extern __shared__ uint8_t smem[];
+    uint32_t *keys = (uint32_t *)smem;                    // [T]
+    uint8_t *sel0 = smem + (size_t)4 * T, *sel1 = sel0 + T;
+    __shared__ int hist[256];
+    __shared__ int scal[4];
+    const int qb = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
+    const int i0 = 2 * qb, i1 = 2 * qb + 1;
+    vsa_select_row(sc + ((size_t)h * T + i0) * T, T, P, kv, all != 0, i0, keys, sel0, hist, scal);
+    if (i1 < T) {
+        vsa_select_row(sc + ((size_t)h * T + i1) * T, T, P, kv, all != 0, i1, keys, sel1, hist, scal);
+    } else {
+        for (int j = tid; j < T; j += nt) sel1[j] = 0;
+        __syncthreads();
+    }
+    // stream compaction in tile order
+    uint16_t *out = lists + ((size_t)h * nqb + qb) * T;
+    if (tid == 0) scal[3] = 0;
+    __syncthreads();
+    for (int j0 = 0; j0 < T; j0 += nt) {
+        const int j = j0 + tid;
+        const int bits = j < T ? (sel0[j] ? 1 : 0) | (sel1[j] ? 2 : 0) : 0;
+        const uint64_t bal = __ballot(bits != 0);
+        const int wave = tid >> 6, lane = tid & 63;
+        if (lane == 0) hist[wave] = __popcll(bal);
+        __syncthreads();
+        int at = scal[3];
+        for (int w = 0; w < wave; w++) at += hist[w];
+        at += __popcll(bal & ((lane ? (~0ull >> (64 - lane)) : 0ull)));
+        if (bits) out[at] = (uint16_t)(j | (bits << 14));
+        __syncthreads();
+        if (tid == 0) {
+            int tot = 0;
+            for (int w = 0; w < (nt >> 6); w++) tot += hist[w];
+            scal[3] += tot;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) list_len[h * nqb + qb] = scal[3];
+}
+
+// Gated coarse branch: per (query tile i, head h) a softmax over all tile
+// scores mixes the pooled v: coarse[h][i][d] = sum_j expf(s_j - max) / sum * vp[h][j][d].
+template <int HD>
+__global__ __launch_bounds__(HD) void k_vsa_coarse(const float *__restrict__ sc, const float *__restrict__ vp,
+                                                   int T, float *__restrict__ coarse) {
+    __shared__ float red[HD / 64];
+    __shared__ float bc[2];
+    const int i = blockIdx.x, h = blockIdx.y, d = threadIdx.x, lane = d & 63, wave = d >> 6;
+    const float *srow = sc + ((size_t)h * T + i) * T;
+    float mx = -1e30f;
+    for (int j = d; j < T; j += HD) mx = fmaxf(mx, srow[j]);
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    if (d == 0) {
+        float m = red[0];
+        for (int w = 1; w < HD / 64; w++) m = fmaxf(m, red[w]);
+        bc[0] = m;
+    }
+    __syncthreads();
+    mx = bc[0];
+    float sum = 0.f;
+    for (int j = d; j < T; j += HD) sum += expf(srow[j] - mx);
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    __syncthreads();
+    if (lane == 0) red[wave] = sum;
+    __syncthreads();
+    if (d == 0) {
+        float t = 0.f;
+        for (int w = 0; w < HD / 64; w++) t += red[w];
+        bc[1] = 1.0f / t;
+    }
+    __syncthreads();
+    const float inv = bc[1];
+    float acc = 0.f;
+    const float *vcol = vp + (size_t)h * T * HD + d;
+    for (int j = 0; j < T; j++) acc += expf(srow[j] - mx) * inv * vcol[(size_t)j * HD];
+    coarse[((size_t)h * T + i) * HD + d] = acc;
 }
 
 template <int HD>
@@ -341,13 +608,14 @@ hipError_t attn_launch(const float *q, const float *k, const float *v, int64_t l
     _Float16 *Kp = Qp + (size_t)heads * n_pad * HD;
     _Float16 *Vt = Kp + (size_t)heads * n_pad * HD;
     const float qscale = 1.4426950408889634f / sqrtf((float)HD);
-    hipLaunchKernelGGL(k_attn_prep<HD>, dim3(n_pad / ATT_PREP_T, heads), dim3(256), 0, st, q, k, v, ld, n,
-                       (const int *)nullptr, qn_w, kn_w, eps, cosb, sinb, rot, qscale, n_pad, Qp, Kp, Vt);
+    hipLaunchKernelGGL((k_attn_prep<HD, false>), dim3(n_pad / ATT_PREP_T, heads), dim3(256), 0, st, q, k, v, ld, ld,
+                       n, (const int *)nullptr, qn_w, kn_w, eps, cosb, sinb, rot, qscale, n_pad, Qp, Kp, Vt,
+                       (float *)nullptr, (float *)nullptr, heads);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int blocks = heads * (n_pad / ATT_QB);
-    hipLaunchKernelGGL(k_attn_fwd<HD>, dim3(blocks), dim3(64 * ATT_NW), 0, st, Qp, Kp, Vt, n, n_pad, heads, o,
-                       o_ld);
+    hipLaunchKernelGGL((k_attn_fwd<HD, false>), dim3(blocks), dim3(64 * ATT_NW), 0, st, Qp, Kp, Vt, n, n_pad, heads,
+                       o, o_ld, Sparse{});
     return hipGetLastError();
 }
 
@@ -367,4 +635,109 @@ extern "C" hipError_t fh3k_attention(const float *q, const float *k, const float
     if (hd == 128) return attn_launch<128>(q, k, v, ld, n, heads, qn_w, kn_w, eps, cosb, sinb, rot, ws, o, o_ld, st);
     if (hd == 64) return attn_launch<64>(q, k, v, ld, n, heads, qn_w, kn_w, eps, cosb, sinb, rot, ws, o, o_ld, st);
     return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// Video sparse attention launchers
+// ---------------------------------------------------------------------------
+namespace {
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+struct VsaWs {
+    _Float16 *Qp, *Kp, *Vt;
+    float *qp, *kp, *vp, *sc, *coarse;
+    uint16_t *lists;
+    int *list_len;
+    size_t bytes;
+};
+
+VsaWs vsa_ws(void *base, int T, int heads, int hd) {
+    const int64_t n_pad = fh3k_attn_pad(ATT_KT * T);
+    const int64_t nqb = n_pad / ATT_QB;
+    char *p = (char *)base;
+    VsaWs w;
+    size_t at = 0;
+    auto take = [&](size_t b) {
+        char *r = p ? p + at : nullptr;
+        at += align256(b);
+        return r;
+    };
+    const size_t op = (size_t)heads * n_pad * hd * sizeof(_Float16);
+    w.Qp = (_Float16 *)take(op);
+    w.Kp = (_Float16 *)take(op);
+    w.Vt = (_Float16 *)take(op);
+    const size_t pool = (size_t)heads * T * hd * sizeof(float);
+    w.qp = (float *)take(pool);
+    w.kp = (float *)take(pool);
+    w.vp = (float *)take(pool);
+    w.coarse = (float *)take(pool);
+    w.sc = (float *)take((size_t)heads * T * T * sizeof(float));
+    w.lists = (uint16_t *)take((size_t)heads * nqb * T * sizeof(uint16_t));
+    w.list_len = (int *)take((size_t)heads * nqb * sizeof(int));
+    w.bytes = at;
+    return w;
+}
+
+template <int HD>
+hipError_t vsa_launch(const float *q, const float *k, const float *v, int64_t ld, int64_t ldv, const float *gate,
+                      float *o, int64_t o_ld, int heads, const int *tok, const int *off, const float *inv,
+                      const int *gather, const int *cnt, int T, int P, int kv, int all, float scale, void *ws,
+                      hipStream_t st) {
+    const int n_pad = (int)fh3k_attn_pad(ATT_KT * T);
+    const int nqb = n_pad / ATT_QB;
+    VsaWs w = vsa_ws(ws, T, heads, HD);
+    const float qscale = 1.4426950408889634f / sqrtf((float)HD);
+    hipLaunchKernelGGL((k_attn_prep<HD, false>), dim3(n_pad / ATT_PREP_T, heads), dim3(256), 0, st, q, k, v, ld, ldv,
+                       ATT_KT * T, gather, (const float *)nullptr, (const float *)nullptr, 0.f,
+                       (const float *)nullptr, (const float *)nullptr, 0, qscale, n_pad, w.Qp, w.Kp, w.Vt,
+                       (float *)nullptr, (float *)nullptr, heads);
+    hipLaunchKernelGGL((k_vsa_pool<HD>), dim3(T, heads), dim3(HD), 0, st, q, k, v, ld, ldv, heads, tok, off, inv, T, w.qp,
+                       w.kp, gate ? w.vp : (float *)nullptr);
+    hipLaunchKernelGGL((k_vsa_scores<HD>), dim3(T, heads), dim3(256), 0, st, w.qp, w.kp, T, scale, w.sc);
+    hipLaunchKernelGGL(k_vsa_lists, dim3(nqb, heads), dim3(256), (size_t)align256(6 * (size_t)T), st, w.sc, T, P, kv,
+                       all, nqb, w.lists, w.list_len);
+    if (gate) hipLaunchKernelGGL((k_vsa_coarse<HD>), dim3(T, heads), dim3(HD), 0, st, w.sc, w.vp, T, w.coarse);
+    Sparse sp{w.lists, w.list_len, cnt, gather, gate ? w.coarse : nullptr, gate, T};
+    hipLaunchKernelGGL((k_attn_fwd<HD, true>), dim3(heads * nqb), dim3(64 * ATT_NW), 0, st, w.Qp, w.Kp, w.Vt,
+                       ATT_KT * T, n_pad, heads, o, o_ld, sp);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" int fh3k_vsa_max_tiles(void) { return 4096; }
+
+extern "C" size_t fh3k_vsa_ws_bytes(int T, int heads, int hd) { return vsa_ws(nullptr, T, heads, hd).bytes; }
+
+extern "C" hipError_t fh3k_vsa_attention(const float *q, const float *k, const float *v, int64_t ld, int64_t ldv,
+                                         const float *gate, float *o, int64_t o_ld, int heads, int hd,
+                                         const int *tok, const int *off, const float *inv, const int *gather,
+                                         const int *cnt, int T, int P, int kv, int all, float scale, void *ws,
+                                         hipStream_t st) {
+    if (T <= 0 || T > fh3k_vsa_max_tiles()) return hipErrorInvalidValue;
+    if (hd == 128)
+        return vsa_launch<128>(q, k, v, ld, ldv, gate, o, o_ld, heads, tok, off, inv, gather, cnt, T, P, kv, all,
+                               scale, ws, st);
+    if (hd == 64)
+        return vsa_launch<64>(q, k, v, ld, ldv, gate, o, o_ld, heads, tok, off, inv, gather, cnt, T, P, kv, all,
+                              scale, ws, st);
+    return hipErrorInvalidValue;
+}
+
+extern "C" hipError_t fh3k_qk_normrope_f32(const float *q, const float *k, int64_t ld, int n, int heads, int hd,
+                                           const float *qn_w, const float *kn_w, float eps, const float *cosb,
+                                           const float *sinb, int rot, float *qo, float *ko, hipStream_t st) {
+    const int n64 = (n + ATT_PREP_T - 1) / ATT_PREP_T * ATT_PREP_T;
+    if (hd == 128)
+        hipLaunchKernelGGL((k_attn_prep<128, true>), dim3(n64 / ATT_PREP_T, heads), dim3(256), 0, st, q, k,
+                           (const float *)nullptr, ld, ld, n, (const int *)nullptr, qn_w, kn_w, eps, cosb, sinb, rot,
+                           1.f, n64, (_Float16 *)nullptr, (_Float16 *)nullptr, (_Float16 *)nullptr, qo, ko, heads);
+    else if (hd == 64)
+        hipLaunchKernelGGL((k_attn_prep<64, true>), dim3(n64 / ATT_PREP_T, heads), dim3(256), 0, st, q, k,
+                           (const float *)nullptr, ld, ld, n, (const int *)nullptr, qn_w, kn_w, eps, cosb, sinb, rot,
+                           1.f, n64, (_Float16 *)nullptr, (_Float16 *)nullptr, (_Float16 *)nullptr, qo, ko, heads);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
 }

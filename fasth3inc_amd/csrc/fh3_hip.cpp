@@ -12,6 +12,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <vector>
 
 #include "fh3/fh3.h"
 #include "fh3/fh3_hip.h"
@@ -33,6 +34,11 @@ struct State {
     DevBuf ws2;                     // x16 made from a prepared fp32 copy (other weight types)
     DevBuf w16;                     // fp16 rows of a weight of another type
     DevBuf attn;                    // fp16 attention operands (Qp, Kp, Vt)
+    DevBuf vsa_ws;                  // VSA operands, tile statistics, scores and tile lists
+    DevBuf vsa_qk;                  // fp32 normalised/rotated q, k of the qkv VSA entry
+    DevBuf vsa_geo;                 // VSA tile geometry of the last sequence shape
+    int vsa_key[8] = {-1, -1, -1, -1, -1, -1, -1, -1};
+    int vsa_T = 0, vsa_P = 0;
     DevBuf st_w, st_x, st_y, st_b;  // staging for the host-pointer wrappers
     int path = FH3_HIP_PATH_AUTO;
     std::recursive_mutex mu;
@@ -196,7 +202,8 @@ extern "C" void fh3_hip_shutdown(void) {
     std::lock_guard<std::recursive_mutex> lk(g.mu);
     if (!g.init) return;
     (void)hipDeviceSynchronize();
-    DevBuf *bufs[] = {&g.ws, &g.ws2, &g.w16, &g.attn, &g.st_w, &g.st_x, &g.st_y, &g.st_b};
+    DevBuf *bufs[] = {&g.ws, &g.ws2, &g.w16, &g.attn, &g.vsa_ws, &g.vsa_qk, &g.vsa_geo,
+                      &g.st_w, &g.st_x, &g.st_y, &g.st_b};
     for (DevBuf *b : bufs) {
         if (b->p) (void)hipFree(b->p);
         b->p = nullptr;
@@ -591,6 +598,145 @@ extern "C" int fh3_hip_attention_qkv_dev(const float *d_qkv, int n, int heads, i
 }
 
 // ---------------------------------------------------------------------------
+// Video sparse attention
+// ---------------------------------------------------------------------------
+// Tile geometry of src/core/fh3_vsa.c:31-163: text tokens, then audio tokens,
+// in runs of `tile`; then the video grid in 4x4x4 cubes (t-major, tokens of a
+// cube in (t, h, w) order).  Counts that do not sum to n make every token
+// video; a grid that does not match the video count becomes 1 x 1 x V.
+static int vsa_geometry(const Fh3Seq *sq, int tile, std::vector<int> &tok, std::vector<int> &off, int *n_prefix) {
+    const int n = sq->seq_len;
+    int T = sq->num_text > 0 ? sq->num_text : 0, A = sq->num_audio > 0 ? sq->num_audio : 0;
+    int V = sq->num_video > 0 ? sq->num_video : 0;
+    if (T + A + V != n) T = 0, A = 0, V = n;
+    int gt = sq->grid_t, gh = sq->grid_h, gw = sq->grid_w;
+    if (gt <= 0 || gh <= 0 || gw <= 0 || (int64_t)gt * gh * gw != V) gt = 1, gh = 1, gw = V;
+    tok.clear();
+    off.assign(1, 0);
+    const int runs[2][2] = {{0, T}, {T, A}};
+    for (const auto &rn : runs)
+        for (int s0 = 0; s0 < rn[1]; s0 += tile) {
+            for (int e = s0; e < rn[1] && e < s0 + tile; e++) tok.push_back(rn[0] + e);
+            off.push_back((int)tok.size());
+        }
+    *n_prefix = (int)off.size() - 1;
+    if (V > 0)
+        for (int t0 = 0; t0 < gt; t0 += 4)
+            for (int h0 = 0; h0 < gh; h0 += 4)
+                for (int w0 = 0; w0 < gw; w0 += 4) {
+                    for (int t = t0; t < gt && t < t0 + 4; t++)
+                        for (int h = h0; h < gh && h < h0 + 4; h++)
+                            for (int w = w0; w < gw && w < w0 + 4; w++) tok.push_back(T + A + (t * gh + h) * gw + w);
+                    off.push_back((int)tok.size());
+                }
+    return (int)off.size() - 1;
+}
+
+// Device copy of the geometry: tok[n], off[T+1], inv[T], cnt[T], gather[slots]
+// (kept while the sequence shape does not change).
+static int vsa_plan(const Fh3Seq *sq, int tile, const char *fn) {
+    const int key[8] = {sq->seq_len, sq->num_text, sq->num_audio, sq->num_video, sq->grid_t, sq->grid_h, sq->grid_w,
+                        tile};
+    if (memcmp(key, g.vsa_key, sizeof key) == 0) return FH3_OK;
+    std::vector<int> tok, off;
+    int P = 0;
+    const int T = vsa_geometry(sq, tile, tok, off, &P);
+    if (T <= 0 || T > fh3k_vsa_max_tiles())
+        return set_err(FH3_E_INVALID, "%s: %d tiles (at most %d on the device)", fn, T, fh3k_vsa_max_tiles());
+    const int64_t slots = fh3k_attn_pad(64 * T);
+    const size_t n = (size_t)sq->seq_len;
+    std::vector<int> host(n + (T + 1) + 2 * (size_t)T + (size_t)slots);
+    int *h_tok = host.data(), *h_off = h_tok + n, *h_inv = h_off + T + 1, *h_cnt = h_inv + T, *h_gat = h_cnt + T;
+    memcpy(h_tok, tok.data(), n * sizeof(int));
+    memcpy(h_off, off.data(), (T + 1) * sizeof(int));
+    for (int i = 0; i < T; i++) {
+        const int c = off[i + 1] - off[i];
+        const float inv = 1.0f / (float)c;
+        memcpy(&h_inv[i], &inv, sizeof inv);
+        h_cnt[i] = c;
+    }
+    for (int64_t sl = 0; sl < slots; sl++) {
+        const int i = (int)(sl / 64), r = (int)(sl % 64);
+        h_gat[sl] = (i < T && r < h_cnt[i]) ? tok[off[i] + r] : -1;
+    }
+    int rc = grow(g.vsa_geo, host.size() * sizeof(int));
+    if (rc != FH3_OK) return rc;
+    FH3_HIPCALL(hipDeviceSynchronize());  // earlier calls may still read the old geometry
+    FH3_HIPCALL(hipMemcpy(g.vsa_geo.p, host.data(), host.size() * sizeof(int), hipMemcpyHostToDevice));
+    memcpy(g.vsa_key, key, sizeof key);
+    g.vsa_T = T;
+    g.vsa_P = P;
+    return FH3_OK;
+}
+
+static int vsa_dev(const Fh3VsaCfg *c, const float *q, const float *k, const float *v, int64_t ld, int64_t ldv,
+                   const float *gate, float *o, const Fh3Seq *sq, int heads, int hd, void *stream, const char *fn) {
+    if (!q || !k || !v || !o || !sq || sq->seq_len <= 0 || heads <= 0 || hd <= 0)
+        return set_err(FH3_E_INVALID, "%s: NULL pointer or non-positive size", fn);
+    if (!fh3k_attn_head_dim_ok(hd)) return set_err(FH3_E_INVALID, "%s: head_dim %d is not supported (64 or 128)", fn, hd);
+    const int tile = c && c->tile > 0 ? c->tile : 64;
+    const float sparsity = c ? c->sparsity : 0.8f;
+    if (tile > 64) return set_err(FH3_E_INVALID, "%s: tile %d above 64 is not supported on the device", fn, tile);
+    if ((uintptr_t)q & 15u || (uintptr_t)k & 15u || (uintptr_t)v & 15u || (uintptr_t)o & 15u || (uintptr_t)gate & 15u)
+        return set_err(FH3_E_INVALID, "%s: q, k, v, gate and o must be 16-byte aligned", fn);
+    if ((int64_t)sq->seq_len * heads * hd > ((int64_t)1 << 31))
+        return set_err(FH3_E_INVALID, "%s: n * heads * head_dim too large", fn);
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    std::lock_guard<std::recursive_mutex> lk(g.mu);
+    if ((rc = vsa_plan(sq, tile, fn)) != FH3_OK) return rc;
+    const int T = g.vsa_T, P = g.vsa_P, NV = T - P;
+    int kv = 0;
+    if (NV > 0) {  // src/core/fh3_vsa.c:165-172
+        kv = (int)ceilf((1.0f - sparsity) * (float)NV);
+        kv = kv < 1 ? 1 : (kv > NV ? NV : kv);
+    }
+    const int all = sparsity <= 0.0f || kv == NV;
+    if ((rc = grow(g.vsa_ws, fh3k_vsa_ws_bytes(T, heads, hd))) != FH3_OK) return rc;
+    const size_t n = (size_t)sq->seq_len;
+    const int *d_tok = (const int *)g.vsa_geo.p, *d_off = d_tok + n;
+    const float *d_inv = (const float *)(d_off + T + 1);
+    const int *d_cnt = (const int *)(d_inv + T), *d_gat = d_cnt + T;
+    const float scale = 1.0f / sqrtf((float)hd);
+    FH3_HIPCALL(fh3k_vsa_attention(q, k, v, ld, ldv, gate, o, (int64_t)heads * hd, heads, hd, d_tok, d_off, d_inv,
+                                   d_gat, d_cnt, T, P, kv, all, scale, g.vsa_ws.p,
+                                   stream ? (hipStream_t)stream : g.stream));
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_vsa_attention_dev(const Fh3VsaCfg *c, const float *d_q, const float *d_k, const float *d_v,
+                                         const float *d_gate, float *d_o, const Fh3Seq *seq, int heads, int head_dim,
+                                         void *stream) {
+    const int64_t ld = (int64_t)heads * head_dim;
+    return vsa_dev(c, d_q, d_k, d_v, ld, ld, d_gate, d_o, seq, heads, head_dim, stream, "fh3_hip_vsa_attention_dev");
+}
+
+extern "C" int fh3_hip_vsa_attention_qkv_dev(const Fh3VsaCfg *c, const float *d_qkv, const float *d_qnorm_w,
+                                             const float *d_knorm_w, float eps, const float *d_cos,
+                                             const float *d_sin, int rot_dim, const float *d_gate, float *d_o,
+                                             const Fh3Seq *seq, int heads, int head_dim, void *stream) {
+    const char *fn = "fh3_hip_vsa_attention_qkv_dev";
+    if (!d_qkv || !seq || seq->seq_len <= 0 || heads <= 0 || !fh3k_attn_head_dim_ok(head_dim))
+        return set_err(FH3_E_INVALID, "%s: bad arguments", fn);
+    if ((d_qnorm_w == nullptr) != (d_knorm_w == nullptr))
+        return set_err(FH3_E_INVALID, "%s: give both q and k norm weights or neither", fn);
+    if ((d_cos == nullptr) != (d_sin == nullptr) || (d_cos && (rot_dim <= 0 || rot_dim > head_dim || rot_dim % 2)))
+        return set_err(FH3_E_INVALID, "%s: rope needs cos and sin with an even rot_dim <= head_dim", fn);
+    if ((uintptr_t)d_qkv & 15u || (uintptr_t)d_cos & 15u || (uintptr_t)d_sin & 15u)
+        return set_err(FH3_E_INVALID, "%s: qkv, cos and sin must be 16-byte aligned", fn);
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    std::lock_guard<std::recursive_mutex> lk(g.mu);
+    const int64_t inner = (int64_t)heads * head_dim, n = seq->seq_len;
+    if ((rc = grow(g.vsa_qk, (size_t)(2 * n * inner) * sizeof(float))) != FH3_OK) return rc;
+    float *qf = (float *)g.vsa_qk.p, *kf = qf + n * inner;
+    hipStream_t st = stream ? (hipStream_t)stream : g.stream;
+    FH3_HIPCALL(fh3k_qk_normrope_f32(d_qkv, d_qkv + inner, 3 * inner, (int)n, heads, head_dim, d_qnorm_w, d_knorm_w,
+                                     eps, d_cos, d_sin, d_cos ? rot_dim : 0, qf, kf, st));
+    return vsa_dev(c, qf, kf, d_qkv + 2 * inner, inner, 3 * inner, d_gate, d_o, seq, heads, head_dim, stream, fn);
+}
+
+// ---------------------------------------------------------------------------
 // fh3.h host-pointer wrappers
 // ---------------------------------------------------------------------------
 extern "C" size_t fh3_row_bytes(int type, int64_t n) {
@@ -696,6 +842,27 @@ extern "C" void fh3_attention(const float *q, const float *k, const float *v, fl
     e = hipStreamSynchronize(g.stream);
     if (e == hipSuccess) e = hipMemcpy(o, g.st_y.p, b, hipMemcpyDeviceToHost);
     if (e != hipSuccess) report("fh3_attention", hip_fail(e, "fh3_attention download"));
+}
+
+extern "C" void fh3_vsa_attention(const Fh3VsaCfg *c, const float *q, const float *k, const float *v,
+                                  const float *gate, float *o, const Fh3Seq *seq, int heads, int head_dim) {
+    if (!q || !k || !v || !o || !seq || seq->seq_len <= 0 || heads <= 0 || head_dim <= 0) return;
+    int rc = ensure_init();
+    if (rc != FH3_OK) { report("fh3_vsa_attention", rc); return; }
+    std::lock_guard<std::recursive_mutex> lk(g.mu);
+    const size_t b = (size_t)seq->seq_len * (size_t)heads * (size_t)head_dim * sizeof(float);
+    if ((rc = grow(g.st_w, (gate ? 4 : 3) * b)) || (rc = grow(g.st_y, b))) { report("fh3_vsa_attention", rc); return; }
+    float *dq = (float *)g.st_w.p, *dk = dq + b / 4, *dv = dk + b / 4, *dg = gate ? dv + b / 4 : nullptr;
+    hipError_t e = hipMemcpy(dq, q, b, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dk, k, b, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dv, v, b, hipMemcpyHostToDevice);
+    if (e == hipSuccess && gate) e = hipMemcpy(dg, gate, b, hipMemcpyHostToDevice);
+    if (e != hipSuccess) { report("fh3_vsa_attention", hip_fail(e, "fh3_vsa_attention upload")); return; }
+    rc = fh3_hip_vsa_attention_dev(c, dq, dk, dv, dg, (float *)g.st_y.p, seq, heads, head_dim, nullptr);
+    if (rc != FH3_OK) { report("fh3_vsa_attention", rc); return; }
+    e = hipStreamSynchronize(g.stream);
+    if (e == hipSuccess) e = hipMemcpy(o, g.st_y.p, b, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) report("fh3_vsa_attention", hip_fail(e, "fh3_vsa_attention download"));
 }
 
 extern "C" void fh3_matmul_scalar(const Fh3W *w, const float *x, float *y, int n_tok, const float *bias_or_null) {

@@ -57,6 +57,17 @@ FH3_PACK_ALIGNMENT = 4096
 FH3_PACK_MAX_TENSORS_PER_LAYER = 16
 
 
+class Fh3VsaCfg(ctypes.Structure):       # include/fh3/fh3.h
+    _fields_ = [("tile", ctypes.c_int), ("sparsity", ctypes.c_float)]
+
+
+class Fh3Seq(ctypes.Structure):          # include/fh3/fh3.h (the reference's layout)
+    _fields_ = [("seq_len", ctypes.c_int), ("num_text", ctypes.c_int), ("num_audio", ctypes.c_int),
+                ("num_video", ctypes.c_int), ("grid_t", ctypes.c_int), ("grid_h", ctypes.c_int),
+                ("grid_w", ctypes.c_int), ("tags", ctypes.c_void_p), ("pair_index", ctypes.c_void_p),
+                ("pos", ctypes.c_void_p), ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p)]
+
+
 class Fh3LayerView(ctypes.Structure):
     _fields_ = [(n, Fh3W) for n in LAYER_TENSORS]
 
@@ -128,6 +139,8 @@ SIGNATURES = {
     "fh3_matmul_avx2": (None, [ctypes.POINTER(Fh3W), _c_void_p, _c_void_p, _c_int, _c_void_p]),
     "fh3_rng_normal": (None, [_c_u64, _c_u64, _c_void_p, _c_size]),
     "fh3_attention": (None, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int]),
+    "fh3_vsa_attention": (None, [ctypes.POINTER(Fh3VsaCfg), _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                 ctypes.POINTER(Fh3Seq), _c_int, _c_int]),
     # fh3_hip.h
     "fh3_hip_init": (_c_int, [_c_int]),
     "fh3_hip_shutdown": (None, []),
@@ -158,6 +171,11 @@ SIGNATURES = {
                                        _c_void_p]),
     "fh3_hip_attention_qkv_dev": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_void_p, ctypes.c_float,
                                            _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p]),
+    "fh3_hip_vsa_attention_dev": (_c_int, [ctypes.POINTER(Fh3VsaCfg), _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                           _c_void_p, ctypes.POINTER(Fh3Seq), _c_int, _c_int, _c_void_p]),
+    "fh3_hip_vsa_attention_qkv_dev": (_c_int, [ctypes.POINTER(Fh3VsaCfg), _c_void_p, _c_void_p, _c_void_p,
+                                               ctypes.c_float, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p,
+                                               ctypes.POINTER(Fh3Seq), _c_int, _c_int, _c_void_p]),
     "fh3_hip_graph_begin": (_c_int, [_c_void_p]),
     "fh3_hip_graph_end": (_c_int, [_c_void_p, ctypes.POINTER(_c_void_p)]),
     "fh3_hip_graph_launch": (_c_int, [_c_void_p, _c_void_p]),
@@ -406,6 +424,41 @@ def attention_host(q, k, v):
     o = np.full_like(q, np.nan)
     n, heads, hd = q.shape
     lib().fh3_attention(_p(q), _p(k), _p(v), _p(o), n, heads, hd)
+    return o
+
+
+def seq_of(n, num_text=0, num_audio=0, num_video=None, grid=(0, 0, 0)):
+    """An Fh3Seq with the fields the attention calls read."""
+    return Fh3Seq(n, num_text, num_audio, n - num_text - num_audio if num_video is None else num_video, *grid,
+                  None, None, None, None, None)
+
+
+def vsa_attention_dev(d_q, d_k, d_v, d_gate, d_o, seq, heads, hd, sparsity=0.8, tile=64, stream_ptr=None):
+    """fh3_hip_vsa_attention_dev over [n][heads][hd] device rows; seq an Fh3Seq."""
+    cfg = Fh3VsaCfg(tile, sparsity)
+    _check(lib().fh3_hip_vsa_attention_dev(ctypes.byref(cfg), _ptr_of(d_q), _ptr_of(d_k), _ptr_of(d_v),
+                                           _ptr_of(d_gate), _ptr_of(d_o), ctypes.byref(seq), heads, hd, stream_ptr),
+           "fh3_hip_vsa_attention_dev")
+
+
+def vsa_attention_qkv_dev(d_qkv, d_gate, d_o, seq, heads, hd, sparsity=0.8, tile=64, d_qnorm_w=None,
+                          d_knorm_w=None, eps=1e-5, d_cos=None, d_sin=None, rot_dim=0, stream_ptr=None):
+    cfg = Fh3VsaCfg(tile, sparsity)
+    _check(lib().fh3_hip_vsa_attention_qkv_dev(ctypes.byref(cfg), _ptr_of(d_qkv), _ptr_of(d_qnorm_w),
+                                               _ptr_of(d_knorm_w), eps, _ptr_of(d_cos), _ptr_of(d_sin), rot_dim,
+                                               _ptr_of(d_gate), _ptr_of(d_o), ctypes.byref(seq), heads, hd,
+                                               stream_ptr), "fh3_hip_vsa_attention_qkv_dev")
+
+
+def vsa_attention_host(q, k, v, gate, seq, sparsity=0.8, tile=64):
+    """fh3_vsa_attention on host arrays (staged through the GPU)."""
+    q, k, v = (np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v))
+    g = None if gate is None else np.ascontiguousarray(gate, dtype=np.float32)
+    o = np.full_like(q, np.nan)
+    n, heads, hd = q.shape
+    cfg = Fh3VsaCfg(tile, sparsity)
+    lib().fh3_vsa_attention(ctypes.byref(cfg), _p(q), _p(k), _p(v), None if g is None else _p(g), _p(o),
+                            ctypes.byref(seq), heads, hd)
     return o
 
 

@@ -49,6 +49,31 @@ typedef struct Fh3W {
     const uint8_t *data;
 } Fh3W;
 
+/* Video sparse attention settings (reference include/fh3/fh3.h:41-44):
+ * tile <= 0 means 64; sparsity is the share of video key tiles dropped. */
+typedef struct Fh3VsaCfg {
+    int tile;
+    float sparsity;
+} Fh3VsaCfg;
+
+/* The reference's sequence descriptor (src/model/fh3_seq.h:32-45; opaque in
+ * its fh3.h).  Laid out identically so a caller's Fh3Seq passes unchanged;
+ * the attention calls read only the counts and the video grid. */
+typedef struct Fh3Seq {
+    int seq_len;     /* N = num_text + num_audio + num_video */
+    int num_text;
+    int num_audio;
+    int num_video;
+    int grid_t;      /* video grid (t, h, w) in tokens */
+    int grid_h;
+    int grid_w;
+    int *tags;
+    int *pair_index;
+    double *pos;
+    float *cos;      /* [N][96] rope tables */
+    float *sin;
+} Fh3Seq;
+
 /* Per-layer tensor views into a packed trunk layer
  * (reference include/fh3/fh3.h:90-100; run order src/io/fh3_pack.h:26-37). */
 typedef struct Fh3LayerView {
@@ -111,6 +136,21 @@ void fh3_matmul_avx2(const Fh3W *w, const float *x, float *y, int n_tok, const f
  * CPU result.  Replaces src/core/fh3_ops.c:589-695 (declared at
  * include/fh3/fh3.h:117 there). */
 void fh3_attention(const float *q, const float *k, const float *v, float *o, int n, int heads, int hd);
+
+/* Video sparse attention on host buffers q, k, v, gate (may be NULL), o
+ * [n][heads][head_dim], computed on the GPU (copied in and out on every call):
+ * per 64-token tile (text and audio runs, then 4x4x4 video cubes) mean-pooled
+ * q/k scores pick each video query tile's top (1 - sparsity) share of video
+ * key tiles (text/audio tiles always kept), fine attention runs over the
+ * chosen tiles, and with a gate a softmax over all tile scores mixes the
+ * pooled v in: o = fine + coarse * gate.  The tile statistics are computed in
+ * the reference's order, so the tile choice is the CPU's; the attention itself
+ * matches within rel-Frobenius 2e-3.  NULL pointers or non-positive sizes are
+ * a silent no-op; head dims other than 64/128, tiles above 64 or more than
+ * 4096 tiles print "not supported" and leave o unwritten.  Replaces
+ * src/core/fh3_vsa.c:186-507 (declared at include/fh3/fh3.h:118 there). */
+void fh3_vsa_attention(const Fh3VsaCfg *c, const float *q, const float *k, const float *v, const float *gate,
+                       float *o, const Fh3Seq *seq, int heads, int head_dim);
 
 /* Seeded N(0,1) fp32 generator: Philox4x32-10 (Salmon et al., SC'11) with
  * Box-Muller, one counter per 4 outputs.  Same stream layout as the

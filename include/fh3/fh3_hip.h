@@ -140,6 +140,25 @@ int fh3_hip_attention_qkv_dev(const float *d_qkv, int n, int heads, int hd, cons
                               const float *d_knorm_w, float eps, const float *d_cos, const float *d_sin, int rot_dim,
                               float *d_o, void *stream);
 
+/* Video sparse attention on the device (fh3_vsa_attention, reference
+ * src/core/fh3_vsa.c:186-507): q, k, v, gate (may be NULL), o are device
+ * arrays [n][heads][head_dim]; c and seq are host structs (seq's counts and
+ * video grid).  The qkv form reads q, k, v from the qkv projection output
+ * d_qkv [n][3 * heads * head_dim] and first applies the per-head q/k rmsnorm
+ * and rope3 (as fh3_hip_attention_qkv_dev; src/model/fh3_dit.c:390-409).
+ * Same limits as fh3_vsa_attention.  The tile geometry of the last sequence
+ * shape is kept on the device; a new shape synchronises the device once to
+ * replace it.  Workspace (library-owned): the fp16 operands, pooled tiles,
+ * heads * T^2 tile scores and the tile lists (T = number of tiles); calls that
+ * overlap on different streams must not share it. */
+int fh3_hip_vsa_attention_dev(const Fh3VsaCfg *c, const float *d_q, const float *d_k, const float *d_v,
+                              const float *d_gate, float *d_o, const Fh3Seq *seq, int heads, int head_dim,
+                              void *stream);
+int fh3_hip_vsa_attention_qkv_dev(const Fh3VsaCfg *c, const float *d_qkv, const float *d_qnorm_w,
+                                  const float *d_knorm_w, float eps, const float *d_cos, const float *d_sin,
+                                  int rot_dim, const float *d_gate, float *d_o, const Fh3Seq *seq, int heads,
+                                  int head_dim, void *stream);
+
 /* HIP graph capture of work enqueued on a stream (NULL = the compute
  * stream), for launch-bound loops such as small-M text-encoder layers:
  * begin, enqueue fh3_hip_* calls on that stream, end -> an executable graph

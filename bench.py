@@ -282,6 +282,47 @@ def dit_attention(ev, st, n=16384, heads=40, hd=128, rot=96):
             b.close()
 
 
+def dit_vsa(ev, st, heads=56, hd=128, rot=96, sparsity=0.8):
+    """The DiT's default attention, video sparse attention, at two sequence
+    shapes from the reference CLI's dimension rules (src/cli/fh3_cli.c:217-252;
+    6 text tokens): its default 640x384, 39 frames (130 audio tokens, video
+    grid 12x12x20, n = 3016) and 1024x576, 73 frames (244 audio tokens, grid
+    22x18x32, n = 12922); 56 heads of 128 as the real model.  One call =
+    fh3_hip_vsa_attention_qkv_dev from a qkv projection output with q/k
+    rmsnorm, rope3 and the gate.  dense_equiv_TFLOPs = 4 n^2 hd heads / time:
+    the rate dense attention would need to match it."""
+    out = []
+    for label, n_text, n_audio, grid in (("640x384x39f", 6, 130, (12, 12, 20)), ("1024x576x73f", 6, 244, (22, 18, 32))):
+        nv = grid[0] * grid[1] * grid[2]
+        n = n_text + n_audio + nv
+        inner = heads * hd
+        qkv = F.DeviceBuffer.from_array(F.synth_x("normal", 4, 700, n, 3 * inner))
+        gate = F.DeviceBuffer.from_array(F.synth_x("normal", 4, 701, n, inner))
+        w = F.DeviceBuffer.from_array(np.ones(hd, np.float32))
+        ang = np.outer(np.arange(n, dtype=np.float64), 1e-2 * np.arange(1, rot // 2 + 1))
+        ang = np.concatenate([ang, ang], axis=1)
+        cs = F.DeviceBuffer.from_array(np.cos(ang).astype(np.float32))
+        sn = F.DeviceBuffer.from_array(np.sin(ang).astype(np.float32))
+        o = F.DeviceBuffer(n * inner * 4)
+        seq = F.seq_of(n, n_text, n_audio, grid=grid)
+        try:
+            def call(i):
+                F.vsa_attention_qkv_dev(qkv, gate, o, seq, heads, hd, sparsity, 64, w, w, 1e-5, cs, sn, rot)
+            for i in range(3):
+                call(i)
+            F.synchronize()
+            ms = ev.time_ms(call, 10, st)
+            dense = 4.0 * n * n * hd * heads
+            out.append({"shape": label, "n": n, "text": n_text, "audio": n_audio, "video_grid": list(grid),
+                        "heads": heads, "head_dim": hd, "sparsity": sparsity, "call_ms": round(ms, 4),
+                        "dense_equiv_TFLOPs": round(dense / (ms * 1e-3) / 1e12, 1)})
+            log("[bench] DiT VSA %s n=%d: %.3f ms" % (label, n, ms))
+        finally:
+            for b in (qkv, gate, w, cs, sn, o):
+                b.close()
+    return out
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline
 # ---------------------------------------------------------------------------
@@ -477,6 +518,12 @@ def main():
     except Exception as e:  # keep the headline line when this leg fails
         log("[bench] DiT attention failed: %r" % (e,))
         extra["dit_attention"] = {"error": repr(e)}
+
+    try:
+        extra["dit_vsa"] = dit_vsa(ev, st)
+    except Exception as e:  # keep the headline line when this leg fails
+        log("[bench] DiT VSA failed: %r" % (e,))
+        extra["dit_vsa"] = {"error": repr(e)}
 
     # ---------------- DiT blocks streamed through the trunk ----------------
     if not args.no_stream:

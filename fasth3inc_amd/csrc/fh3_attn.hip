@@ -50,10 +50,31 @@ __device__ __forceinline__ int vt_key(int p) {
     return (p & ~15) + ((b & 3) | ((b & 4) << 1) | ((b & 8) >> 1));
 }
 
-// F32OUT: write the normalised / rotated q and k as fp32 rows
-// Qf/Kf[slot][h][d] (token order, stride heads * HD) instead of the fp16
-// operands, and leave v alone -- the inputs of the VSA tile statistics.
-template <int HD, bool F32OUT>
+// Tile pooling (video sparse attention): with a gather map each prep
+// workgroup holds exactly one 64-slot tile, so it also writes the tile's
+// mean-pooled q, k (and v when vpool is set), pool[h][tile][d] = sum over the
+// tile's tokens in order of x * inv[tile], from the final fp32 rows (after
+// norm and rope, before the softmax scale) -- the reference's accumulation
+// order and roundings (src/core/fh3_vsa.c:224-250).
+struct Pool {
+    const float *inv;
+    const int *cnt;
+    float *q, *k, *v;
+    int T;
+};
+
+// sum over the first cnt rows of sx, in row order, times w (thread d < HD)
+template <int HD>
+__device__ __forceinline__ void pool_rows(const float (*sx)[HD + 4], int cnt, float w, float *dst) {
+    const int d = threadIdx.x;
+    if (d < HD) {
+        float a = 0.f;
+        for (int r = 0; r < cnt; r++) a = a + sx[r][d] * w;
+        dst[d] = a;
+    }
+}
+
+template <int HD>
 __global__ __launch_bounds__(256) void k_attn_prep(const float *__restrict__ q, const float *__restrict__ k,
                                                    const float *__restrict__ v, int64_t ld, int64_t ldv, int n,
                                                    const int *__restrict__ gather,
@@ -61,8 +82,7 @@ __global__ __launch_bounds__(256) void k_attn_prep(const float *__restrict__ q, 
                                                    float eps, const float *__restrict__ cosb,
                                                    const float *__restrict__ sinb, int rot, float qscale,
                                                    int n_pad, _Float16 *__restrict__ Qp, _Float16 *__restrict__ Kp,
-                                                   _Float16 *__restrict__ Vt, float *__restrict__ Qf,
-                                                   float *__restrict__ Kf, int heads) {
+                                                   _Float16 *__restrict__ Vt, Pool pl) {
     constexpr int DPT = HD / 4;
     __shared__ float sx[ATT_PREP_T][HD + 4];
     const int t = threadIdx.x, r = t >> 2, c = t & 3;
@@ -134,13 +154,13 @@ __global__ __launch_bounds__(256) void k_attn_prep(const float *__restrict__ q, 
                 }
             }
         }
-        if (F32OUT) {
-            if (tok >= 0) {
-                f32x4 *dst = (f32x4 *)((which ? Kf : Qf) + ((size_t)tok * heads + h) * HD + d0);
+        const int tile = blockIdx.x;
+        if (pl.q && tile < pl.T) {  // uniform over the workgroup
+            __syncthreads();
 #pragma unroll
-                for (int i = 0; i < DPT / 4; i++) dst[i] = f32x4{x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]};
-            }
-            continue;
+            for (int i = 0; i < DPT; i++) sx[r][d0 + i] = x[i];
+            __syncthreads();
+            pool_rows<HD>(sx, pl.cnt[tile], pl.inv[tile], (which ? pl.k : pl.q) + ((size_t)h * pl.T + tile) * HD);
         }
         if (!which) {
 #pragma unroll
@@ -156,7 +176,6 @@ __global__ __launch_bounds__(256) void k_attn_prep(const float *__restrict__ q, 
         }
     }
 
-    if (F32OUT) return;
     // v: through LDS, written transposed in the vt_key order
     __syncthreads();
     if (tok >= 0) {
@@ -172,6 +191,8 @@ __global__ __launch_bounds__(256) void k_attn_prep(const float *__restrict__ q, 
         for (int i = 0; i < DPT; i++) sx[r][d0 + i] = 0.f;
     }
     __syncthreads();
+    if (pl.v && blockIdx.x < pl.T)
+        pool_rows<HD>(sx, pl.cnt[blockIdx.x], pl.inv[blockIdx.x], pl.v + ((size_t)h * pl.T + blockIdx.x) * HD);
     constexpr int PER = ATT_PREP_T * HD / 256;  // slots written per thread (32 or 16)
     constexpr int GROUPS = ATT_PREP_T / PER;
     const int d = t / GROUPS, p0 = (t % GROUPS) * PER;
@@ -405,28 +426,6 @@ __global__ __launch_bounds__(256, 2) void k_attn_fwd(const _Float16 *__restrict_
 // attention then runs on k_attn_fwd over each query tile's selected tiles.
 // ---------------------------------------------------------------------------
 
-// pool[h][i][d] = sum over the tile's tokens in order of x[tok][h][d] * inv[i]
-template <int HD>
-__global__ __launch_bounds__(HD) void k_vsa_pool(const float *__restrict__ q, const float *__restrict__ k,
-                                                 const float *__restrict__ v, int64_t ld, int64_t ldv, int heads,
-                                                 const int *__restrict__ tok, const int *__restrict__ off,
-                                                 const float *__restrict__ inv, int T, float *__restrict__ qp,
-                                                 float *__restrict__ kp, float *__restrict__ vp) {
-    const int i = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
-    const float w = inv[i];
-    float aq = 0.f, ak = 0.f, av = 0.f;
-    for (int r = off[i]; r < off[i + 1]; r++) {
-        const size_t t = (size_t)tok[r], at = t * ld + (size_t)h * HD + d;
-        aq = aq + q[at] * w;
-        ak = ak + k[at] * w;
-        if (vp) av = av + v[t * ldv + (size_t)h * HD + d] * w;
-    }
-    const size_t o = ((size_t)h * T + i) * HD + d;
-    qp[o] = aq;
-    kp[o] = ak;
-    if (vp) vp[o] = av;
-}
-
 // scores[h][i][j] = (sum_d qp[h][i][d] * kp[h][j][d], in order) * scale
 template <int HD>
 __global__ __launch_bounds__(256) void k_vsa_scores(const float *__restrict__ qp, const float *__restrict__ kp,
@@ -564,6 +563,7 @@ __global__ __launch_bounds__(256) void k_vsa_lists(const float *__restrict__ sc,
 template <int HD>
 __global__ __launch_bounds__(HD) void k_vsa_coarse(const float *__restrict__ sc, const float *__restrict__ vp,
                                                    int T, float *__restrict__ coarse) {
+    extern __shared__ float wsh[];  // [T] softmax weights
     __shared__ float red[HD / 64];
     __shared__ float bc[2];
     const int i = blockIdx.x, h = blockIdx.y, d = threadIdx.x, lane = d & 63, wave = d >> 6;
@@ -581,7 +581,10 @@ __global__ __launch_bounds__(HD) void k_vsa_coarse(const float *__restrict__ sc,
     __syncthreads();
     mx = bc[0];
     float sum = 0.f;
-    for (int j = d; j < T; j += HD) sum += expf(srow[j] - mx);
+    for (int j = d; j < T; j += HD) {
+        wsh[j] = expf(srow[j] - mx);
+        sum += wsh[j];
+    }
     for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
     __syncthreads();
     if (lane == 0) red[wave] = sum;
@@ -593,9 +596,11 @@ __global__ __launch_bounds__(HD) void k_vsa_coarse(const float *__restrict__ sc,
     }
     __syncthreads();
     const float inv = bc[1];
+    for (int j = d; j < T; j += HD) wsh[j] = wsh[j] * inv;
+    __syncthreads();
     float acc = 0.f;
     const float *vcol = vp + (size_t)h * T * HD + d;
-    for (int j = 0; j < T; j++) acc += expf(srow[j] - mx) * inv * vcol[(size_t)j * HD];
+    for (int j = 0; j < T; j++) acc += wsh[j] * vcol[(size_t)j * HD];
     coarse[((size_t)h * T + i) * HD + d] = acc;
 }
 
@@ -608,9 +613,8 @@ hipError_t attn_launch(const float *q, const float *k, const float *v, int64_t l
     _Float16 *Kp = Qp + (size_t)heads * n_pad * HD;
     _Float16 *Vt = Kp + (size_t)heads * n_pad * HD;
     const float qscale = 1.4426950408889634f / sqrtf((float)HD);
-    hipLaunchKernelGGL((k_attn_prep<HD, false>), dim3(n_pad / ATT_PREP_T, heads), dim3(256), 0, st, q, k, v, ld, ld,
-                       n, (const int *)nullptr, qn_w, kn_w, eps, cosb, sinb, rot, qscale, n_pad, Qp, Kp, Vt,
-                       (float *)nullptr, (float *)nullptr, heads);
+    hipLaunchKernelGGL(k_attn_prep<HD>, dim3(n_pad / ATT_PREP_T, heads), dim3(256), 0, st, q, k, v, ld, ld, n,
+                       (const int *)nullptr, qn_w, kn_w, eps, cosb, sinb, rot, qscale, n_pad, Qp, Kp, Vt, Pool{});
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int blocks = heads * (n_pad / ATT_QB);
@@ -680,24 +684,23 @@ VsaWs vsa_ws(void *base, int T, int heads, int hd) {
 }
 
 template <int HD>
-hipError_t vsa_launch(const float *q, const float *k, const float *v, int64_t ld, int64_t ldv, const float *gate,
-                      float *o, int64_t o_ld, int heads, const int *tok, const int *off, const float *inv,
-                      const int *gather, const int *cnt, int T, int P, int kv, int all, float scale, void *ws,
-                      hipStream_t st) {
+hipError_t vsa_launch(const float *q, const float *k, const float *v, int64_t ld, int64_t ldv, const float *qn_w,
+                      const float *kn_w, float eps, const float *cosb, const float *sinb, int rot, const float *gate,
+                      float *o, int64_t o_ld, int heads, const float *inv, const int *gather, const int *cnt, int T,
+                      int P, int kv, int all, float scale, void *ws, hipStream_t st) {
     const int n_pad = (int)fh3k_attn_pad(ATT_KT * T);
     const int nqb = n_pad / ATT_QB;
     VsaWs w = vsa_ws(ws, T, heads, HD);
     const float qscale = 1.4426950408889634f / sqrtf((float)HD);
-    hipLaunchKernelGGL((k_attn_prep<HD, false>), dim3(n_pad / ATT_PREP_T, heads), dim3(256), 0, st, q, k, v, ld, ldv,
-                       ATT_KT * T, gather, (const float *)nullptr, (const float *)nullptr, 0.f,
-                       (const float *)nullptr, (const float *)nullptr, 0, qscale, n_pad, w.Qp, w.Kp, w.Vt,
-                       (float *)nullptr, (float *)nullptr, heads);
-    hipLaunchKernelGGL((k_vsa_pool<HD>), dim3(T, heads), dim3(HD), 0, st, q, k, v, ld, ldv, heads, tok, off, inv, T, w.qp,
-                       w.kp, gate ? w.vp : (float *)nullptr);
+    Pool pl{inv, cnt, w.qp, w.kp, gate ? w.vp : nullptr, T};
+    hipLaunchKernelGGL(k_attn_prep<HD>, dim3(n_pad / ATT_PREP_T, heads), dim3(256), 0, st, q, k, v, ld, ldv,
+                       ATT_KT * T, gather, qn_w, kn_w, eps, cosb, sinb, rot, qscale, n_pad, w.Qp, w.Kp, w.Vt, pl);
     hipLaunchKernelGGL((k_vsa_scores<HD>), dim3(T, heads), dim3(256), 0, st, w.qp, w.kp, T, scale, w.sc);
     hipLaunchKernelGGL(k_vsa_lists, dim3(nqb, heads), dim3(256), (size_t)align256(6 * (size_t)T), st, w.sc, T, P, kv,
                        all, nqb, w.lists, w.list_len);
-    if (gate) hipLaunchKernelGGL((k_vsa_coarse<HD>), dim3(T, heads), dim3(HD), 0, st, w.sc, w.vp, T, w.coarse);
+    if (gate)
+        hipLaunchKernelGGL((k_vsa_coarse<HD>), dim3(T, heads), dim3(HD), (size_t)T * sizeof(float), st, w.sc, w.vp, T,
+                           w.coarse);
     Sparse sp{w.lists, w.list_len, cnt, gather, gate ? w.coarse : nullptr, gate, T};
     hipLaunchKernelGGL((k_attn_fwd<HD, true>), dim3(heads * nqb), dim3(64 * ATT_NW), 0, st, w.Qp, w.Kp, w.Vt,
                        ATT_KT * T, n_pad, heads, o, o_ld, sp);
@@ -711,33 +714,16 @@ extern "C" int fh3k_vsa_max_tiles(void) { return 4096; }
 extern "C" size_t fh3k_vsa_ws_bytes(int T, int heads, int hd) { return vsa_ws(nullptr, T, heads, hd).bytes; }
 
 extern "C" hipError_t fh3k_vsa_attention(const float *q, const float *k, const float *v, int64_t ld, int64_t ldv,
-                                         const float *gate, float *o, int64_t o_ld, int heads, int hd,
-                                         const int *tok, const int *off, const float *inv, const int *gather,
-                                         const int *cnt, int T, int P, int kv, int all, float scale, void *ws,
-                                         hipStream_t st) {
+                                         const float *qn_w, const float *kn_w, float eps, const float *cosb,
+                                         const float *sinb, int rot, const float *gate, float *o, int64_t o_ld,
+                                         int heads, int hd, const float *inv, const int *gather, const int *cnt,
+                                         int T, int P, int kv, int all, float scale, void *ws, hipStream_t st) {
     if (T <= 0 || T > fh3k_vsa_max_tiles()) return hipErrorInvalidValue;
     if (hd == 128)
-        return vsa_launch<128>(q, k, v, ld, ldv, gate, o, o_ld, heads, tok, off, inv, gather, cnt, T, P, kv, all,
-                               scale, ws, st);
+        return vsa_launch<128>(q, k, v, ld, ldv, qn_w, kn_w, eps, cosb, sinb, rot, gate, o, o_ld, heads, inv, gather,
+                               cnt, T, P, kv, all, scale, ws, st);
     if (hd == 64)
-        return vsa_launch<64>(q, k, v, ld, ldv, gate, o, o_ld, heads, tok, off, inv, gather, cnt, T, P, kv, all,
-                              scale, ws, st);
+        return vsa_launch<64>(q, k, v, ld, ldv, qn_w, kn_w, eps, cosb, sinb, rot, gate, o, o_ld, heads, inv, gather,
+                              cnt, T, P, kv, all, scale, ws, st);
     return hipErrorInvalidValue;
-}
-
-extern "C" hipError_t fh3k_qk_normrope_f32(const float *q, const float *k, int64_t ld, int n, int heads, int hd,
-                                           const float *qn_w, const float *kn_w, float eps, const float *cosb,
-                                           const float *sinb, int rot, float *qo, float *ko, hipStream_t st) {
-    const int n64 = (n + ATT_PREP_T - 1) / ATT_PREP_T * ATT_PREP_T;
-    if (hd == 128)
-        hipLaunchKernelGGL((k_attn_prep<128, true>), dim3(n64 / ATT_PREP_T, heads), dim3(256), 0, st, q, k,
-                           (const float *)nullptr, ld, ld, n, (const int *)nullptr, qn_w, kn_w, eps, cosb, sinb, rot,
-                           1.f, n64, (_Float16 *)nullptr, (_Float16 *)nullptr, (_Float16 *)nullptr, qo, ko, heads);
-    else if (hd == 64)
-        hipLaunchKernelGGL((k_attn_prep<64, true>), dim3(n64 / ATT_PREP_T, heads), dim3(256), 0, st, q, k,
-                           (const float *)nullptr, ld, ld, n, (const int *)nullptr, qn_w, kn_w, eps, cosb, sinb, rot,
-                           1.f, n64, (_Float16 *)nullptr, (_Float16 *)nullptr, (_Float16 *)nullptr, qo, ko, heads);
-    else
-        return hipErrorInvalidValue;
-    return hipGetLastError();
 }

@@ -35,7 +35,6 @@ struct State {
     DevBuf w16;                     // fp16 rows of a weight of another type
     DevBuf attn;                    // fp16 attention operands (Qp, Kp, Vt)
     DevBuf vsa_ws;                  // VSA operands, tile statistics, scores and tile lists
-    DevBuf vsa_qk;                  // fp32 normalised/rotated q, k of the qkv VSA entry
     DevBuf vsa_geo;                 // VSA tile geometry of the last sequence shape
     int vsa_key[8] = {-1, -1, -1, -1, -1, -1, -1, -1};
     int vsa_T = 0, vsa_P = 0;
@@ -202,7 +201,7 @@ extern "C" void fh3_hip_shutdown(void) {
     std::lock_guard<std::recursive_mutex> lk(g.mu);
     if (!g.init) return;
     (void)hipDeviceSynchronize();
-    DevBuf *bufs[] = {&g.ws, &g.ws2, &g.w16, &g.attn, &g.vsa_ws, &g.vsa_qk, &g.vsa_geo,
+    DevBuf *bufs[] = {&g.ws, &g.ws2, &g.w16, &g.attn, &g.vsa_ws, &g.vsa_geo,
                       &g.st_w, &g.st_x, &g.st_y, &g.st_b};
     for (DevBuf *b : bufs) {
         if (b->p) (void)hipFree(b->p);
@@ -632,8 +631,9 @@ static int vsa_geometry(const Fh3Seq *sq, int tile, std::vector<int> &tok, std::
     return (int)off.size() - 1;
 }
 
-// Device copy of the geometry: tok[n], off[T+1], inv[T], cnt[T], gather[slots]
-// (kept while the sequence shape does not change).
+// Device copy of the geometry: inv[T] (1/count), cnt[T], gather[slots] (token
+// of each 64-slot tile position, -1 empty), kept while the sequence shape
+// does not change.
 static int vsa_plan(const Fh3Seq *sq, int tile, const char *fn) {
     const int key[8] = {sq->seq_len, sq->num_text, sq->num_audio, sq->num_video, sq->grid_t, sq->grid_h, sq->grid_w,
                         tile};
@@ -644,11 +644,8 @@ static int vsa_plan(const Fh3Seq *sq, int tile, const char *fn) {
     if (T <= 0 || T > fh3k_vsa_max_tiles())
         return set_err(FH3_E_INVALID, "%s: %d tiles (at most %d on the device)", fn, T, fh3k_vsa_max_tiles());
     const int64_t slots = fh3k_attn_pad(64 * T);
-    const size_t n = (size_t)sq->seq_len;
-    std::vector<int> host(n + (T + 1) + 2 * (size_t)T + (size_t)slots);
-    int *h_tok = host.data(), *h_off = h_tok + n, *h_inv = h_off + T + 1, *h_cnt = h_inv + T, *h_gat = h_cnt + T;
-    memcpy(h_tok, tok.data(), n * sizeof(int));
-    memcpy(h_off, off.data(), (T + 1) * sizeof(int));
+    std::vector<int> host(2 * (size_t)T + (size_t)slots);
+    int *h_inv = host.data(), *h_cnt = h_inv + T, *h_gat = h_cnt + T;
     for (int i = 0; i < T; i++) {
         const int c = off[i + 1] - off[i];
         const float inv = 1.0f / (float)c;
@@ -670,6 +667,7 @@ static int vsa_plan(const Fh3Seq *sq, int tile, const char *fn) {
 }
 
 static int vsa_dev(const Fh3VsaCfg *c, const float *q, const float *k, const float *v, int64_t ld, int64_t ldv,
+                   const float *qn_w, const float *kn_w, float eps, const float *cs, const float *sn, int rot,
                    const float *gate, float *o, const Fh3Seq *sq, int heads, int hd, void *stream, const char *fn) {
     if (!q || !k || !v || !o || !sq || sq->seq_len <= 0 || heads <= 0 || hd <= 0)
         return set_err(FH3_E_INVALID, "%s: NULL pointer or non-positive size", fn);
@@ -693,14 +691,12 @@ static int vsa_dev(const Fh3VsaCfg *c, const float *q, const float *k, const flo
     }
     const int all = sparsity <= 0.0f || kv == NV;
     if ((rc = grow(g.vsa_ws, fh3k_vsa_ws_bytes(T, heads, hd))) != FH3_OK) return rc;
-    const size_t n = (size_t)sq->seq_len;
-    const int *d_tok = (const int *)g.vsa_geo.p, *d_off = d_tok + n;
-    const float *d_inv = (const float *)(d_off + T + 1);
+    const float *d_inv = (const float *)g.vsa_geo.p;
     const int *d_cnt = (const int *)(d_inv + T), *d_gat = d_cnt + T;
     const float scale = 1.0f / sqrtf((float)hd);
-    FH3_HIPCALL(fh3k_vsa_attention(q, k, v, ld, ldv, gate, o, (int64_t)heads * hd, heads, hd, d_tok, d_off, d_inv,
-                                   d_gat, d_cnt, T, P, kv, all, scale, g.vsa_ws.p,
-                                   stream ? (hipStream_t)stream : g.stream));
+    FH3_HIPCALL(fh3k_vsa_attention(q, k, v, ld, ldv, qn_w, kn_w, eps, cs, sn, cs ? rot : 0, gate, o,
+                                   (int64_t)heads * hd, heads, hd, d_inv, d_gat, d_cnt, T, P, kv, all, scale,
+                                   g.vsa_ws.p, stream ? (hipStream_t)stream : g.stream));
     return FH3_OK;
 }
 
@@ -708,7 +704,8 @@ extern "C" int fh3_hip_vsa_attention_dev(const Fh3VsaCfg *c, const float *d_q, c
                                          const float *d_gate, float *d_o, const Fh3Seq *seq, int heads, int head_dim,
                                          void *stream) {
     const int64_t ld = (int64_t)heads * head_dim;
-    return vsa_dev(c, d_q, d_k, d_v, ld, ld, d_gate, d_o, seq, heads, head_dim, stream, "fh3_hip_vsa_attention_dev");
+    return vsa_dev(c, d_q, d_k, d_v, ld, ld, nullptr, nullptr, 0.f, nullptr, nullptr, 0, d_gate, d_o, seq, heads,
+                   head_dim, stream, "fh3_hip_vsa_attention_dev");
 }
 
 extern "C" int fh3_hip_vsa_attention_qkv_dev(const Fh3VsaCfg *c, const float *d_qkv, const float *d_qnorm_w,
@@ -724,16 +721,9 @@ extern "C" int fh3_hip_vsa_attention_qkv_dev(const Fh3VsaCfg *c, const float *d_
         return set_err(FH3_E_INVALID, "%s: rope needs cos and sin with an even rot_dim <= head_dim", fn);
     if ((uintptr_t)d_qkv & 15u || (uintptr_t)d_cos & 15u || (uintptr_t)d_sin & 15u)
         return set_err(FH3_E_INVALID, "%s: qkv, cos and sin must be 16-byte aligned", fn);
-    int rc = ensure_init();
-    if (rc != FH3_OK) return rc;
-    std::lock_guard<std::recursive_mutex> lk(g.mu);
-    const int64_t inner = (int64_t)heads * head_dim, n = seq->seq_len;
-    if ((rc = grow(g.vsa_qk, (size_t)(2 * n * inner) * sizeof(float))) != FH3_OK) return rc;
-    float *qf = (float *)g.vsa_qk.p, *kf = qf + n * inner;
-    hipStream_t st = stream ? (hipStream_t)stream : g.stream;
-    FH3_HIPCALL(fh3k_qk_normrope_f32(d_qkv, d_qkv + inner, 3 * inner, (int)n, heads, head_dim, d_qnorm_w, d_knorm_w,
-                                     eps, d_cos, d_sin, d_cos ? rot_dim : 0, qf, kf, st));
-    return vsa_dev(c, qf, kf, d_qkv + 2 * inner, inner, 3 * inner, d_gate, d_o, seq, heads, head_dim, stream, fn);
+    const int64_t inner = (int64_t)heads * head_dim;
+    return vsa_dev(c, d_qkv, d_qkv + inner, d_qkv + 2 * inner, 3 * inner, 3 * inner, d_qnorm_w, d_knorm_w, eps, d_cos,
+                   d_sin, rot_dim, d_gate, d_o, seq, heads, head_dim, stream, fn);
 }
 
 // ---------------------------------------------------------------------------

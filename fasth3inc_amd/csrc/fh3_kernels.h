@@ -86,23 +86,19 @@ hipError_t fh3k_attention(const float *q, const float *k, const float *v, int64_
                           const float *qn_w, const float *kn_w, float eps, const float *cosb, const float *sinb,
                           int rot, void *ws, float *o, int64_t o_ld, hipStream_t st);
 
-// Video sparse attention.  q, k at token stride ld, v at ldv; gate and o
-// [n][heads][hd] at stride o_ld.  Tile geometry from the host: tok[n] (token
-// of each tile position), off[T + 1], inv[T] = 1/count, gather[round_up(64 T,
-// 128)] (token of each slot, -1 empty), cnt[T]; P prefix tiles, kv video tiles
-// kept per video query tile (all = 1 keeps every tile), scale = 1/sqrt(hd).
-// T <= fh3k_vsa_max_tiles(); ws holds fh3k_vsa_ws_bytes(T, heads, hd).
+// Video sparse attention.  q, k at token stride ld, v at ldv; optional per-head
+// q/k rmsnorm and rope3 as fh3k_attention; gate and o [n][heads][hd] at stride
+// o_ld.  Tile geometry from the host: inv[T] = 1/count, cnt[T], gather[
+// round_up(64 T, 128)] (token of each slot, -1 empty); P prefix tiles, kv video
+// tiles kept per video query tile (all = 1 keeps every tile), scale =
+// 1/sqrt(hd).  T <= fh3k_vsa_max_tiles(); ws holds fh3k_vsa_ws_bytes(T, heads, hd).
 int fh3k_vsa_max_tiles(void);
 size_t fh3k_vsa_ws_bytes(int T, int heads, int hd);
 hipError_t fh3k_vsa_attention(const float *q, const float *k, const float *v, int64_t ld, int64_t ldv,
-                              const float *gate, float *o, int64_t o_ld, int heads, int hd, const int *tok,
-                              const int *off, const float *inv, const int *gather, const int *cnt, int T, int P,
-                              int kv, int all, float scale, void *ws, hipStream_t st);
-// q/k per-head rmsnorm (optional) and rope3 (optional) into fp32 rows
-// qo/ko[n][heads][hd] (stride heads * hd).
-hipError_t fh3k_qk_normrope_f32(const float *q, const float *k, int64_t ld, int n, int heads, int hd,
-                                const float *qn_w, const float *kn_w, float eps, const float *cosb,
-                                const float *sinb, int rot, float *qo, float *ko, hipStream_t st);
+                              const float *qn_w, const float *kn_w, float eps, const float *cosb, const float *sinb,
+                              int rot, const float *gate, float *o, int64_t o_ld, int heads, int hd, const float *inv,
+                              const int *gather, const int *cnt, int T, int P, int kv, int all, float scale, void *ws,
+                              hipStream_t st);
 
 // Largest in-dimension (K) the activation preparation handles.
 int fh3k_max_in(void);

@@ -16,6 +16,10 @@ Workloads (each launch sequence is preceded by one untimed warmup launch):
          (hidden 5120): fh3_hip_attention_qkv_dev from a qkv projection
          output with q/k rmsnorm and rope3 on 96 channels -> k_attn_prep,
          k_attn_fwd
+  vsa    video sparse attention at the reference CLI's 1024x576, 73-frame
+         shape (6 text + 244 audio tokens, video grid 22x18x32, n = 12922),
+         56 heads of 128, sparsity 0.8, with q/k rmsnorm, rope3 and the gate:
+         fh3_hip_vsa_attention_qkv_dev -> every VSA kernel
 """
 import argparse
 import sys
@@ -89,9 +93,30 @@ def attn(reps, n=16384, heads=40, hd=128, rot=96):
         b.close()
 
 
+def vsa(reps, heads=56, hd=128, rot=96):
+    n_text, n_audio, grid = 6, 244, (22, 18, 32)
+    n = n_text + n_audio + grid[0] * grid[1] * grid[2]
+    inner = heads * hd
+    qkv = F.DeviceBuffer.from_array(F.synth_x("normal", 4, 700, n, 3 * inner))
+    gate = F.DeviceBuffer.from_array(F.synth_x("normal", 4, 701, n, inner))
+    w = F.DeviceBuffer.from_array(np.ones(hd, np.float32))
+    ang = np.outer(np.arange(n, dtype=np.float64), 1e-2 * np.arange(1, rot // 2 + 1))
+    ang = np.concatenate([ang, ang], axis=1)
+    cs = F.DeviceBuffer.from_array(np.cos(ang).astype(np.float32))
+    sn = F.DeviceBuffer.from_array(np.sin(ang).astype(np.float32))
+    o = F.DeviceBuffer(n * inner * 4)
+    seq = F.seq_of(n, n_text, n_audio, grid=grid)
+    for _ in range(reps + 1):
+        F.vsa_attention_qkv_dev(qkv, gate, o, seq, heads, hd, 0.8, 64, w, w, 1e-5, cs, sn, rot)
+    F.synchronize()
+    print("vsa n=%d heads=%d hd=%d: %d launches" % (n, heads, hd, reps), flush=True)
+    for b in (qkv, gate, w, cs, sn, o):
+        b.close()
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("workload", choices=("gemv", "gemm", "copy", "attn", "all"))
+    ap.add_argument("workload", choices=("gemv", "gemm", "copy", "attn", "vsa", "all"))
     ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args(argv)
     F.init(0)

@@ -933,10 +933,13 @@ struct GemmRaw {
     u32x4 hv, qv;
 };
 
-__device__ __forceinline__ void gemm_load_raw(const uint8_t *wrow, int s, int h, GemmRaw &r, const GemmRaw &prev) {
-    const uint8_t *blk = wrow + (size_t)(s >> 2) * 144;
-    r.hv = (s & 3) == 0 ? ld16(blk) : prev.hv;
-    r.qv = ld16(blk + 16 + 32 * (s & 3) + 16 * h);
+// CH (the chunk, s % 4) is a compile-time constant, so the header load of
+// chunk 0 is not a branch and a K step is one basic block.
+template <int CH>
+__device__ __forceinline__ void gemm_load_raw(const uint8_t *wrow, int sb, int h, GemmRaw &r, const GemmRaw &prev) {
+    const uint8_t *blk = wrow + (size_t)sb * 144;
+    r.hv = CH == 0 ? ld16(blk) : prev.hv;
+    r.qv = ld16(blk + 16 + 32 * CH + 16 * h);
 }
 
 // B-fragment layout: fragment rb*4 + kk holds rows 32rb..32rb+31 x k 16kk..16kk+15
@@ -1016,24 +1019,40 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
 
     GemmRaw re, ro;            // raw weights of even / odd steps
     half8 xe[2][4], xo[2][4];  // activations of even / odd steps
-    gemm_load_raw(wrow, 0, h, re, re);
+    gemm_load_raw<0>(wrow, 0, h, re, re);
     gemm_load_x(xa0, xa1, 0, xe);
-    gemm_load_raw(wrow, 1, h, ro, re);
+    gemm_load_raw<1>(wrow, 0, h, ro, re);
     gemm_dequant(lds[0], re, 0, wf, wl, h);
     __syncthreads();
-    for (int s = 0; s < S; s += 2) {
-        // even step s: MFMA(s) from lds[0]; dequant(s+1) into lds[1]
+    // one super-block (4 K steps) per iteration; the loads and the dequant of
+    // the step after the last are clamped onto the last super-block (valid
+    // addresses, results unused), so no step has a branch and the scheduler
+    // can interleave each step's loads and dequant with its MFMAs
+    for (int sb = 0; sb < S / 4; sb++) {
+        const int s = 4 * sb;
+        const int nb = sb + 1 < S / 4 ? sb + 1 : sb;
+        // step s (chunk 0): MFMA from lds[0]; dequant chunk 1 into lds[1]
         gemm_load_x(xa0, xa1, s + 1, xo);
-        if (s + 2 < S) gemm_load_raw(wrow, s + 2, h, re, ro);
-        gemm_dequant(lds[1], ro, s + 1, wf, wl, h);
+        gemm_load_raw<2>(wrow, sb, h, re, ro);
+        gemm_dequant(lds[1], ro, 1, wf, wl, h);
         gemm_mfma(lds[0], lane, xe, acc);
         __syncthreads();
-        // odd step s+1: MFMA(s+1) from lds[1]; dequant(s+2) into lds[0]
-        if (s + 2 < S) {
-            gemm_load_x(xa0, xa1, s + 2, xe);
-            gemm_load_raw(wrow, s + 3, h, ro, re);
-            gemm_dequant(lds[0], re, s + 2, wf, wl, h);
-        }
+        // step s+1 (chunk 1): MFMA from lds[1]; dequant chunk 2 into lds[0]
+        gemm_load_x(xa0, xa1, s + 2, xe);
+        gemm_load_raw<3>(wrow, sb, h, ro, re);
+        gemm_dequant(lds[0], re, 2, wf, wl, h);
+        gemm_mfma(lds[1], lane, xo, acc);
+        __syncthreads();
+        // step s+2 (chunk 2): MFMA from lds[0]; dequant chunk 3 into lds[1]
+        gemm_load_x(xa0, xa1, s + 3, xo);
+        gemm_load_raw<0>(wrow, nb, h, re, ro);
+        gemm_dequant(lds[1], ro, 3, wf, wl, h);
+        gemm_mfma(lds[0], lane, xe, acc);
+        __syncthreads();
+        // step s+3 (chunk 3): MFMA from lds[1]; dequant the next chunk 0 into lds[0]
+        gemm_load_x(xa0, xa1, 4 * nb, xe);
+        gemm_load_raw<1>(wrow, nb, h, ro, re);
+        gemm_dequant(lds[0], re, 0, wf, wl, h);
         gemm_mfma(lds[1], lane, xo, acc);
         __syncthreads();
     }

@@ -10,14 +10,15 @@
 //                per-head rmsnorm of q and k (weights [hd]) and rope3 on their
 //                first rot_dim channels are applied on the way; q is scaled by
 //                log2(e)/sqrt(hd) so that the softmax runs on exp2.
-//   k_attn_fwd   flash-style attention: a workgroup owns 128 queries of one
-//                head (4 wavefronts x 32), streams 64-key tiles of K and V^T
+//   k_attn_fwd   flash-style attention: a workgroup owns 32 queries per
+//                wavefront of one head (8 wavefronts for hd 128, 4 for hd 64
+//                and for the sparse form), streams 64-key tiles of K and V^T
 //                through double-buffered LDS, S^T = K.Q^T and O^T = V^T.P^T on
 //                v_mfma_f32_32x32x16_f16 with fp32 accumulation, and keeps the
 //                running max / sum in fp32 registers.
 //
 // Slots beyond n are zero in the prepared operands and masked as keys, so
-// any n >= 1 works; the prepared buffers hold n_pad = round_up(n, 128) slots.
+// any n >= 1 works; the prepared buffers hold n_pad = round_up(n, 32 x wavefronts) slots.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -32,8 +33,12 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 constexpr int ATT_KT = 64;   // keys per tile
 constexpr int ATT_QW = 32;   // queries per wavefront
-constexpr int ATT_NW = 4;    // wavefronts per workgroup
+constexpr int ATT_NW = 4;    // wavefronts per workgroup of the sparse kernel (two query tiles)
 constexpr int ATT_QB = ATT_QW * ATT_NW;
+// Dense kernel: with hd = 128, 8 wavefronts (256 queries, 2 per SIMD) share
+// each K/V tile in LDS, halving the tile loads and LDS writes per query (+5 %);
+// with hd = 64 the 4-wavefront form keeps 3 wavefronts per SIMD and is faster.
+constexpr int dense_nw(int hd) { return hd == 128 ? 8 : 4; }
 constexpr int ATT_PREP_T = 64;  // slots per prep workgroup
 // The softmax offset m of a query is only raised when a tile's maximum
 // exceeds it by more than ATT_TAU (log2 units), so p = exp2(s - m) <= 2^8 and
@@ -227,8 +232,8 @@ struct Sparse {
     int T;
 };
 
-template <int HD, bool SPARSE>
-__global__ __launch_bounds__(256, 2) void k_attn_fwd(const _Float16 *__restrict__ Qp,
+template <int HD, bool SPARSE, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void k_attn_fwd(const _Float16 *__restrict__ Qp,
                                                      const _Float16 *__restrict__ Kp,
                                                      const _Float16 *__restrict__ Vt, int n, int n_pad,
                                                      int heads, float *__restrict__ O, int64_t o_ld, Sparse sp) {
@@ -236,7 +241,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_fwd(const _Float16 *__restrict_
     constexpr int DB = HD / 32;            // 32-row blocks of O^T
     constexpr int KROW = HD + 8;           // LDS row of K (halfs), padded against bank conflicts
     constexpr int VROW = ATT_KT + 8;       // LDS row of V^T (halfs)
-    constexpr int NT = 64 * ATT_NW;
+    constexpr int NT = 64 * NW;
+    constexpr int QB = ATT_QW * NW;
     constexpr int KCH = ATT_KT * HD / 8 / NT;  // 16-byte chunks per thread per tile, K and V each
     __shared__ _Float16 sk[2][ATT_KT][KROW];
     __shared__ _Float16 sv[2][HD][VROW];
@@ -246,13 +252,13 @@ __global__ __launch_bounds__(256, 2) void k_attn_fwd(const _Float16 *__restrict_
 
     // XCD-aware order: consecutive workgroup ids land on different XCDs, so
     // give each XCD a contiguous run of (head, query block) pairs
-    const int nqb = n_pad / ATT_QB;
+    const int nqb = n_pad / QB;
     const int total = heads * nqb;
     const int id = blockIdx.x;
     const int per = total >> 3;
     const int L = (id < per * 8) ? (id & 7) * per + (id >> 3) : id;
     const int h = L / nqb, qb = L - h * nqb;
-    const int q0 = qb * ATT_QB + wave * ATT_QW;
+    const int q0 = qb * QB + wave * ATT_QW;
 
     const _Float16 *kh = Kp + (size_t)h * n_pad * HD;
     const _Float16 *vh = Vt + (size_t)h * HD * n_pad;
@@ -417,6 +423,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fwd(const _Float16 *__restrict_
             }
     }
 }
+
 
 // ---------------------------------------------------------------------------
 // Video sparse attention (src/core/fh3_vsa.c:186-507).  The tile statistics
@@ -604,11 +611,16 @@ __global__ __launch_bounds__(HD) void k_vsa_coarse(const float *__restrict__ sc,
     coarse[((size_t)h * T + i) * HD + d] = acc;
 }
 
+int64_t attn_pad_dense(int n, int hd) {
+    const int64_t qb = ATT_QW * dense_nw(hd);
+    return ((int64_t)n + qb - 1) / qb * qb;
+}
+
 template <int HD>
 hipError_t attn_launch(const float *q, const float *k, const float *v, int64_t ld, int n, int heads,
                        const float *qn_w, const float *kn_w, float eps, const float *cosb, const float *sinb,
                        int rot, void *ws, float *o, int64_t o_ld, hipStream_t st) {
-    const int n_pad = (int)fh3k_attn_pad(n);
+    const int n_pad = (int)attn_pad_dense(n, HD);
     _Float16 *Qp = (_Float16 *)ws;
     _Float16 *Kp = Qp + (size_t)heads * n_pad * HD;
     _Float16 *Vt = Kp + (size_t)heads * n_pad * HD;
@@ -617,9 +629,10 @@ hipError_t attn_launch(const float *q, const float *k, const float *v, int64_t l
                        (const int *)nullptr, qn_w, kn_w, eps, cosb, sinb, rot, qscale, n_pad, Qp, Kp, Vt, Pool{});
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int blocks = heads * (n_pad / ATT_QB);
-    hipLaunchKernelGGL((k_attn_fwd<HD, false>), dim3(blocks), dim3(64 * ATT_NW), 0, st, Qp, Kp, Vt, n, n_pad, heads,
-                       o, o_ld, Sparse{});
+    constexpr int NW = dense_nw(HD);
+    const int blocks = heads * (n_pad / (ATT_QW * NW));
+    hipLaunchKernelGGL((k_attn_fwd<HD, false, NW>), dim3(blocks), dim3(64 * NW), 0, st, Qp, Kp, Vt, n, n_pad, heads, o,
+                       o_ld, Sparse{});
     return hipGetLastError();
 }
 
@@ -628,7 +641,7 @@ hipError_t attn_launch(const float *q, const float *k, const float *v, int64_t l
 extern "C" int64_t fh3k_attn_pad(int n) { return ((int64_t)n + ATT_QB - 1) / ATT_QB * ATT_QB; }
 
 extern "C" size_t fh3k_attn_ws_bytes(int n, int heads, int hd) {
-    return (size_t)3 * heads * fh3k_attn_pad(n) * hd * sizeof(_Float16);
+    return (size_t)3 * heads * attn_pad_dense(n, hd) * hd * sizeof(_Float16);
 }
 
 extern "C" int fh3k_attn_head_dim_ok(int hd) { return hd == 64 || hd == 128; }
@@ -702,7 +715,7 @@ hipError_t vsa_launch(const float *q, const float *k, const float *v, int64_t ld
         hipLaunchKernelGGL((k_vsa_coarse<HD>), dim3(T, heads), dim3(HD), (size_t)T * sizeof(float), st, w.sc, w.vp, T,
                            w.coarse);
     Sparse sp{w.lists, w.list_len, cnt, gather, gate ? w.coarse : nullptr, gate, T};
-    hipLaunchKernelGGL((k_attn_fwd<HD, true>), dim3(heads * nqb), dim3(64 * ATT_NW), 0, st, w.Qp, w.Kp, w.Vt,
+    hipLaunchKernelGGL((k_attn_fwd<HD, true, ATT_NW>), dim3(heads * nqb), dim3(64 * ATT_NW), 0, st, w.Qp, w.Kp, w.Vt,
                        ATT_KT * T, n_pad, heads, o, o_ld, sp);
     return hipGetLastError();
 }

@@ -232,8 +232,9 @@ struct Sparse {
     int T;
 };
 
+// (the second launch bound is the minimum number of wavefronts per SIMD: two)
 template <int HD, bool SPARSE, int NW>
-__global__ __launch_bounds__(64 * NW, 8 / NW) void k_attn_fwd(const _Float16 *__restrict__ Qp,
+__global__ __launch_bounds__(64 * NW, 2) void k_attn_fwd(const _Float16 *__restrict__ Qp,
                                                      const _Float16 *__restrict__ Kp,
                                                      const _Float16 *__restrict__ Vt, int n, int n_pad,
                                                      int heads, float *__restrict__ O, int64_t o_ld, Sparse sp) {

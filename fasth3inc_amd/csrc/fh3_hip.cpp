@@ -37,6 +37,12 @@ struct State {
     DevBuf vsa_ws;                  // VSA operands, tile statistics, scores and tile lists
     DevBuf vsa_geo;                 // VSA tile geometry of the last sequence shape
     int vsa_key[8] = {-1, -1, -1, -1, -1, -1, -1, -1};
+    struct Reg {
+        const uint8_t *host;
+        size_t bytes;
+        void *dev;
+    };
+    std::vector<Reg> regs;          // registered host weight ranges and their device copies
     int vsa_T = 0, vsa_P = 0;
     DevBuf st_w, st_x, st_y, st_b;  // staging for the host-pointer wrappers
     int path = FH3_HIP_PATH_AUTO;
@@ -208,6 +214,8 @@ extern "C" void fh3_hip_shutdown(void) {
         b->p = nullptr;
         b->cap = 0;
     }
+    for (auto &r : g.regs) (void)hipFree(r.dev);
+    g.regs.clear();
     (void)hipStreamDestroy(g.stream);
     g.stream = nullptr;
     g.init = false;
@@ -597,6 +605,64 @@ extern "C" int fh3_hip_attention_qkv_dev(const float *d_qkv, int n, int heads, i
 }
 
 // ---------------------------------------------------------------------------
+// Weight registration: a host range uploaded once, kept on the device and
+// found by the host-pointer wrappers, which then copy only x in and y out
+// ---------------------------------------------------------------------------
+// Device address of [p, p + bytes) when it lies inside a registered range.
+static const void *registered(const void *p, size_t bytes) {
+    const uint8_t *q = (const uint8_t *)p;
+    for (const auto &r : g.regs)
+        if (q >= r.host && q + bytes <= r.host + r.bytes) return (const uint8_t *)r.dev + (q - r.host);
+    return nullptr;
+}
+
+extern "C" int fh3_hip_register_weights(const void *host, size_t bytes, const void **d_out) {
+    const char *fn = "fh3_hip_register_weights";
+    if (!host || bytes == 0) return set_err(FH3_E_INVALID, "%s: NULL pointer or zero size", fn);
+    int rc = ensure_init();
+    if (rc != FH3_OK) return rc;
+    std::lock_guard<std::recursive_mutex> lk(g.mu);
+    const uint8_t *h = (const uint8_t *)host;
+    for (auto &r : g.regs) {
+        if (r.host == h && r.bytes == bytes) {  // re-registration refreshes the device copy
+            FH3_HIPCALL(hipDeviceSynchronize());
+            FH3_HIPCALL(hipMemcpy(r.dev, host, bytes, hipMemcpyHostToDevice));
+            if (d_out) *d_out = r.dev;
+            return FH3_OK;
+        }
+        if (h < r.host + r.bytes && r.host < h + bytes)
+            return set_err(FH3_E_INVALID, "%s: range overlaps a registered range", fn);
+    }
+    void *dev = nullptr;
+    FH3_HIPCALL(hipMalloc(&dev, bytes));
+    const hipError_t e = hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(dev);
+        return hip_fail(e, "fh3_hip_register_weights upload");
+    }
+    g.regs.push_back({h, bytes, dev});
+    if (d_out) *d_out = dev;
+    return FH3_OK;
+}
+
+extern "C" int fh3_hip_unregister_weights(const void *host) {
+    std::lock_guard<std::recursive_mutex> lk(g.mu);
+    for (size_t i = 0; i < g.regs.size(); i++)
+        if (g.regs[i].host == (const uint8_t *)host) {
+            FH3_HIPCALL(hipDeviceSynchronize());  // enqueued work may still read it
+            FH3_HIPCALL(hipFree(g.regs[i].dev));
+            g.regs.erase(g.regs.begin() + (long)i);
+            return FH3_OK;
+        }
+    return set_err(FH3_E_INVALID, "fh3_hip_unregister_weights: %p is not registered", host);
+}
+
+extern "C" const void *fh3_hip_registered_ptr(const void *host, size_t bytes) {
+    std::lock_guard<std::recursive_mutex> lk(g.mu);
+    return host ? registered(host, bytes) : nullptr;
+}
+
+// ---------------------------------------------------------------------------
 // Video sparse attention
 // ---------------------------------------------------------------------------
 // Tile geometry of src/core/fh3_vsa.c:31-163: text tokens, then audio tokens,
@@ -775,8 +841,10 @@ extern "C" void fh3_dequant(int type, const void *src, float *dst, int64_t n) {
         report("fh3_dequant", rc);
         return;
     }
-    hipError_t e = hipMemcpy(g.st_w.p, src, in_bytes, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = fh3k_dequant_f32(type, g.st_w.p, (int64_t)in_bytes, cnt, 1, (float *)g.st_y.p, g.stream);
+    const void *dsrc = registered(src, in_bytes);
+    hipError_t e = dsrc ? hipSuccess : hipMemcpy(g.st_w.p, src, in_bytes, hipMemcpyHostToDevice);
+    if (!dsrc) dsrc = g.st_w.p;
+    if (e == hipSuccess) e = fh3k_dequant_f32(type, dsrc, (int64_t)in_bytes, cnt, 1, (float *)g.st_y.p, g.stream);
     if (e == hipSuccess) e = hipStreamSynchronize(g.stream);
     if (e == hipSuccess) e = hipMemcpy(dst, g.st_y.p, out_bytes, hipMemcpyDeviceToHost);
     if (e != hipSuccess) report("fh3_dequant", hip_fail(e, "fh3_dequant"));
@@ -796,17 +864,20 @@ extern "C" void fh3_matmul(const Fh3W *w, const float *x, float *y, int n_tok, c
     const size_t xb = (size_t)n_tok * (size_t)w->in * sizeof(float);
     const size_t yb = (size_t)n_tok * (size_t)w->out * sizeof(float);
     const size_t bb = (size_t)w->out * sizeof(float);
-    if ((rc = grow(g.st_w, wb)) || (rc = grow(g.st_x, xb)) || (rc = grow(g.st_y, yb)) ||
+    // a registered weight (fh3_hip_register_weights) is used in place
+    const void *dw = registered(w->data, wb);
+    if (dw && ((uintptr_t)dw & 15u)) dw = nullptr;
+    if ((!dw && (rc = grow(g.st_w, wb))) || (rc = grow(g.st_x, xb)) || (rc = grow(g.st_y, yb)) ||
         (bias_or_null && (rc = grow(g.st_b, bb)))) {
         report("fh3_matmul", rc);
         return;
     }
-    hipError_t e = hipMemcpy(g.st_w.p, w->data, wb, hipMemcpyHostToDevice);
+    hipError_t e = dw ? hipSuccess : hipMemcpy(g.st_w.p, w->data, wb, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(g.st_x.p, x, xb, hipMemcpyHostToDevice);
     if (e == hipSuccess && bias_or_null) e = hipMemcpy(g.st_b.p, bias_or_null, bb, hipMemcpyHostToDevice);
     if (e != hipSuccess) { report("fh3_matmul", hip_fail(e, "fh3_matmul upload")); return; }
     Fh3W wd = *w;
-    wd.data = (const uint8_t *)g.st_w.p;
+    wd.data = (const uint8_t *)(dw ? dw : g.st_w.p);
     rc = fh3_hip_matmul_dev(&wd, (const float *)g.st_x.p, (float *)g.st_y.p, n_tok,
                             bias_or_null ? (const float *)g.st_b.p : nullptr, nullptr);
     if (rc != FH3_OK) { report("fh3_matmul", rc); return; }

@@ -176,6 +176,9 @@ SIGNATURES = {
     "fh3_hip_vsa_attention_qkv_dev": (_c_int, [ctypes.POINTER(Fh3VsaCfg), _c_void_p, _c_void_p, _c_void_p,
                                                ctypes.c_float, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p,
                                                ctypes.POINTER(Fh3Seq), _c_int, _c_int, _c_void_p]),
+    "fh3_hip_register_weights": (_c_int, [_c_void_p, _c_size, ctypes.POINTER(_c_void_p)]),
+    "fh3_hip_unregister_weights": (_c_int, [_c_void_p]),
+    "fh3_hip_registered_ptr": (_c_void_p, [_c_void_p, _c_size]),
     "fh3_hip_graph_begin": (_c_int, [_c_void_p]),
     "fh3_hip_graph_end": (_c_int, [_c_void_p, ctypes.POINTER(_c_void_p)]),
     "fh3_hip_graph_launch": (_c_int, [_c_void_p, _c_void_p]),
@@ -460,6 +463,19 @@ def vsa_attention_host(q, k, v, gate, seq, sparsity=0.8, tile=64):
     lib().fh3_vsa_attention(ctypes.byref(cfg), _p(q), _p(k), _p(v), None if g is None else _p(g), _p(o),
                             ctypes.byref(seq), heads, hd)
     return o
+
+
+def register_weights(host_array):
+    """fh3_hip_register_weights on a numpy array (kept alive by the caller);
+    returns the device address."""
+    d = _c_void_p()
+    _check(lib().fh3_hip_register_weights(host_array.ctypes.data, host_array.nbytes, ctypes.byref(d)),
+           "fh3_hip_register_weights")
+    return d.value
+
+
+def unregister_weights(host_array):
+    _check(lib().fh3_hip_unregister_weights(host_array.ctypes.data), "fh3_hip_unregister_weights")
 
 
 class Graph:

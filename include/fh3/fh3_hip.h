@@ -159,6 +159,24 @@ int fh3_hip_vsa_attention_qkv_dev(const Fh3VsaCfg *c, const float *d_qkv, const 
                                   int rot_dim, const float *d_gate, float *d_o, const Fh3Seq *seq, int heads,
                                   int head_dim, void *stream);
 
+/* Weight registration (the boundary's "host data -> device pointer" hook).
+ * fh3_hip_register_weights uploads [host, host + bytes) once and keeps the
+ * copy on the device; the host-pointer wrappers fh3_matmul / fh3_dequant then
+ * find any weight lying inside a registered range and use the device copy in
+ * place, copying only x in and y out (a registered range is typically a
+ * packed layer or an mmapped GGUF tensor region).  *d_out (may be NULL) gets
+ * the device address of `host`, usable directly as Fh3W.data with the _dev
+ * entry points.  The host bytes must not change while registered:
+ * registering the same range again refreshes the device copy.  Ranges may
+ * not overlap.  fh3_hip_unregister_weights frees the copy (after the device
+ * is idle); fh3_hip_registered_ptr returns the device address of
+ * [host, host + bytes) or NULL.  Replaces the per-call weight upload of the
+ * wrappers; the reference keeps weights in host memory
+ * (src/io/fh3_trunk.c:413-431, src/io/fh3_pack.c:148-158). */
+int fh3_hip_register_weights(const void *host, size_t bytes, const void **d_out);
+int fh3_hip_unregister_weights(const void *host);
+const void *fh3_hip_registered_ptr(const void *host, size_t bytes);
+
 /* HIP graph capture of work enqueued on a stream (NULL = the compute
  * stream), for launch-bound loops such as small-M text-encoder layers:
  * begin, enqueue fh3_hip_* calls on that stream, end -> an executable graph

@@ -484,7 +484,7 @@ def main():
             g.call(i)
             g.kernel(i)
         F.synchronize()
-        reps = 5 if M >= 32768 else 10
+        reps = 20
         t_k = ev.time_ms(g.kernel, reps, st)
         t_c = ev.time_ms(g.call, reps, st)
         tf_k = g.flop / (t_k * 1e-3) / 1e12

@@ -216,6 +216,8 @@ extern "C" void fh3_hip_shutdown(void) {
     }
     for (auto &r : g.regs) (void)hipFree(r.dev);
     g.regs.clear();
+    for (int &k : g.vsa_key) k = -1;  // the VSA geometry was freed with vsa_geo
+    g.vsa_T = g.vsa_P = 0;
     (void)hipStreamDestroy(g.stream);
     g.stream = nullptr;
     g.init = false;

@@ -192,3 +192,18 @@ def test_vsa_argument_errors(gpu):
         F.vsa_attention_qkv_dev(b, None, b, sq, 1, 64, 0.8, 64, None, None, 1e-5, b, None, 64)
     with pytest.raises(F.Fh3Error):          # misaligned
         F.vsa_attention_dev(b.ptr + 4, b, b, None, b, sq, 1, 64)
+
+
+def test_vsa_after_shutdown_and_reinit(gpu):
+    """fh3_hip_shutdown frees the library's buffers, the kept tile geometry
+    included; the next call after re-initialisation rebuilds it."""
+    F = gpu
+    rng = np.random.default_rng(8)
+    n, heads, hd = 268, 2, 64
+    q, k, v, g = (rng.standard_normal((n, heads, hd)).astype(np.float32) for _ in range(4))
+    seq = (n, 35, 23, 210, 5, 6, 7)
+    a = _gpu_vsa(F, q, k, v, g, seq, 0.8)
+    F.lib().fh3_hip_shutdown()
+    F.init(0)
+    b = _gpu_vsa(F, q, k, v, g, seq, 0.8)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

@@ -110,21 +110,28 @@ __device__ __forceinline__ half2v q4k_magic_pair(uint32_t a, uint32_t sel) {
 // fma(D, 1024 + q, C) = D*q - Mn evaluated in fp32 and rounded once to fp16
 // (v_fma_mix).  C carries an fp32 rounding of at most 2^-24 * 1024 * D, far
 // below the fp16 rounding of the result.
+// fp16(D*p + C) for both halves of a pair p of fp16 values, with an fp32
+// fused multiply-add: v_fma_mixlo/mixhi_f16 take the f16 operand and the f32
+// operands as they are and write one half of the result each, so a pair costs
+// two instructions instead of two conversions in, two FMAs and one pack.
+__device__ __forceinline__ uint32_t fma_mix_pair(float D, uint32_t p, float C) {
+    uint32_t r;
+    asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[0,1,0]\n\t"
+        "v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+        : "=&v"(r)
+        : "v"(D), "v"(p), "v"(C));
+    return r;
+}
+
 __device__ __forceinline__ half8 q4k_deq8_f16(uint32_t u0, uint32_t u1, bool hi, float D, float C) {
     const uint32_t a = (hi ? (u0 >> 4) : u0) & 0x0F0F0F0Fu;
     const uint32_t b = (hi ? (u1 >> 4) : u1) & 0x0F0F0F0Fu;
-    const half2v p0 = q4k_magic_pair(a, 0x04010400u), p1 = q4k_magic_pair(a, 0x04030402u);
-    const half2v p2 = q4k_magic_pair(b, 0x04010400u), p3 = q4k_magic_pair(b, 0x04030402u);
-    half8 r;
-    r[0] = (_Float16)__builtin_fmaf(D, (float)p0[0], C);
-    r[1] = (_Float16)__builtin_fmaf(D, (float)p0[1], C);
-    r[2] = (_Float16)__builtin_fmaf(D, (float)p1[0], C);
-    r[3] = (_Float16)__builtin_fmaf(D, (float)p1[1], C);
-    r[4] = (_Float16)__builtin_fmaf(D, (float)p2[0], C);
-    r[5] = (_Float16)__builtin_fmaf(D, (float)p2[1], C);
-    r[6] = (_Float16)__builtin_fmaf(D, (float)p3[0], C);
-    r[7] = (_Float16)__builtin_fmaf(D, (float)p3[1], C);
-    return r;
+    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u);
+    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u);
+    const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u);
+    const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u);
+    const u32x4 r = {fma_mix_pair(D, p0, C), fma_mix_pair(D, p1, C), fma_mix_pair(D, p2, C), fma_mix_pair(D, p3, C)};
+    return __builtin_bit_cast(half8, r);
 }
 
 __device__ __forceinline__ u32x4 ld16(const uint8_t *p) {
@@ -935,11 +942,20 @@ struct GemmRaw {
 
 // CH (the chunk, s % 4) is a compile-time constant, so the header load of
 // chunk 0 is not a branch and a K step is one basic block.
+// k_gemm reads through buffer resources: wr covers the workgroup's weight
+// rows from its first one, woff is the byte offset of this thread's row and
+// woffq that offset plus the thread's 16-byte piece of a chunk; the super-block
+// offset goes in the scalar offset.  No per-lane address arithmetic per load.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
 template <int CH>
-__device__ __forceinline__ void gemm_load_raw(const uint8_t *wrow, int sb, int h, GemmRaw &r, const GemmRaw &prev) {
-    const uint8_t *blk = wrow + (size_t)sb * 144;
-    r.hv = CH == 0 ? ld16(blk) : prev.hv;
-    r.qv = ld16(blk + 16 + 32 * CH + 16 * h);
+__device__ __forceinline__ void gemm_load_raw(__amdgpu_buffer_rsrc_t wr, uint32_t woff, uint32_t woffq, int sb,
+                                              GemmRaw &r, const GemmRaw &prev) {
+    const int so = sb * 144;
+    r.hv = CH == 0 ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)woff, so, 0)) : prev.hv;
+    r.qv = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)woffq + 32 * CH, so, 0));
 }
 
 // B-fragment layout: fragment rb*4 + kk holds rows 32rb..32rb+31 x k 16kk..16kk+15
@@ -953,6 +969,19 @@ __device__ __forceinline__ void gemm_dequant(half8 (*ldsb)[64], const GemmRaw &r
     ldsb[wf + h][wl + 32] = q4k_deq8_f16(r.qv.z, r.qv.w, false, Dlo, Clo);
     ldsb[wf + 2 + h][wl] = q4k_deq8_f16(r.qv.x, r.qv.y, true, Dhi, Chi);
     ldsb[wf + 2 + h][wl + 32] = q4k_deq8_f16(r.qv.z, r.qv.w, true, Dhi, Chi);
+}
+
+// Activation fragments of K step s for k_gemm: xr covers the wavefront's two
+// token blocks, xoff is the lane's byte offset, tbs the byte stride of a token
+// block.
+__device__ __forceinline__ void gemm_load_xs(__amdgpu_buffer_rsrc_t xr, uint32_t xoff, int tbs, int s,
+                                             half8 (&xf)[2][4]) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int so = (s * 4 + k) * 1024;
+        xf[0][k] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)xoff, so, 0));
+        xf[1][k] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)xoff, so + tbs, 0));
+    }
 }
 
 __device__ __forceinline__ void gemm_load_x(const half8 *xa0, const half8 *xa1, int s, half8 (&xf)[2][4]) {
@@ -985,7 +1014,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
                                                  float *__restrict__ Y, int M, int m_tiles,
                                                  int n_tiles, int epi, const float *__restrict__ aux) {
     __shared__ half8 lds[2][16][64];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     const int total = m_tiles * n_tiles;
     const int id = blockIdx.x;
@@ -995,20 +1025,26 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
     const int m0 = mt * GEMM_BM, n0 = nt * GEMM_BN;
 
     // weight-loader role: rows n0..n0+127, or (SwiGLU) 64 val rows from
-    // nt*64 and the 64 gate rows F + nt*64..
+    // nt*64 and the 64 gate rows F + nt*64..  Offsets from the first row fit
+    // 32 bits (the launcher requires N * row_bytes < 2^32).
     const int r = tid & 127, h = tid >> 7;
     const int F = N >> 1;
+    const int rowbase = epi == EPI_SWIGLU ? nt * 64 : n0;
     int orow = n0 + r;
     if (epi == EPI_SWIGLU) orow = r < 64 ? nt * 64 + r : F + nt * 64 + r - 64;
     orow = orow < N ? orow : N - 1;
-    const uint8_t *wrow = W + (size_t)orow * row_bytes;
+    const __amdgpu_buffer_rsrc_t wr =
+        buf_rsrc(W + (size_t)rowbase * row_bytes, (uint32_t)((size_t)(N - rowbase) * row_bytes));
+    const uint32_t woff = (uint32_t)(orow - rowbase) * (uint32_t)row_bytes;
+    const uint32_t woffq = woff + 16u + 16u * (uint32_t)h;
     const int wf = (r >> 5) * 4;   // first LDS fragment of this row's 32-row block
     const int wl = r & 31;
 
     // activation fragments of this wavefront: token blocks T0, T0+1
     const int kf_n = K / 16;
-    const half8 *xa0 = X16 + ((size_t)(m0 / 32 + 2 * wave) * kf_n) * 64 + lane;
-    const half8 *xa1 = xa0 + (size_t)kf_n * 64;
+    const int tbs = kf_n * 1024;
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X16 + ((size_t)(m0 / 32 + 2 * wave) * kf_n) * 64, 2u * (uint32_t)tbs);
+    const uint32_t xoff = (uint32_t)lane * 16u;
 
     const int S = K / 64;  // a multiple of 4 (K % 256 == 0)
     f32x16 acc[2][4];
@@ -1019,9 +1055,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
 
     GemmRaw re, ro;            // raw weights of even / odd steps
     half8 xe[2][4], xo[2][4];  // activations of even / odd steps
-    gemm_load_raw<0>(wrow, 0, h, re, re);
-    gemm_load_x(xa0, xa1, 0, xe);
-    gemm_load_raw<1>(wrow, 0, h, ro, re);
+    gemm_load_raw<0>(wr, woff, woffq, 0, re, re);
+    gemm_load_xs(xr, xoff, tbs, 0, xe);
+    gemm_load_raw<1>(wr, woff, woffq, 0, ro, re);
     gemm_dequant(lds[0], re, 0, wf, wl, h);
     __syncthreads();
     // one super-block (4 K steps) per iteration; the loads and the dequant of
@@ -1032,26 +1068,26 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
         const int s = 4 * sb;
         const int nb = sb + 1 < S / 4 ? sb + 1 : sb;
         // step s (chunk 0): MFMA from lds[0]; dequant chunk 1 into lds[1]
-        gemm_load_x(xa0, xa1, s + 1, xo);
-        gemm_load_raw<2>(wrow, sb, h, re, ro);
+        gemm_load_xs(xr, xoff, tbs, s + 1, xo);
+        gemm_load_raw<2>(wr, woff, woffq, sb, re, ro);
         gemm_dequant(lds[1], ro, 1, wf, wl, h);
         gemm_mfma(lds[0], lane, xe, acc);
         __syncthreads();
         // step s+1 (chunk 1): MFMA from lds[1]; dequant chunk 2 into lds[0]
-        gemm_load_x(xa0, xa1, s + 2, xe);
-        gemm_load_raw<3>(wrow, sb, h, ro, re);
+        gemm_load_xs(xr, xoff, tbs, s + 2, xe);
+        gemm_load_raw<3>(wr, woff, woffq, sb, ro, re);
         gemm_dequant(lds[0], re, 2, wf, wl, h);
         gemm_mfma(lds[1], lane, xo, acc);
         __syncthreads();
         // step s+2 (chunk 2): MFMA from lds[0]; dequant chunk 3 into lds[1]
-        gemm_load_x(xa0, xa1, s + 3, xo);
-        gemm_load_raw<0>(wrow, nb, h, re, ro);
+        gemm_load_xs(xr, xoff, tbs, s + 3, xo);
+        gemm_load_raw<0>(wr, woff, woffq, nb, re, ro);
         gemm_dequant(lds[1], ro, 3, wf, wl, h);
         gemm_mfma(lds[0], lane, xe, acc);
         __syncthreads();
         // step s+3 (chunk 3): MFMA from lds[1]; dequant the next chunk 0 into lds[0]
-        gemm_load_x(xa0, xa1, 4 * nb, xe);
-        gemm_load_raw<1>(wrow, nb, h, ro, re);
+        gemm_load_xs(xr, xoff, tbs, 4 * nb, xe);
+        gemm_load_raw<1>(wr, woff, woffq, nb, ro, re);
         gemm_dequant(lds[0], re, 0, wf, wl, h);
         gemm_mfma(lds[1], lane, xo, acc);
         __syncthreads();
@@ -1551,6 +1587,7 @@ extern "C" hipError_t fh3k_gemm_epi(const void *W, int64_t row_bytes, int N, int
                                     const float *xs_inv, const float *bias, float *y, int M, int epi,
                                     const float *aux, hipStream_t st) {
     if (epi == EPI_SWIGLU && (N % 128)) return hipErrorInvalidValue;
+    if ((uint64_t)N * (uint64_t)row_bytes >= (1ull << 32)) return hipErrorInvalidValue;  // 32-bit row offsets
     const int m_tiles = (M + GEMM_BM - 1) / GEMM_BM;
     const int n_tiles = epi == EPI_SWIGLU ? (N / 2) / 64 : (N + GEMM_BN - 1) / GEMM_BN;
     hipLaunchKernelGGL(k_gemm, dim3((unsigned)(m_tiles * n_tiles)), dim3(256), 0, st,

@@ -1007,6 +1007,26 @@ __device__ __forceinline__ void gemm_mfma(half8 (*ldsb)[64], int lane, const hal
     }
 }
 
+// Instruction order of one K step, given to the scheduler: the 32 MFMAs each
+// followed by three VALU (the next step's dequant), the B-fragment reads of
+// k-slice k+1 spread over the MFMAs of slice k, the next step's loads one per
+// three MFMAs and the LDS writes late.  Without it the compiler clusters the
+// loads and the dequant into runs that stall the matrix pipe.
+template <int I>
+__device__ __forceinline__ void gemm_pipe_slot() {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+    if constexpr (I % 2 == 1 && I < 24) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    if constexpr (I % 3 == 0 && I < 30) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+    if constexpr (I >= 24 && I < 28) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);     // DS write
+    if constexpr (I + 1 < 32) gemm_pipe_slot<I + 1>();
+}
+
+__device__ __forceinline__ void gemm_pipe() {
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // B fragments of the first k-slice
+    gemm_pipe_slot<0>();
+}
+
 __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, int64_t row_bytes,
                                                  int N, int K, const half8 *__restrict__ X16,
                                                  const float *__restrict__ xs_inv,
@@ -1072,24 +1092,28 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
         gemm_load_raw<2>(wr, woff, woffq, sb, re, ro);
         gemm_dequant(lds[1], ro, 1, wf, wl, h);
         gemm_mfma(lds[0], lane, xe, acc);
+        gemm_pipe();
         __syncthreads();
         // step s+1 (chunk 1): MFMA from lds[1]; dequant chunk 2 into lds[0]
         gemm_load_xs(xr, xoff, tbs, s + 2, xe);
         gemm_load_raw<3>(wr, woff, woffq, sb, ro, re);
         gemm_dequant(lds[0], re, 2, wf, wl, h);
         gemm_mfma(lds[1], lane, xo, acc);
+        gemm_pipe();
         __syncthreads();
         // step s+2 (chunk 2): MFMA from lds[0]; dequant chunk 3 into lds[1]
         gemm_load_xs(xr, xoff, tbs, s + 3, xo);
         gemm_load_raw<0>(wr, woff, woffq, nb, re, ro);
         gemm_dequant(lds[1], ro, 3, wf, wl, h);
         gemm_mfma(lds[0], lane, xe, acc);
+        gemm_pipe();
         __syncthreads();
         // step s+3 (chunk 3): MFMA from lds[1]; dequant the next chunk 0 into lds[0]
         gemm_load_xs(xr, xoff, tbs, 4 * nb, xe);
         gemm_load_raw<1>(wr, woff, woffq, nb, ro, re);
         gemm_dequant(lds[0], re, 0, wf, wl, h);
         gemm_mfma(lds[1], lane, xo, acc);
+        gemm_pipe();
         __syncthreads();
     }
 

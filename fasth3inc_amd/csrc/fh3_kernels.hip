@@ -1008,17 +1008,18 @@ __device__ __forceinline__ void gemm_mfma(half8 (*ldsb)[64], int lane, const hal
 }
 
 // Instruction order of one K step, given to the scheduler: the 32 MFMAs each
-// followed by three VALU (the next step's dequant), the B-fragment reads of
-// k-slice k+1 spread over the MFMAs of slice k, the next step's loads one per
-// three MFMAs and the LDS writes late.  Without it the compiler clusters the
+// followed by up to four VALU (the next step's dequant), the B-fragment reads
+// of k-slice k+1 spread over the MFMAs of slice k, the next step's loads one
+// per three MFMAs and the LDS writes after MFMA 20 (the best of a sweep of
+// these counts on the DiT shapes).  Without it the compiler clusters the
 // loads and the dequant into runs that stall the matrix pipe.
 template <int I>
 __device__ __forceinline__ void gemm_pipe_slot() {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
     if constexpr (I % 2 == 1 && I < 24) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
     if constexpr (I % 3 == 0 && I < 30) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
-    if constexpr (I >= 24 && I < 28) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);     // DS write
+    if constexpr (I >= 20 && I < 24) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);     // DS write
     if constexpr (I + 1 < 32) gemm_pipe_slot<I + 1>();
 }
 

@@ -65,6 +65,15 @@ hipError_t fh3k_gemv8_epi(const void *W, int64_t row_bytes, int N, int K, const 
 hipError_t fh3k_gemm_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16, const float *xs_inv,
                          const float *bias, float *y, int M, int epi, const float *aux, hipStream_t st);
 
+// Middle M (1 <= M <= fh3k_midm_max_tokens()): K split into S windows, partial
+// sums in part (fh3k_midm_part_bytes(N, K, M) bytes), then an ordered sum with
+// the epilogue.  Same prepared fragments as fh3k_skinny (round_up(M, 32) rows).
+hipError_t fh3k_midm_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16, const float *xs_inv,
+                         const float *bias, float *y, int M, int epi, const float *aux, float *part,
+                         hipStream_t st);
+size_t fh3k_midm_part_bytes(int N, int K, int M);
+int fh3k_midm_max_tokens(void);
+
 // fh3k_xprep with the rows first normalised: rmsnorm with weight norm_w and
 // eps, then (shift and scale both set, [M][K]) AdaLN modulate.
 hipError_t fh3k_xprep_norm(const float *x, int M, int K, int Mpad, void *x16, float *xs_inv, const float *norm_w,

@@ -1629,6 +1629,202 @@ extern "C" hipError_t fh3k_gemm(const void *W, int64_t row_bytes, int N, int K, 
 extern "C" int fh3k_gemm_row_pad(void) { return GEMM_BM; }
 
 // ---------------------------------------------------------------------------
+// Middle M (17..64 tokens): split K, then an ordered sum.
+//
+// With few tokens and few weight rows (M = 64, N = 4096 is 256 tiles of
+// 32 x 32) the work only fills the chip when K is split as well, and a
+// 16-row wavefront that reads every token's activations for the whole of K
+// (k_skinny) moves M*K*2 bytes through L2 per 16 rows.  k_midm gives a
+// workgroup 128 weight rows (4 wavefronts x 32) and a window of C super-blocks:
+//   - the window's activation fragments (TB2 token blocks of 32) are staged
+//     once per super-block into LDS and read by all four wavefronts;
+//   - each wavefront dequantises its own 32 rows straight into B operands
+//     (v_fma_mix, as k_gemm rounds Q4_K), so the weights need no LDS;
+//   - v_mfma_f32_32x32x16_f16, one 32x32 accumulator per token block.
+// Partial sums go to part[ks][t][o]; k_midm_sum adds the S windows in
+// window order (deterministic), scales, adds the bias and applies the
+// epilogue.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int MIDM_ROWS = 128;
+
+template <int TB2>
+__global__ __launch_bounds__(256, 2) void k_midm(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int K,
+                                                 const half8 *__restrict__ X16, int M, int C, int n_rg,
+                                                 float *__restrict__ part) {
+    __shared__ half8 sx[2][TB2][16][64];  // staged fragments of one super-block, double-buffered
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5;
+
+    // consecutive ids go to different XCDs: give each XCD a contiguous run of
+    // (window, row group) pairs so that one window's activations stay in one L2
+    const int total = gridDim.x, id = blockIdx.x, per = total >> 3;
+    const int L = (id < per * 8) ? (id & 7) * per + (id >> 3) : id;
+    const int ks = L / n_rg, rg = L - ks * n_rg;
+    const int nsb = K / 256, kf_n = K / 16;
+    const int sb0 = ks * C;
+    const int nw = nsb - sb0 < C ? nsb - sb0 : C;  // >= 1 by the launch
+
+    int orow = rg * MIDM_ROWS + 32 * wave + (lane & 31);
+    const bool orow_ok = orow < N;
+    orow = orow_ok ? orow : N - 1;
+    const uint8_t *wrow = W + (size_t)orow * row_bytes;
+
+    // raw bytes of one super-block for this lane: the header and, per chunk c,
+    // bytes 8h..8h+7 and 16+8h..16+8h+7 (k steps 4c..4c+3 take them)
+    struct Raw {
+        u32x4 hv;
+        uint32_t q[4][2][2];
+    };
+    auto load_raw = [&](int sb, Raw &r) {
+        const uint8_t *b = wrow + (size_t)sb * 144;
+        r.hv = ld16(b);
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                const uint2 u = *reinterpret_cast<const uint2 *>(b + 16 + 32 * c + 16 * hf + 8 * h);
+                r.q[c][hf][0] = u.x;
+                r.q[c][hf][1] = u.y;
+            }
+    };
+    // staging: thread tid moves fragment pieces f = tid + 256 i of the
+    // TB2 x 16 x 64 half8 of one super-block
+    constexpr int SPT = TB2 * 16 * 64 / 256;
+    half8 stg[SPT];
+    auto stage_load = [&](int sb) {
+#pragma unroll
+        for (int i = 0; i < SPT; i++) {
+            const int f = tid + 256 * i;
+            const int tb = f / 1024, fr = (f / 64) % 16, l = f % 64;
+            stg[i] = X16[((size_t)tb * kf_n + (size_t)sb * 16 + fr) * 64 + l];
+        }
+    };
+    auto stage_store = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < SPT; i++) {
+            const int f = tid + 256 * i;
+            (&sx[b][0][0][0])[f] = stg[i];
+        }
+    };
+
+    f32x16 acc[TB2];
+#pragma unroll
+    for (int t = 0; t < TB2; t++) acc[t] = f32x16{};
+
+    Raw ra, rb;
+    load_raw(sb0, ra);
+    stage_load(sb0);
+    stage_store(0);
+    __syncthreads();
+    for (int i = 0; i < nw; i++) {
+        const int b = i & 1;
+        const bool more = i + 1 < nw;
+        if (more) {
+            load_raw(sb0 + i + 1, rb);
+            stage_load(sb0 + i + 1);
+        }
+        float Dg[8], Cg[8];
+#pragma unroll
+        for (int g = 0; g < 8; g++) q4k_group_fast(ra.hv, g, Dg[g], Cg[g]);
+#pragma unroll
+        for (int st = 0; st < 16; st++) {
+            const int c = st >> 2, nib = (st >> 1) & 1, hf = st & 1, g = 2 * c + nib;
+            const half8 bq = q4k_deq8_f16(ra.q[c][hf][0], ra.q[c][hf][1], nib != 0, Dg[g], Cg[g]);
+#pragma unroll
+            for (int t = 0; t < TB2; t++)
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sx[b][t][st][lane], bq, acc[t], 0, 0, 0);
+        }
+        if (more) stage_store(b ^ 1);
+        ra = rb;
+        __syncthreads();
+    }
+
+    // D: lane holds weight row orow, tokens 32 t + 8 (v/4) + 4 h + v%4
+    if (orow_ok) {
+        float *pp = part + (size_t)ks * M * N + orow;
+#pragma unroll
+        for (int t = 0; t < TB2; t++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int tok = 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
+                if (tok < M) pp[(size_t)tok * N] = acc[t][v];
+            }
+    }
+}
+
+// y[t][o] = (sum over windows in order) * xs_inv[t] + bias[o], then the
+// epilogue; one thread per output (SwiGLU: per val/gate pair).
+__global__ __launch_bounds__(256) void k_midm_sum(const float *__restrict__ part, int S, int M, int N,
+                                                  const float *__restrict__ xs_inv, const float *__restrict__ bias,
+                                                  float *__restrict__ Y, int epi, const float *__restrict__ aux) {
+    const int F = N >> 1;
+    const int width = epi == EPI_SWIGLU ? F : N;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)M * width) return;
+    const int t = (int)(i / width), o = (int)(i - (int64_t)t * width);
+    const size_t mn = (size_t)M * N;
+    const float *p = part + (size_t)t * N + o;
+    float s = p[0];
+    for (int k = 1; k < S; k++) s += p[k * mn];
+    if (epi == EPI_SWIGLU) {
+        float sg = p[F];
+        for (int k = 1; k < S; k++) sg += p[k * mn + F];
+        const float bv = bias ? bias[o] : 0.f, bg = bias ? bias[F + o] : 0.f;
+        Y[(size_t)t * F + o] = (s * xs_inv[t] + bv) * silu_f32(sg * xs_inv[t] + bg);
+        return;
+    }
+    epi_store(Y, aux, epi, (size_t)t * N + o, s * xs_inv[t] + (bias ? bias[o] : 0.f));
+}
+
+}  // namespace
+
+// Window length C and split count S for k_midm: about two workgroups per CU
+// (512) and at least two super-blocks per window where K allows it.
+static void midm_split(int N, int K, int &C, int &S) {
+    const int nsb = K / 256, n_rg = (N + MIDM_ROWS - 1) / MIDM_ROWS;
+    int s = (512 + n_rg - 1) / n_rg;
+    const int smax = nsb >= 2 ? nsb / 2 : 1;
+    s = s < 1 ? 1 : (s > smax ? smax : s);
+    C = (nsb + s - 1) / s;
+    S = (nsb + C - 1) / C;
+}
+
+extern "C" int fh3k_midm_max_tokens(void) { return 64; }
+
+extern "C" size_t fh3k_midm_part_bytes(int N, int K, int M) {
+    int C, S;
+    if (N <= 0 || K < 256 || M <= 0) return 0;
+    midm_split(N, K, C, S);
+    return (size_t)S * (size_t)M * (size_t)N * sizeof(float);
+}
+
+extern "C" hipError_t fh3k_midm_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16,
+                                    const float *xs_inv, const float *bias, float *y, int M, int epi,
+                                    const float *aux, float *part, hipStream_t st) {
+    if (M < 1 || M > 64 || K % 256 || (epi == EPI_SWIGLU && (N % 2))) return hipErrorInvalidValue;
+    int C, S;
+    midm_split(N, K, C, S);
+    const int n_rg = (N + MIDM_ROWS - 1) / MIDM_ROWS;
+    const dim3 grid((unsigned)(n_rg * S)), block(256);
+    if (M <= 32)
+        hipLaunchKernelGGL(k_midm<1>, grid, block, 0, st, (const uint8_t *)W, row_bytes, N, K, (const half8 *)x16, M,
+                           C, n_rg, part);
+    else
+        hipLaunchKernelGGL(k_midm<2>, grid, block, 0, st, (const uint8_t *)W, row_bytes, N, K, (const half8 *)x16, M,
+                           C, n_rg, part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int width = epi == EPI_SWIGLU ? N / 2 : N;
+    const int64_t outs = (int64_t)M * width;
+    hipLaunchKernelGGL(k_midm_sum, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, st, part, S, M, N, xs_inv,
+                       bias, y, epi, aux);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // Other weight types: decode to fp16 rows, then k_skinny16 / k_gemm16
 // ---------------------------------------------------------------------------
 template <int T>

@@ -193,8 +193,12 @@ int fh3_hip_graph_destroy(void *graph_exec);
  *     planes, one power-of-two scale per token and wavefront window) inside
  *     the kernel, integer MFMA on the raw 4-bit weights, no preparation launch
  *     and no workspace;
+ *   - FH3_HIP_PATH_MIDM for 17 <= n_tok <= 64 and in >= 8192: K split into
+ *     windows over 128-row workgroups that share staged activations, partial
+ *     sums in a library workspace, then an ordered sum (any n_tok <= 64 when
+ *     forced);
  *   - FH3_HIP_PATH_SKINNY (fp16 activations, exact fp16 sc*q weights) for
- *     n_tok <= fh3_hip_skinny_max();
+ *     the other n_tok <= fh3_hip_skinny_max();
  *   - FH3_HIP_PATH_GEMM above.
  * Setting a path forces it where it can take the shape (tests); prepare and
  * product of the two-stage API must run under the same setting. */
@@ -202,6 +206,7 @@ int fh3_hip_graph_destroy(void *graph_exec);
 #define FH3_HIP_PATH_SKINNY 1
 #define FH3_HIP_PATH_GEMM   2
 #define FH3_HIP_PATH_GEMV8  3
+#define FH3_HIP_PATH_MIDM   4
 int fh3_hip_set_path(int path);
 int fh3_hip_skinny_max(void);
 /* The kernel family fh3_hip_matmul_dev would use for n_tok tokens of in

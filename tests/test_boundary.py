@@ -87,7 +87,12 @@ def test_matmul_path_selection(fh3):
     assert F.matmul_path(2, 8960) == G8 and F.matmul_path(2, 9216) == SK
     assert F.matmul_path(3, 5120) == SK and F.matmul_path(64, 5120) == SK
     assert F.matmul_path(65, 5120) == GM
+    MD = F.PATH_MIDM
+    assert F.matmul_path(17, 8192) == MD and F.matmul_path(64, 13824) == MD
+    assert F.matmul_path(16, 13824) == SK and F.matmul_path(17, 7936) == SK and F.matmul_path(65, 13824) == GM
     try:
+        F.set_path(MD)
+        assert F.matmul_path(1, 5120) == MD and F.matmul_path(64, 256) == MD and F.matmul_path(65, 5120) == GM
         F.set_path(SK)
         assert F.matmul_path(1, 5120) == SK
         F.set_path(G8)

@@ -44,7 +44,7 @@ METRIC = "Q4_K GEMM TFLOP/s + GEMV weight GB/s (% roofline); DiT block linear ms
 # profiles/k_skinny_gemv_m1-16_k5120.md, profiles/k_gemm_dit_attention_m8192_k5120.md,
 # profiles/hbm_counters_copy_256MiB.md.  Re-measure when the kernels change.
 TRAFFIC_GEMV_MEAN = 33615898        # mean over the six GEMV shapes (algorithmic mean 32899072)
-TRAFFIC_GEMM = {"attn_qkv": 2346014125, "attn_out": 776729119}
+TRAFFIC_GEMM = {"attn_qkv": 2382307601, "attn_out": 785992328}
 
 
 def q4k_bytes(N, K):

@@ -63,7 +63,10 @@ int fh3_hip_dequant_dev(int type, const void *d_src, float *d_dst, int64_t rows,
  * with fp32 accumulation.  Deterministic: no atomics, fixed reduction order.
  * Non-finite activations give NaN outputs for that token on the GEMV8 path.
  * Except on the GEMV8 path, uses a library-owned workspace of about
- * n_tok * in * 2 bytes; calls that overlap on different streams race on it. */
+ * n_tok * in * 2 bytes (plus S * n_tok * out * 4 bytes of partial sums on the
+ * FH3_HIP_PATH_MIDM path, S <= in / 512); calls that overlap on different
+ * streams race on it.  Q4_K products of more than 64 tokens need
+ * out * row_bytes < 2^32 (32-bit row offsets; 7.6e9 weights). */
 int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok,
                        const float *d_bias_or_null, void *stream);
 
@@ -75,8 +78,9 @@ int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok,
  *     per row);
  *   fh3_hip_prepare_x_dev: fill d_prep (16-byte aligned) from d_x[n_tok][in];
  *   fh3_hip_matmul_prepared_dev: the product from a prepared buffer; same
- *     results as fh3_hip_matmul_dev, no library workspace.  (For the
- *     FH3_HIP_PATH_GEMV8 shapes the prepared form is a copy of x.) */
+ *     results as fh3_hip_matmul_dev, no library workspace except the partial
+ *     sums of the FH3_HIP_PATH_MIDM path.  (For the FH3_HIP_PATH_GEMV8 shapes
+ *     the prepared form is a copy of x.) */
 size_t fh3_hip_prepared_bytes(int n_tok, int64_t in);
 int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, void *d_prep, void *stream);
 int fh3_hip_matmul_prepared_dev(const Fh3W *w, const void *d_prep, float *d_y, int n_tok,

@@ -446,7 +446,16 @@ static int product(const Fh3W *w, const void *prep, int n_tok, const float *bias
         FH3_HIPCALL(fh3k_midm_epi(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, epi, aux,
                                   (float *)g.part.p, st));
     } else {
-        FH3_HIPCALL(fh3k_gemm_epi(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, epi, aux, st));
+        // few tokens: the kernel splits K and needs the partial-sum workspace
+        const size_t pb = fh3k_gemm_part_bytes(N, K, n_tok, epi);
+        std::unique_lock<std::recursive_mutex> lk(g.mu, std::defer_lock);
+        if (pb) {
+            lk.lock();
+            int rc = grow(g.part, pb);
+            if (rc != FH3_OK) return rc;
+        }
+        FH3_HIPCALL(fh3k_gemm_epi(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, epi, aux,
+                                  (float *)g.part.p, st));
     }
     return FH3_OK;
 }

@@ -62,8 +62,14 @@ hipError_t fh3k_skinny_epi(const void *W, int64_t row_bytes, int N, int K, const
                            const float *bias, float *y, int M, int epi, const float *aux, hipStream_t st);
 hipError_t fh3k_gemv8_epi(const void *W, int64_t row_bytes, int N, int K, const float *x, const float *bias,
                           float *y, int M, int epi, const float *aux, hipStream_t st);
+// Large M.  When the 256 x 128 tiles alone would not fill the chip, K is split
+// into windows whose raw sums go to part (fh3k_gemm_part_bytes bytes; 0 = no
+// split) and are added in window order with the epilogue; x16 must hold
+// round_up(M, fh3k_gemm_row_pad()) rows.
 hipError_t fh3k_gemm_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16, const float *xs_inv,
-                         const float *bias, float *y, int M, int epi, const float *aux, hipStream_t st);
+                         const float *bias, float *y, int M, int epi, const float *aux, float *part,
+                         hipStream_t st);
+size_t fh3k_gemm_part_bytes(int N, int K, int M, int epi);
 
 // Middle M (1 <= M <= fh3k_midm_max_tokens()): K split into S windows, partial
 // sums in part (fh3k_midm_part_bytes(N, K, M) bytes), then an ordered sum with
@@ -112,10 +118,6 @@ hipError_t fh3k_vsa_attention(const float *q, const float *k, const float *v, in
 // Largest in-dimension (K) the activation preparation handles.
 int fh3k_max_in(void);
 
-// y = x * W^T (+bias) from prepared fragments; x16 must hold
-// round_up(M, fh3k_gemm_row_pad()) rows.
-hipError_t fh3k_gemm(const void *W, int64_t row_bytes, int N, int K, const void *x16,
-                     const float *xs_inv, const float *bias, float *y, int M, hipStream_t st);
 int fh3k_gemm_row_pad(void);
 
 #ifdef __cplusplus

@@ -1033,16 +1033,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
                                                  const float *__restrict__ xs_inv,
                                                  const float *__restrict__ bias,
                                                  float *__restrict__ Y, int M, int m_tiles,
-                                                 int n_tiles, int epi, const float *__restrict__ aux) {
+                                                 int n_tiles, int epi, const float *__restrict__ aux, int C,
+                                                 float *__restrict__ part) {
     __shared__ half8 lds[2][16][64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-    const int total = m_tiles * n_tiles;
+    // grid = tiles x S windows of C super-blocks (S = 1: the whole of K)
+    const int tiles = m_tiles * n_tiles;
+    const int total = gridDim.x;
     const int id = blockIdx.x;
     const int per = total >> 3;
     const int L = (id < per * 8) ? (id & 7) * per + (id >> 3) : id;
-    const int mt = L / n_tiles, nt = L - mt * n_tiles;
+    const int ks = L / tiles, tl = L - ks * tiles;
+    const int mt = tl / n_tiles, nt = tl - mt * n_tiles;
     const int m0 = mt * GEMM_BM, n0 = nt * GEMM_BN;
 
     // weight-loader role: rows n0..n0+127, or (SwiGLU) 64 val rows from
@@ -1067,7 +1071,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
     const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X16 + ((size_t)(m0 / 32 + 2 * wave) * kf_n) * 64, 2u * (uint32_t)tbs);
     const uint32_t xoff = (uint32_t)lane * 16u;
 
-    const int S = K / 64;  // a multiple of 4 (K % 256 == 0)
+    // super-blocks [sb0, sb1) of K: all of them, or this workgroup's window
+    const int nsb = K / 256;
+    const int sb0 = ks * C;
+    const int sb1 = sb0 + C < nsb ? sb0 + C : nsb;
     f32x16 acc[2][4];
 #pragma unroll
     for (int a = 0; a < 2; a++)
@@ -1076,18 +1083,18 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
 
     GemmRaw re, ro;            // raw weights of even / odd steps
     half8 xe[2][4], xo[2][4];  // activations of even / odd steps
-    gemm_load_raw<0>(wr, woff, woffq, 0, re, re);
-    gemm_load_xs(xr, xoff, tbs, 0, xe);
-    gemm_load_raw<1>(wr, woff, woffq, 0, ro, re);
+    gemm_load_raw<0>(wr, woff, woffq, sb0, re, re);
+    gemm_load_xs(xr, xoff, tbs, 4 * sb0, xe);
+    gemm_load_raw<1>(wr, woff, woffq, sb0, ro, re);
     gemm_dequant(lds[0], re, 0, wf, wl, h);
     __syncthreads();
     // one super-block (4 K steps) per iteration; the loads and the dequant of
     // the step after the last are clamped onto the last super-block (valid
     // addresses, results unused), so no step has a branch and the scheduler
     // can interleave each step's loads and dequant with its MFMAs
-    for (int sb = 0; sb < S / 4; sb++) {
+    for (int sb = sb0; sb < sb1; sb++) {
         const int s = 4 * sb;
-        const int nb = sb + 1 < S / 4 ? sb + 1 : sb;
+        const int nb = sb + 1 < sb1 ? sb + 1 : sb;
         // step s (chunk 0): MFMA from lds[0]; dequant chunk 1 into lds[1]
         gemm_load_xs(xr, xoff, tbs, s + 1, xo);
         gemm_load_raw<2>(wr, woff, woffq, sb, re, ro);
@@ -1120,6 +1127,26 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
 
     // epilogue: 32x32 output D, lane l holds column l%32 (weight row) and rows
     // 8*(v/4) + 4*(l/32) + v%4 (tokens)
+    if (part) {
+        // split K: this window's raw sums, part[ks][t][row] over all N rows
+#pragma unroll
+        for (int tb = 0; tb < 2; tb++) {
+            const int tbase = m0 + 64 * wave + 32 * tb + 4 * (lane >> 5);
+#pragma unroll
+            for (int ob = 0; ob < 4; ob++) {
+                int o = n0 + 32 * ob + (lane & 31);
+                if (epi == EPI_SWIGLU) o = ob < 2 ? nt * 64 + 32 * ob + (lane & 31) : F + nt * 64 + 32 * (ob - 2) + (lane & 31);
+                if (o >= N) continue;
+                float *pp = part + (size_t)ks * M * N + o;
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const int t = tbase + 8 * (v >> 2) + (v & 3);
+                    if (t < M) pp[(size_t)t * N] = acc[tb][ob][v];
+                }
+            }
+        }
+        return;
+    }
     if (epi == EPI_SWIGLU) {
         // tiles ob = 0, 1 hold val rows nt*64 + 32*ob + l%32, tiles 2, 3 the
         // matching gate rows
@@ -1608,23 +1635,6 @@ extern "C" hipError_t fh3k_gemv8(const void *W, int64_t row_bytes, int N, int K,
     return fh3k_gemv8_epi(W, row_bytes, N, K, x, bias, y, M, EPI_NONE, nullptr, st);
 }
 
-extern "C" hipError_t fh3k_gemm_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16,
-                                    const float *xs_inv, const float *bias, float *y, int M, int epi,
-                                    const float *aux, hipStream_t st) {
-    if (epi == EPI_SWIGLU && (N % 128)) return hipErrorInvalidValue;
-    if ((uint64_t)N * (uint64_t)row_bytes >= (1ull << 32)) return hipErrorInvalidValue;  // 32-bit row offsets
-    const int m_tiles = (M + GEMM_BM - 1) / GEMM_BM;
-    const int n_tiles = epi == EPI_SWIGLU ? (N / 2) / 64 : (N + GEMM_BN - 1) / GEMM_BN;
-    hipLaunchKernelGGL(k_gemm, dim3((unsigned)(m_tiles * n_tiles)), dim3(256), 0, st,
-                       (const uint8_t *)W, row_bytes, N, K, (const half8 *)x16, xs_inv, bias, y, M,
-                       m_tiles, n_tiles, epi, aux);
-    return hipGetLastError();
-}
-
-extern "C" hipError_t fh3k_gemm(const void *W, int64_t row_bytes, int N, int K, const void *x16,
-                                const float *xs_inv, const float *bias, float *y, int M, hipStream_t st) {
-    return fh3k_gemm_epi(W, row_bytes, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st);
-}
 
 extern "C" int fh3k_gemm_row_pad(void) { return GEMM_BM; }
 
@@ -1817,6 +1827,59 @@ extern "C" hipError_t fh3k_midm_epi(const void *W, int64_t row_bytes, int N, int
                            C, n_rg, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    const int width = epi == EPI_SWIGLU ? N / 2 : N;
+    const int64_t outs = (int64_t)M * width;
+    hipLaunchKernelGGL(k_midm_sum, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, st, part, S, M, N, xs_inv,
+                       bias, y, epi, aux);
+    return hipGetLastError();
+}
+
+// Split K for k_gemm when its tiles alone would not fill the chip (a few
+// hundred tokens or fewer): S windows of C super-blocks (at least two each).
+// S minimises a simple time model in units of one super-block step of a
+// workgroup (~5 us): rounds of 512 resident workgroups x (C + 1), plus the
+// partial sums (written and read: S*M*N*8 bytes at ~5 TB/s) and the extra
+// launch.
+static void gemm_split(int M, int N, int K, int epi, int &C, int &S) {
+    const int nsb = K / 256;
+    const int m_tiles = (M + GEMM_BM - 1) / GEMM_BM;
+    const int n_tiles = epi == EPI_SWIGLU ? (N / 2) / 64 : (N + GEMM_BN - 1) / GEMM_BN;
+    const int64_t tiles = (int64_t)m_tiles * n_tiles;
+    const int smax = nsb >= 4 ? nsb / 2 : 1;
+    auto rounds = [](int64_t wgs) { return (double)((wgs + 511) / 512); };
+    double best = rounds(tiles) * (nsb + 1);
+    C = nsb;
+    S = 1;
+    for (int s = 2; s <= smax && tiles * s <= 4096; s++) {
+        const int c = (nsb + s - 1) / s;
+        if ((nsb + c - 1) / c != s) continue;  // same windows as a smaller s
+        const double cost = rounds(tiles * s) * (c + 1) + (double)s * M * N * 8.0 / 2.5e7 + 0.4;
+        if (cost < best) best = cost, C = c, S = s;
+    }
+}
+
+extern "C" size_t fh3k_gemm_part_bytes(int N, int K, int M, int epi) {
+    int C, S;
+    if (N <= 0 || K < 256 || M <= 0) return 0;
+    gemm_split(M, N, K, epi, C, S);
+    return S > 1 ? (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+extern "C" hipError_t fh3k_gemm_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16,
+                                    const float *xs_inv, const float *bias, float *y, int M, int epi,
+                                    const float *aux, float *part, hipStream_t st) {
+    if (epi == EPI_SWIGLU && (N % 128)) return hipErrorInvalidValue;
+    if ((uint64_t)N * (uint64_t)row_bytes >= (1ull << 32)) return hipErrorInvalidValue;  // 32-bit row offsets
+    int C, S;
+    gemm_split(M, N, K, epi, C, S);
+    if (S > 1 && !part) return hipErrorInvalidValue;
+    const int m_tiles = (M + GEMM_BM - 1) / GEMM_BM;
+    const int n_tiles = epi == EPI_SWIGLU ? (N / 2) / 64 : (N + GEMM_BN - 1) / GEMM_BN;
+    hipLaunchKernelGGL(k_gemm, dim3((unsigned)(m_tiles * n_tiles * S)), dim3(256), 0, st,
+                       (const uint8_t *)W, row_bytes, N, K, (const half8 *)x16, xs_inv, bias, y, M,
+                       m_tiles, n_tiles, epi, aux, C, S > 1 ? part : nullptr);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || S == 1) return e;
     const int width = epi == EPI_SWIGLU ? N / 2 : N;
     const int64_t outs = (int64_t)M * width;
     hipLaunchKernelGGL(k_midm_sum, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, st, part, S, M, N, xs_inv,

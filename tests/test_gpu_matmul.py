@@ -162,6 +162,24 @@ def test_matmul_vs_oracle(gpu, oracle, M, K, N, path, dist, spread, use_bias):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("M,K,N", [(100, 1280, 384), (200, 13824, 640), (300, 5120, 1000)])
+def test_gemm_split_k(gpu, oracle, M, K, N):
+    """Large-M path with few tiles: K is split into windows (uneven last window
+    for K = 1280, 27 windows for K = 13824) whose sums are added in window
+    order; within tolerance of the oracle and bitwise repeatable."""
+    _say("gemm split-K M=%d K=%d N=%d" % (M, K, N))
+    rng = np.random.default_rng(M + K + N)
+    raw = H.random_q4k(rng, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    a = _dev_matmul(gpu, raw, K, N, x, bias, path=gpu.PATH_GEMM)
+    b = _dev_matmul(gpu, raw, K, N, x, bias, path=gpu.PATH_GEMM)
+    assert _bits_equal(a, b)
+    err = H.rel_fro(a, H.oracle_matmul(oracle, raw, K, N, x, bias))
+    _say("  rel_fro = %.3e" % err)
+    assert err <= TOL
+
+
 def test_matmul_deterministic_and_paths_agree(gpu, oracle):
     rng = np.random.default_rng(11)
     K, N, M = 2048, 256, 48

@@ -1007,6 +1007,9 @@ __device__ __forceinline__ void gemm_mfma(half8 (*ldsb)[64], int lane, const hal
     }
 }
 
+// Within a K step the wavefront runs at raised priority (s_setprio 2) from its
+// first MFMA to the barrier, so that of the two wavefronts on a SIMD the one
+// with matrix work issues first (measured +1.7 % on the DiT shapes).
 // Instruction order of one K step, given to the scheduler: the 32 MFMAs each
 // followed by up to four VALU (the next step's dequant), the B-fragment reads
 // of k-slice k+1 spread over the MFMAs of slice k, the next step's loads one
@@ -1099,29 +1102,37 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
         gemm_load_xs(xr, xoff, tbs, s + 1, xo);
         gemm_load_raw<2>(wr, woff, woffq, sb, re, ro);
         gemm_dequant(lds[1], ro, 1, wf, wl, h);
+        __builtin_amdgcn_s_setprio(2);
         gemm_mfma(lds[0], lane, xe, acc);
         gemm_pipe();
+        __builtin_amdgcn_s_setprio(0);
         __syncthreads();
         // step s+1 (chunk 1): MFMA from lds[1]; dequant chunk 2 into lds[0]
         gemm_load_xs(xr, xoff, tbs, s + 2, xe);
         gemm_load_raw<3>(wr, woff, woffq, sb, ro, re);
         gemm_dequant(lds[0], re, 2, wf, wl, h);
+        __builtin_amdgcn_s_setprio(2);
         gemm_mfma(lds[1], lane, xo, acc);
         gemm_pipe();
+        __builtin_amdgcn_s_setprio(0);
         __syncthreads();
         // step s+2 (chunk 2): MFMA from lds[0]; dequant chunk 3 into lds[1]
         gemm_load_xs(xr, xoff, tbs, s + 3, xo);
         gemm_load_raw<0>(wr, woff, woffq, nb, re, ro);
         gemm_dequant(lds[1], ro, 3, wf, wl, h);
+        __builtin_amdgcn_s_setprio(2);
         gemm_mfma(lds[0], lane, xe, acc);
         gemm_pipe();
+        __builtin_amdgcn_s_setprio(0);
         __syncthreads();
         // step s+3 (chunk 3): MFMA from lds[1]; dequant the next chunk 0 into lds[0]
         gemm_load_xs(xr, xoff, tbs, 4 * nb, xe);
         gemm_load_raw<1>(wr, woff, woffq, nb, ro, re);
         gemm_dequant(lds[0], re, 0, wf, wl, h);
+        __builtin_amdgcn_s_setprio(2);
         gemm_mfma(lds[1], lane, xo, acc);
         gemm_pipe();
+        __builtin_amdgcn_s_setprio(0);
         __syncthreads();
     }
 

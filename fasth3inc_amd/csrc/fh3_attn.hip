@@ -322,6 +322,10 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_fwd(const _Float16 *__restr
         const int kv = SPARSE ? sp.cnt[j] : n - j * ATT_KT;
         const bool active = SPARSE ? ((lst[e] >> (14 + (wave >> 1))) & 1) != 0 : true;
         if (active) {
+            // dense: raised wave priority through the tile's matrix and softmax
+            // work (the other wavefront on the SIMD is then mostly loading or
+            // waiting; +1-2 %; the sparse walk loses with it)
+            if constexpr (!SPARSE) __builtin_amdgcn_s_setprio(2);
             // S^T[key][query] for the 64 keys: two 32-key accumulators
             f32x16 s[2] = {f32x16{}, f32x16{}};
 #pragma unroll
@@ -387,6 +391,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_fwd(const _Float16 *__restr
                 }
             }
         }
+        if constexpr (!SPARSE) __builtin_amdgcn_s_setprio(0);
         if (e + 1 < nkt) store_tile(b ^ 1);
         __syncthreads();
     }

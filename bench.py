@@ -465,6 +465,21 @@ def main():
                                   "call_TFLOPs": round(g1.flop / (t_c * 1e-3) / 1e12, 2)}
     g1.free()
 
+    # ---------------- few-hundred-token products (split-K GEMM path) -------
+    # text-encoder prompt lengths: 65..512 tokens at K = N = 5120, where the
+    # 256 x 128 GEMM tiles alone would leave most CUs idle
+    mid = []
+    for M in (65, 128, 256, 512):
+        gm = Gemm("mid_%d" % M, M, 5120, 5120, "normal", 0.0, seed=0)
+        for i in range(5):
+            gm.call(i)
+        t_k = ev.time_ms(gm.kernel, 50, st)
+        mid.append({"M": M, "K": 5120, "N": 5120, "path": F.matmul_path(M, 5120), "kernel_us": round(t_k * 1e3, 2),
+                    "kernel_TFLOPs": round(gm.flop / (t_k * 1e-3) / 1e12, 1)})
+        gm.free()
+    extra["gemm_few_hundred_tokens"] = mid
+    log("[bench] GEMM 65..512 tokens: %s" % ", ".join("M=%d %.1f us" % (r["M"], r["kernel_us"]) for r in mid))
+
     # ---------------- DiT GEMMs --------------------------------------------
     shapes = [("attn_qkv", 8192, 5120, 15360, "outliers", 0.0), ("attn_out", 8192, 5120, 5120, "outliers", 0.0)]
     if not args.quick:

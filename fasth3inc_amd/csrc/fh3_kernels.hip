@@ -1273,6 +1273,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
         __builtin_amdgcn_wave_barrier();
     };
     const bool rows_in = m0 + 64 * wave + 64 <= M;
+    // 16-byte stores and gate reads need 16-byte aligned Y and aux (the
+    // entry points accept any float pointer for them; part is the library's)
+    const bool out16 = ((reinterpret_cast<uintptr_t>(Y) | reinterpret_cast<uintptr_t>(aux)) & 15) == 0;
     if (part) {
         // split K: this window's raw sums, part[ks][t][row] over all N rows
         const bool vec = rows_in && (N & 3) == 0 &&
@@ -1314,7 +1317,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
     if (epi == EPI_SWIGLU) {
         // tiles ob = 0, 1 hold val rows nt*64 + 32*ob + l%32, tiles 2, 3 the
         // matching gate rows
-        if (rows_in && (F & 3) == 0 && nt * 64 + 64 <= F) {
+        if (rows_in && out16 && (F & 3) == 0 && nt * 64 + 64 <= F) {
 #pragma unroll
             for (int tb = 0; tb < 2; tb++) {
                 const int tb0 = m0 + 64 * wave + 32 * tb;
@@ -1351,7 +1354,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
         }
         return;
     }
-    if (rows_in && (N & 3) == 0 && n0 + 128 <= N) {
+    if (rows_in && out16 && (N & 3) == 0 && n0 + 128 <= N) {
 #pragma unroll
         for (int tb = 0; tb < 2; tb++) {
             const int tb0 = m0 + 64 * wave + 32 * tb;

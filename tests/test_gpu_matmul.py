@@ -291,3 +291,40 @@ def test_graph_replay_matches_eager(gpu):
                 assert _bits_equal(dy.download(np.float32, (M, N)), ref), (rep, M)
     finally:
         g.close()
+
+
+@pytest.mark.parametrize("epi", [0, 1, 2])
+def test_gemm_output_any_float_alignment(gpu, epi):
+    """y (and the gate) may sit at any float offset: a 4-byte-offset output
+    gives bit for bit what an aligned one does, for every epilogue (the GEMM
+    stores full blocks 16 bytes at a time only when both are 16-byte aligned)."""
+    F = gpu
+    M, K, N = 300, 1024, 256
+    _say("gemm unaligned output epi=%d" % epi)
+    rng = np.random.default_rng(31 + epi)
+    raw = H.random_q4k(rng, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    W = N // 2 if epi == 2 else N
+    gate = rng.standard_normal((M, N)).astype(np.float32)
+    h = rng.standard_normal((M, N)).astype(np.float32)
+    dw = F.DeviceBuffer.from_array(raw)
+    dx, db = F.DeviceBuffer.from_array(x), F.DeviceBuffer.from_array(bias)
+    outs = []
+    for off in (0, 4):
+        dy = F.DeviceBuffer(M * W * 4 + 16)
+        dg = F.DeviceBuffer(M * N * 4 + 16)
+        y0 = h[:, :W] if epi == 1 else np.zeros((M, W), np.float32)
+        F._check(F.lib().fh3_hip_memcpy_htod(dy.ptr + off, y0.ctypes.data, y0.nbytes), "htod")
+        F._check(F.lib().fh3_hip_memcpy_htod(dg.ptr + off, gate.ctypes.data, gate.nbytes), "htod")
+        assert F.matmul_path(M, K) == F.PATH_GEMM
+        if epi == 0:
+            F.matmul_dev(dw, K, N, dx, dy.ptr + off, M, db)
+        else:
+            F.matmul_epi_dev(dw, K, N, dx, M, epi, dy.ptr + off, dg.ptr + off if epi == 1 else None, db)
+        F.synchronize()
+        y = np.empty((M, W), np.float32)
+        F._check(F.lib().fh3_hip_memcpy_dtoh(y.ctypes.data, dy.ptr + off, y.nbytes), "dtoh")
+        outs.append(y)
+    assert np.isfinite(outs[0]).all()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))

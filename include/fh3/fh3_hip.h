@@ -50,7 +50,9 @@ int fh3_hip_dequant_dev(int type, const void *d_src, float *d_dst, int64_t rows,
 
 /* Device-resident fh3_matmul: d_y[n_tok][w->out] = d_x[n_tok][w->in] * W^T
  * (+ d_bias).  w->data is a device pointer to the packed rows (16-byte
- * aligned), w->in % 256 == 0.  Q4_K runs the kernels described here; the
+ * aligned; d_x 16-byte aligned, d_y and d_bias any float pointer: a 16-byte
+ * aligned d_y with out % 4 == 0 takes the faster full-block stores of the
+ * large-M kernel), w->in % 256 == 0.  Q4_K runs the kernels described here; the
  * other types fh3_dequant decodes are first decoded to fp16 rows (the exact
  * value rounded once; F16 used as it is) into a library buffer of
  * out * in * 2 bytes, then multiplied with the same activation handling and

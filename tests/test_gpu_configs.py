@@ -8,7 +8,7 @@ Each configuration runs whole on the GPU with the benchmark's seeded inputs:
      and K=13824 -> N=5120 on SiLU-gated activations
 Configurations 1 and 2 are compared with the oracle in full.  For 3 and 4 the
 oracle computes a seeded subset of tokens (output rows depend only on their own
-activation row; the reference's survey of this path suggests the same), which
+activation row, as in the reference's fh3_matmul loop over tokens), which
 includes the first and last token of the tile edges.  At full size a property
 that does not depend on the oracle is also checked: permuting tokens permutes
 the output rows bit for bit (each token's sum runs over k in a fixed order,

@@ -1065,15 +1065,59 @@ __device__ __forceinline__ void gemm_load_raw(__amdgpu_buffer_rsrc_t wr, uint32_
 
 // B-fragment layout: fragment rb*4 + kk holds rows 32rb..32rb+31 x k 16kk..16kk+15
 // of the step; lane l holds row l%32 at k offset 8*(l/32).
+// Group scale of group 4*upper + j (upper uniform, j in 0..3 may differ per
+// lane): the same D and C as q4k_group_fast.
+__device__ __forceinline__ void q4k_group_j(const u32x4 hdr, bool upper, int j, float &D, float &C) {
+    const int sh = 8 * j;
+    uint32_t sc, mn;
+    if (!upper) {
+        sc = (hdr.y >> sh) & 63u;
+        mn = (hdr.z >> sh) & 63u;
+    } else {
+        sc = ((hdr.w >> sh) & 15u) | (((hdr.y >> (sh + 6)) & 3u) << 4);
+        mn = ((hdr.w >> (sh + 4)) & 15u) | (((hdr.z >> (sh + 6)) & 3u) << 4);
+    }
+    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x & 0xFFFFu));
+    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x >> 16));
+    D = d * (float)sc;
+    C = -(dmin * (float)mn + 1024.0f * D);
+}
+
+// q4k_deq8_f16 with the nibble half as a shift (0 low, 4 high) that may
+// differ per lane.
+__device__ __forceinline__ half8 q4k_deq8_sh(uint32_t u0, uint32_t u1, int sh, float D, float C) {
+    const uint32_t a = (u0 >> sh) & 0x0F0F0F0Fu;
+    const uint32_t b = (u1 >> sh) & 0x0F0F0F0Fu;
+    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u);
+    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u);
+    const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u);
+    const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u);
+    const u32x4 q = {fma_mix_pair(D, p0, C), fma_mix_pair(D, p1, C), fma_mix_pair(D, p2, C), fma_mix_pair(D, p3, C)};
+    return __builtin_bit_cast(half8, q);
+}
+
+// Value of the neighbouring lane (lane ^ 1), one DPP move (quad_perm 1,0,3,2).
+__device__ __forceinline__ float lane_swap1(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
+}
+
+// Chunk c of a super-block: 32 quant bytes per row, low nibbles group 2c,
+// high nibbles group 2c + 1.  The two threads of a row are adjacent lanes
+// (h = lane & 1) holding 16 bytes each; each decodes the scale of group
+// 2c + h only and takes the other group's (D, C) from its neighbour, then
+// writes its own nibble half first: low nibbles to fragment wf + h, high
+// nibbles to wf + 2 + h.
 __device__ __forceinline__ void gemm_dequant(half8 (*ldsb)[64], const GemmRaw &r, int s, int wf, int wl, int h) {
     const int c = s & 3;
-    float Dlo, Clo, Dhi, Chi;
-    q4k_group_fast(r.hv, 2 * c, Dlo, Clo);
-    q4k_group_fast(r.hv, 2 * c + 1, Dhi, Chi);
-    ldsb[wf + h][wl] = q4k_deq8_f16(r.qv.x, r.qv.y, false, Dlo, Clo);
-    ldsb[wf + h][wl + 32] = q4k_deq8_f16(r.qv.z, r.qv.w, false, Dlo, Clo);
-    ldsb[wf + 2 + h][wl] = q4k_deq8_f16(r.qv.x, r.qv.y, true, Dhi, Chi);
-    ldsb[wf + 2 + h][wl + 32] = q4k_deq8_f16(r.qv.z, r.qv.w, true, Dhi, Chi);
+    float Dm, Cm;
+    q4k_group_j(r.hv, c >= 2, ((2 * c) & 3) + h, Dm, Cm);
+    const float Do = lane_swap1(Dm), Co = lane_swap1(Cm);
+    const int own = wf + 3 * h, oth = wf + 2 - h;
+    const int sho = 4 * h, sht = 4 - 4 * h;
+    ldsb[own][wl] = q4k_deq8_sh(r.qv.x, r.qv.y, sho, Dm, Cm);
+    ldsb[own][wl + 32] = q4k_deq8_sh(r.qv.z, r.qv.w, sho, Dm, Cm);
+    ldsb[oth][wl] = q4k_deq8_sh(r.qv.x, r.qv.y, sht, Do, Co);
+    ldsb[oth][wl + 32] = q4k_deq8_sh(r.qv.z, r.qv.w, sht, Do, Co);
 }
 
 // Activation fragments of K step s for k_gemm: xr covers the wavefront's two
@@ -1160,7 +1204,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
     // weight-loader role: rows n0..n0+127, or (SwiGLU) 64 val rows from
     // nt*64 and the 64 gate rows F + nt*64..  Offsets from the first row fit
     // 32 bits (the launcher requires N * row_bytes < 2^32).
-    const int r = tid & 127, h = tid >> 7;
+    // two adjacent lanes per weight row (h = which 16 of a chunk's 32 bytes)
+    const int r = tid >> 1, h = tid & 1;
     const int F = N >> 1;
     const int rowbase = epi == EPI_SWIGLU ? nt * 64 : n0;
     int orow = n0 + r;

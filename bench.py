@@ -43,8 +43,8 @@ METRIC = "Q4_K GEMM TFLOP/s + GEMV weight GB/s (% roofline); DiT block linear ms
 # FETCH_SIZE = 128 MiB and WRITE_SIZE = 256 MiB.  Summaries:
 # profiles/k_skinny_gemv_m1-16_k5120.md, profiles/k_gemm_dit_attention_m8192_k5120.md,
 # profiles/hbm_counters_copy_256MiB.md.  Re-measure when the kernels change.
-TRAFFIC_GEMV_MEAN = 33604290        # mean over the six GEMV shapes (algorithmic mean 32899072)
-TRAFFIC_GEMM = {"attn_qkv": 2342062189, "attn_out": 725600585}
+TRAFFIC_GEMV_MEAN = 33604030        # mean over the six GEMV shapes (algorithmic mean 32899072)
+TRAFFIC_GEMM = {"attn_qkv": 2324594574, "attn_out": 703181960}
 
 
 def q4k_bytes(N, K):

@@ -47,6 +47,10 @@ struct State {
     int vsa_T = 0, vsa_P = 0;
     DevBuf st_w, st_x, st_y, st_b;  // staging for the host-pointer wrappers
     int path = FH3_HIP_PATH_AUTO;
+    // Workspace buffers replaced while captured graphs exist stay allocated
+    // (graphs hold their addresses) until the last graph is destroyed.
+    int live_graphs = 0;
+    std::vector<void *> retired;
     std::recursive_mutex mu;
 };
 
@@ -77,16 +81,38 @@ int ensure_init() {
     return fh3_hip_init(env ? atoi(env) : 0);
 }
 
-// Grow-only device buffer.  A grow waits for the device first because
-// previously enqueued kernels may still read the old allocation.
-int grow(DevBuf &b, size_t need) {
-    if (b.cap >= need) return FH3_OK;
+bool capturing(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return st && hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+// Give up b's allocation: freed once the device is idle (enqueued kernels may
+// still read it), or kept until fh3_hip_graph_destroy has destroyed the last
+// graph when captured graphs exist (their kernels hold its address).
+int release(DevBuf &b) {
     if (b.p) {
-        FH3_HIPCALL(hipDeviceSynchronize());
-        FH3_HIPCALL(hipFree(b.p));
-        b.p = nullptr;
-        b.cap = 0;
+        if (g.live_graphs > 0) {
+            g.retired.push_back(b.p);
+        } else {
+            FH3_HIPCALL(hipDeviceSynchronize());
+            FH3_HIPCALL(hipFree(b.p));
+        }
     }
+    b.p = nullptr;
+    b.cap = 0;
+    return FH3_OK;
+}
+
+// Grow-only device buffer.  A grow allocates, so it is refused while `st` is
+// being captured into a graph: the call must have run once eagerly first.
+int grow(DevBuf &b, size_t need, hipStream_t st) {
+    if (b.cap >= need) return FH3_OK;
+    if (capturing(st))
+        return set_err(FH3_E_INVALID,
+                       "the library workspace must grow to %zu bytes while the stream is captured into a graph; "
+                       "run the call once eagerly before capturing it", need);
+    int rc = release(b);
+    if (rc != FH3_OK) return rc;
     FH3_HIPCALL(hipMalloc(&b.p, need));
     b.cap = need;
     return FH3_OK;
@@ -222,6 +248,8 @@ extern "C" void fh3_hip_shutdown(void) {
     }
     for (auto &r : g.regs) (void)hipFree(r.dev);
     g.regs.clear();
+    for (void *p : g.retired) (void)hipFree(p);
+    g.retired.clear();
     for (int &k : g.vsa_key) k = -1;  // the VSA geometry was freed with vsa_geo
     g.vsa_T = g.vsa_P = 0;
     (void)hipStreamDestroy(g.stream);
@@ -300,6 +328,8 @@ extern "C" int fh3_hip_graph_end(void *stream, void **graph_exec) {
     (void)hipGraphDestroy(graph);
     if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
     *graph_exec = (void *)exec;
+    std::lock_guard<std::recursive_mutex> lk(g.mu);
+    g.live_graphs++;
     return FH3_OK;
 }
 
@@ -312,6 +342,17 @@ extern "C" int fh3_hip_graph_launch(void *graph_exec, void *stream) {
 extern "C" int fh3_hip_graph_destroy(void *graph_exec) {
     if (!graph_exec) return FH3_OK;
     FH3_HIPCALL(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+    std::lock_guard<std::recursive_mutex> lk(g.mu);
+    if (g.live_graphs > 0 && --g.live_graphs == 0 && !g.retired.empty()) {
+        // no graph holds the replaced workspace buffers any more
+        hipError_t e = hipDeviceSynchronize();
+        for (void *p : g.retired) {
+            const hipError_t f = hipFree(p);
+            if (e == hipSuccess) e = f;
+        }
+        g.retired.clear();
+        if (e != hipSuccess) return hip_fail(e, "fh3_hip_graph_destroy: freeing replaced workspace");
+    }
     return FH3_OK;
 }
 
@@ -404,7 +445,7 @@ static int product16(const Fh3W *w, const void *x16, const float *xs_inv, int n_
     const int K = (int)w->in, N = (int)w->out;
     const void *w16 = w->data;
     if (w->type != FH3_QUANT_F16) {
-        int rc = grow(g.w16, (size_t)w->out * (size_t)w->in * 2);
+        int rc = grow(g.w16, (size_t)w->out * (size_t)w->in * 2, st);
         if (rc != FH3_OK) return rc;
         FH3_HIPCALL(fh3k_weights_f16(w->type, w->data, (int64_t)fh3_row_bytes(w->type, w->in), K, N, g.w16.p, st));
         w16 = g.w16.p;
@@ -416,13 +457,25 @@ static int product16(const Fh3W *w, const void *x16, const float *xs_inv, int n_
     return FH3_OK;
 }
 
+// Partial-sum bytes of the split-K kernels for a Q4_K product (0 when the
+// chosen kernel does not split K).
+static size_t part_bytes(const Fh3W *w, int n_tok, int epi) {
+    const int K = (int)w->in, N = (int)w->out;
+    const int path = choose_path(n_tok, w->in);
+    if (path == FH3_HIP_PATH_MIDM) return fh3k_midm_part_bytes(N, K, n_tok);
+    if (path == FH3_HIP_PATH_GEMM) return fh3k_gemm_part_bytes(N, K, n_tok, epi);
+    return 0;
+}
+
+// part_ext: partial sums in caller-provided device memory (at least
+// part_bytes()), else in the library's grow-only buffer.
 static int product(const Fh3W *w, const void *prep, int n_tok, const float *bias, float *d_y, hipStream_t st,
-                   int epi = FH3_EPI_NONE, const float *aux = nullptr) {
+                   int epi = FH3_EPI_NONE, const float *aux = nullptr, float *part_ext = nullptr) {
     if (w->type != FH3_QUANT_Q4_K) {
         std::lock_guard<std::recursive_mutex> lk(g.mu);
         if (choose_path(n_tok, w->in) == FH3_HIP_PATH_GEMV8) {
             // the prepared form is then a copy of x: make the fragments here
-            int rc = grow(g.ws2, fh3_hip_prepared_bytes(n_tok, w->in));
+            int rc = grow(g.ws2, fh3_hip_prepared_bytes(n_tok, w->in), st);
             if (rc != FH3_OK) return rc;
             float *xs = (float *)((char *)g.ws2.p + prep_scale_offset(n_tok, w->in));
             FH3_HIPCALL(fh3k_xprep((const float *)prep, n_tok, (int)w->in, (int)prep_rows(n_tok), g.ws2.p, xs, st));
@@ -439,23 +492,22 @@ static int product(const Fh3W *w, const void *prep, int n_tok, const float *bias
         FH3_HIPCALL(fh3k_gemv8_epi(w->data, row_bytes, N, K, (const float *)prep, bias, d_y, n_tok, epi, aux, st));
     } else if (path == FH3_HIP_PATH_SKINNY) {
         FH3_HIPCALL(fh3k_skinny_epi(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, epi, aux, st));
-    } else if (path == FH3_HIP_PATH_MIDM) {
-        std::lock_guard<std::recursive_mutex> lk(g.mu);
-        int rc = grow(g.part, fh3k_midm_part_bytes(N, K, n_tok));
-        if (rc != FH3_OK) return rc;
-        FH3_HIPCALL(fh3k_midm_epi(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, epi, aux,
-                                  (float *)g.part.p, st));
     } else {
-        // few tokens: the kernel splits K and needs the partial-sum workspace
-        const size_t pb = fh3k_gemm_part_bytes(N, K, n_tok, epi);
+        // the split-K kernels (middle M, and the GEMM with few tiles) need the
+        // partial-sum workspace
+        const size_t pb = part_bytes(w, n_tok, epi);
         std::unique_lock<std::recursive_mutex> lk(g.mu, std::defer_lock);
-        if (pb) {
+        float *part = part_ext;
+        if (pb && !part) {
             lk.lock();
-            int rc = grow(g.part, pb);
+            int rc = grow(g.part, pb, st);
             if (rc != FH3_OK) return rc;
+            part = (float *)g.part.p;
         }
-        FH3_HIPCALL(fh3k_gemm_epi(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, epi, aux,
-                                  (float *)g.part.p, st));
+        if (path == FH3_HIP_PATH_MIDM)
+            FH3_HIPCALL(fh3k_midm_epi(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, epi, aux, part, st));
+        else
+            FH3_HIPCALL(fh3k_gemm_epi(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, epi, aux, part, st));
     }
     return FH3_OK;
 }
@@ -499,7 +551,7 @@ static int matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok, co
     if (w->type != FH3_QUANT_Q4_K) {
         std::lock_guard<std::recursive_mutex> lk(g.mu);
         const int64_t rows = path16(n_tok) == FH3_HIP_PATH_SKINNY ? round_up(n_tok, 32) : prep_rows(n_tok);
-        rc = grow(g.ws, fh3_hip_prepared_bytes(n_tok, w->in));
+        rc = grow(g.ws, fh3_hip_prepared_bytes(n_tok, w->in), st);
         if (rc != FH3_OK) return rc;
         float *xs = (float *)((char *)g.ws.p + prep_scale_offset(n_tok, w->in));
         FH3_HIPCALL(fh3k_xprep(d_x, n_tok, (int)w->in, (int)rows, g.ws.p, xs, st));
@@ -515,7 +567,7 @@ static int matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok, co
     // the small- and middle-M kernels only read round_up(n_tok, 32) prepared rows
     const int64_t rows =
         path == FH3_HIP_PATH_SKINNY || path == FH3_HIP_PATH_MIDM ? round_up(n_tok, 32) : prep_rows(n_tok);
-    rc = grow(g.ws, fh3_hip_prepared_bytes(n_tok, w->in));
+    rc = grow(g.ws, fh3_hip_prepared_bytes(n_tok, w->in), st);
     if (rc != FH3_OK) return rc;
     rc = prepare(d_x, n_tok, w->in, g.ws.p, rows, st);
     if (rc != FH3_OK) return rc;
@@ -545,6 +597,21 @@ extern "C" int fh3_hip_matmul_prepared_epi_dev(const Fh3W *w, const void *d_prep
     if (rc != FH3_OK) return rc;
     return product(w, d_prep, n_tok, d_bias_or_null, d_out, stream ? (hipStream_t)stream : g.stream, epi, d_aux);
 }
+
+extern "C" size_t fh3_hip_matmul_workspace_bytes(const Fh3W *w, int n_tok, int epi, int prepared) {
+    if (!w || w->in <= 0 || w->out <= 0 || n_tok <= 0 || w->in % 256 || w->in > fh3k_max_in() ||
+        fh3k_dequant_block_len(w->type) == 0)
+        return 0;
+    const size_t prep = fh3_hip_prepared_bytes(n_tok, w->in);
+    if (w->type != FH3_QUANT_Q4_K) {
+        const size_t w16 = w->type == FH3_QUANT_F16 ? 0 : (size_t)w->out * (size_t)w->in * 2;
+        const bool own_prep = !prepared || choose_path(n_tok, w->in) == FH3_HIP_PATH_GEMV8;
+        return w16 + (own_prep ? prep : 0);
+    }
+    const bool gemv8 = choose_path(n_tok, w->in) == FH3_HIP_PATH_GEMV8;
+    return (prepared || gemv8 ? 0 : prep) + part_bytes(w, n_tok, epi);
+}
+
 
 extern "C" int fh3_hip_prepare_x_norm_dev(const float *d_x, int n_tok, int64_t in, const float *d_norm_w, float eps,
                                           const float *d_shift, const float *d_scale, void *d_prep, void *stream) {
@@ -604,9 +671,10 @@ static int attention_dev(const float *q, const float *k, const float *v, int64_t
     int rc = ensure_init();
     if (rc != FH3_OK) return rc;
     std::lock_guard<std::recursive_mutex> lk(g.mu);
-    if ((rc = grow(g.attn, fh3k_attn_ws_bytes(n, heads, hd))) != FH3_OK) return rc;
+    hipStream_t st = stream ? (hipStream_t)stream : g.stream;
+    if ((rc = grow(g.attn, fh3k_attn_ws_bytes(n, heads, hd), st)) != FH3_OK) return rc;
     FH3_HIPCALL(fh3k_attention(q, k, v, ld, n, heads, hd, qn_w, kn_w, eps, cs, sn, cs ? rot : 0, g.attn.p, d_o,
-                               (int64_t)heads * hd, stream ? (hipStream_t)stream : g.stream));
+                               (int64_t)heads * hd, st));
     return FH3_OK;
 }
 
@@ -724,10 +792,13 @@ static int vsa_geometry(const Fh3Seq *sq, int tile, std::vector<int> &tok, std::
 // Device copy of the geometry: inv[T] (1/count), cnt[T], gather[slots] (token
 // of each 64-slot tile position, -1 empty), kept while the sequence shape
 // does not change.
-static int vsa_plan(const Fh3Seq *sq, int tile, const char *fn) {
+static int vsa_plan(const Fh3Seq *sq, int tile, hipStream_t st, const char *fn) {
     const int key[8] = {sq->seq_len, sq->num_text, sq->num_audio, sq->num_video, sq->grid_t, sq->grid_h, sq->grid_w,
                         tile};
     if (memcmp(key, g.vsa_key, sizeof key) == 0) return FH3_OK;
+    if (capturing(st))
+        return set_err(FH3_E_INVALID, "%s: a new sequence shape during graph capture; run the call once eagerly "
+                                      "before capturing it", fn);
     std::vector<int> tok, off;
     int P = 0;
     const int T = vsa_geometry(sq, tile, tok, off, &P);
@@ -746,7 +817,10 @@ static int vsa_plan(const Fh3Seq *sq, int tile, const char *fn) {
         const int i = (int)(sl / 64), r = (int)(sl % 64);
         h_gat[sl] = (i < T && r < h_cnt[i]) ? tok[off[i] + r] : -1;
     }
-    int rc = grow(g.vsa_geo, host.size() * sizeof(int));
+    // captured graphs keep reading the geometry they were captured with: give
+    // the new one its own buffer
+    int rc = g.live_graphs > 0 ? release(g.vsa_geo) : FH3_OK;
+    if (rc == FH3_OK) rc = grow(g.vsa_geo, host.size() * sizeof(int), st);
     if (rc != FH3_OK) return rc;
     FH3_HIPCALL(hipDeviceSynchronize());  // earlier calls may still read the old geometry
     FH3_HIPCALL(hipMemcpy(g.vsa_geo.p, host.data(), host.size() * sizeof(int), hipMemcpyHostToDevice));
@@ -772,7 +846,8 @@ static int vsa_dev(const Fh3VsaCfg *c, const float *q, const float *k, const flo
     int rc = ensure_init();
     if (rc != FH3_OK) return rc;
     std::lock_guard<std::recursive_mutex> lk(g.mu);
-    if ((rc = vsa_plan(sq, tile, fn)) != FH3_OK) return rc;
+    hipStream_t st = stream ? (hipStream_t)stream : g.stream;
+    if ((rc = vsa_plan(sq, tile, st, fn)) != FH3_OK) return rc;
     const int T = g.vsa_T, P = g.vsa_P, NV = T - P;
     int kv = 0;
     if (NV > 0) {  // src/core/fh3_vsa.c:165-172
@@ -780,13 +855,13 @@ static int vsa_dev(const Fh3VsaCfg *c, const float *q, const float *k, const flo
         kv = kv < 1 ? 1 : (kv > NV ? NV : kv);
     }
     const int all = sparsity <= 0.0f || kv == NV;
-    if ((rc = grow(g.vsa_ws, fh3k_vsa_ws_bytes(T, heads, hd))) != FH3_OK) return rc;
+    if ((rc = grow(g.vsa_ws, fh3k_vsa_ws_bytes(T, heads, hd), st)) != FH3_OK) return rc;
     const float *d_inv = (const float *)g.vsa_geo.p;
     const int *d_cnt = (const int *)(d_inv + T), *d_gat = d_cnt + T;
     const float scale = 1.0f / sqrtf((float)hd);
     FH3_HIPCALL(fh3k_vsa_attention(q, k, v, ld, ldv, qn_w, kn_w, eps, cs, sn, cs ? rot : 0, gate, o,
                                    (int64_t)heads * hd, heads, hd, d_inv, d_gat, d_cnt, T, P, kv, all, scale,
-                                   g.vsa_ws.p, stream ? (hipStream_t)stream : g.stream));
+                                   g.vsa_ws.p, st));
     return FH3_OK;
 }
 
@@ -861,7 +936,7 @@ extern "C" void fh3_dequant(int type, const void *src, float *dst, int64_t n) {
     if (rc != FH3_OK) { report("fh3_dequant", rc); return; }
     std::lock_guard<std::recursive_mutex> lk(g.mu);
     const size_t in_bytes = fh3_row_bytes(type, cnt), out_bytes = (size_t)cnt * sizeof(float);
-    if ((rc = grow(g.st_w, in_bytes)) != FH3_OK || (rc = grow(g.st_y, out_bytes)) != FH3_OK) {
+    if ((rc = grow(g.st_w, in_bytes, g.stream)) != FH3_OK || (rc = grow(g.st_y, out_bytes, g.stream)) != FH3_OK) {
         report("fh3_dequant", rc);
         return;
     }
@@ -891,8 +966,8 @@ extern "C" void fh3_matmul(const Fh3W *w, const float *x, float *y, int n_tok, c
     // a registered weight (fh3_hip_register_weights) is used in place
     const void *dw = registered(w->data, wb);
     if (dw && ((uintptr_t)dw & 15u)) dw = nullptr;
-    if ((!dw && (rc = grow(g.st_w, wb))) || (rc = grow(g.st_x, xb)) || (rc = grow(g.st_y, yb)) ||
-        (bias_or_null && (rc = grow(g.st_b, bb)))) {
+    if ((!dw && (rc = grow(g.st_w, wb, g.stream))) || (rc = grow(g.st_x, xb, g.stream)) || (rc = grow(g.st_y, yb, g.stream)) ||
+        (bias_or_null && (rc = grow(g.st_b, bb, g.stream)))) {
         report("fh3_matmul", rc);
         return;
     }
@@ -916,7 +991,7 @@ extern "C" void fh3_attention(const float *q, const float *k, const float *v, fl
     if (rc != FH3_OK) { report("fh3_attention", rc); return; }
     std::lock_guard<std::recursive_mutex> lk(g.mu);
     const size_t b = (size_t)n * (size_t)heads * (size_t)hd * sizeof(float);
-    if ((rc = grow(g.st_w, 3 * b)) || (rc = grow(g.st_y, b))) { report("fh3_attention", rc); return; }
+    if ((rc = grow(g.st_w, 3 * b, g.stream)) || (rc = grow(g.st_y, b, g.stream))) { report("fh3_attention", rc); return; }
     float *dq = (float *)g.st_w.p, *dk = dq + b / 4, *dv = dk + b / 4;
     hipError_t e = hipMemcpy(dq, q, b, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(dk, k, b, hipMemcpyHostToDevice);
@@ -936,7 +1011,7 @@ extern "C" void fh3_vsa_attention(const Fh3VsaCfg *c, const float *q, const floa
     if (rc != FH3_OK) { report("fh3_vsa_attention", rc); return; }
     std::lock_guard<std::recursive_mutex> lk(g.mu);
     const size_t b = (size_t)seq->seq_len * (size_t)heads * (size_t)head_dim * sizeof(float);
-    if ((rc = grow(g.st_w, (gate ? 4 : 3) * b)) || (rc = grow(g.st_y, b))) { report("fh3_vsa_attention", rc); return; }
+    if ((rc = grow(g.st_w, (gate ? 4 : 3) * b, g.stream)) || (rc = grow(g.st_y, b, g.stream))) { report("fh3_vsa_attention", rc); return; }
     float *dq = (float *)g.st_w.p, *dk = dq + b / 4, *dv = dk + b / 4, *dg = gate ? dv + b / 4 : nullptr;
     hipError_t e = hipMemcpy(dq, q, b, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(dk, k, b, hipMemcpyHostToDevice);

@@ -183,6 +183,7 @@ SIGNATURES = {
     "fh3_hip_graph_end": (_c_int, [_c_void_p, ctypes.POINTER(_c_void_p)]),
     "fh3_hip_graph_launch": (_c_int, [_c_void_p, _c_void_p]),
     "fh3_hip_graph_destroy": (_c_int, [_c_void_p]),
+    "fh3_hip_matmul_workspace_bytes": (_c_size, [ctypes.POINTER(Fh3W), _c_int, _c_int, _c_int]),
     "fh3_hip_set_path": (_c_int, [_c_int]),
     "fh3_hip_skinny_max": (_c_int, []),
     "fh3_hip_matmul_path": (_c_int, [_c_int, _c_i64]),
@@ -361,6 +362,14 @@ def _ptr_of(b):
     return None if b is None else (b.ptr if isinstance(b, DeviceBuffer) else b)
 
 
+def matmul_workspace_bytes(K, N, n_tok, epi=0, prepared=False, qtype=FH3_QUANT_Q4_K):
+    """fh3_hip_matmul_workspace_bytes: library workspace a product allocates."""
+    w = Fh3W(qtype, K, N, None)
+    return lib().fh3_hip_matmul_workspace_bytes(ctypes.byref(w), n_tok, epi, int(prepared))
+
+
+
+
 def prepared_bytes(n_tok, K):
     return lib().fh3_hip_prepared_bytes(n_tok, K)
 
@@ -502,12 +511,15 @@ class Graph:
 def capture(fn, stream_ptr=None):
     """Capture the fh3_hip_* work fn() enqueues on the stream into a Graph."""
     _check(lib().fh3_hip_graph_begin(stream_ptr), "fh3_hip_graph_begin")
+    ex = ctypes.c_void_p()
     try:
         fn()
-    finally:
-        ex = ctypes.c_void_p()
-        rc = lib().fh3_hip_graph_end(stream_ptr, ctypes.byref(ex))
-    _check(rc, "fh3_hip_graph_end")
+    except BaseException:
+        # end the capture; the partial graph is of no use
+        if lib().fh3_hip_graph_end(stream_ptr, ctypes.byref(ex)) == FH3_OK:
+            lib().fh3_hip_graph_destroy(ex.value)
+        raise
+    _check(lib().fh3_hip_graph_end(stream_ptr, ctypes.byref(ex)), "fh3_hip_graph_end")
     return Graph(ex.value)
 
 

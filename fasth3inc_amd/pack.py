@@ -92,14 +92,21 @@ def write_pack(path, n_layers, specs, make_layer, name_fmt="blocks.{L}.{suffix}"
     return hdr.total_bytes
 
 
-def dit_block_specs(hidden, qkv_out, mlp_hidden, qtype=fh3.FH3_QUANT_Q4_K):
+def dit_block_specs(hidden, qkv_out, mlp_hidden, qtype=fh3.FH3_QUANT_Q4_K, inner=None, gate_compress=False):
     """The nine tensors of a DiT block in run order.  fc1 holds the value and
     gate halves of the gated MLP as one (2*mlp_hidden x hidden) matrix; the
-    norm weights are fp32 vectors."""
+    norm weights are fp32 vectors.  inner (default hidden) is the attention
+    width: the out projection maps inner -> hidden.  gate_compress=True makes
+    the VSA gate projection a (inner x hidden) matrix of type qtype, as in the
+    real model (src/model/fh3_dit.c:404-407); otherwise it is an fp32 vector of
+    hidden entries, which the product never reads."""
     f32 = fh3.FH3_QUANT_F32
+    inner = hidden if inner is None else inner
+    gc = (TensorSpec("attn.to_gate_compress.weight", qtype, hidden, inner) if gate_compress
+          else TensorSpec("attn.to_gate_compress.weight", f32, hidden, 1))
     return [TensorSpec("attn.qkv_proj.weight", qtype, hidden, qkv_out),
-            TensorSpec("attn.to_gate_compress.weight", f32, hidden, 1),
-            TensorSpec("attn.out_proj.weight", qtype, hidden, hidden),
+            gc,
+            TensorSpec("attn.out_proj.weight", qtype, inner, hidden),
             TensorSpec("mlp.fc1.weight", qtype, hidden, 2 * mlp_hidden),
             TensorSpec("mlp.fc2.weight", qtype, mlp_hidden, hidden),
             TensorSpec("norm1.weight", f32, hidden),
@@ -108,13 +115,25 @@ def dit_block_specs(hidden, qkv_out, mlp_hidden, qtype=fh3.FH3_QUANT_Q4_K):
             TensorSpec("attn.k_norm.weight", f32, 128)]
 
 
+# The real fh3 DiT block (src/cli/fh3_cli.c:935-941): hidden 5376, 56 heads of
+# 128 (inner 7168), feed-forward 14336; 238,480,384 bytes per block in the
+# reference's census (docs/data/census.json:17).
+REAL_DIT = dict(hidden=5376, qkv_out=21504, mlp_hidden=14336, inner=7168, gate_compress=True)
+
+
+def real_dit_block_specs(qtype=fh3.FH3_QUANT_Q4_K):
+    return dit_block_specs(qtype=qtype, **REAL_DIT)
+
+
 def synth_dit_block(specs, seed, L, sigma=0.02):
-    """Seeded contents of block L: Q4_K matrices quantised from N(0, sigma),
-    fp32 vectors of ones.  Stream ids are 0x100*L + tensor index."""
+    """Seeded contents of block L: matrices quantised to Q4_K from N(0, sigma),
+    fp32 vectors 1 + 0.1 N(0, 1) (norm weights).  Stream ids are
+    0x100*L + tensor index."""
     out = []
     for i, s in enumerate(specs):
         if s.qtype == fh3.FH3_QUANT_Q4_K:
             out.append(fh3.synth_q4k_weights(seed, 0x100 * L + i, s.ne1, s.ne0, sigma))
         else:
-            out.append(np.ones(s.ne0 * s.ne1, dtype=np.float32).view(np.uint8))
+            v = fh3.synth_x("normal", seed, 0x100 * L + i, 1, s.ne0 * s.ne1)[0]
+            out.append((1.0 + 0.1 * v).astype(np.float32).view(np.uint8))
     return out

@@ -81,9 +81,13 @@ int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok,
  *     per row);
  *   fh3_hip_prepare_x_dev: fill d_prep (16-byte aligned) from d_x[n_tok][in];
  *   fh3_hip_matmul_prepared_dev: the product from a prepared buffer; same
- *     results as fh3_hip_matmul_dev, no library workspace except the partial
- *     sums of the FH3_HIP_PATH_MIDM path.  (For the FH3_HIP_PATH_GEMV8 shapes
- *     the prepared form is a copy of x.) */
+ *     results as fh3_hip_matmul_dev.  Its only library workspace is the
+ *     partial sums of the split-K kernels: the FH3_HIP_PATH_MIDM path, and
+ *     the FH3_HIP_PATH_GEMM path while its 256 x 128 tiles number fewer than
+ *     about 512 (roughly 65..2048 tokens; fh3_hip_matmul_workspace_bytes
+ *     gives the exact size).  Weights of a type other than Q4_K also use the
+ *     fp16-row buffer.  (For the FH3_HIP_PATH_GEMV8 shapes the prepared form
+ *     is a copy of x.) */
 size_t fh3_hip_prepared_bytes(int n_tok, int64_t in);
 int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, void *d_prep, void *stream);
 int fh3_hip_matmul_prepared_dev(const Fh3W *w, const void *d_prep, float *d_y, int n_tok,
@@ -187,12 +191,26 @@ const void *fh3_hip_registered_ptr(const void *host, size_t bytes);
 /* HIP graph capture of work enqueued on a stream (NULL = the compute
  * stream), for launch-bound loops such as small-M text-encoder layers:
  * begin, enqueue fh3_hip_* calls on that stream, end -> an executable graph
- * that fh3_hip_graph_launch replays on any stream.  Calls captured this way
- * must not need to grow the library workspace (run them once eagerly first). */
+ * that fh3_hip_graph_launch replays on any stream.  A captured call must not
+ * need to grow the library workspace (or, for VSA, see a new sequence
+ * shape): it then returns FH3_E_INVALID without enqueuing anything, and the
+ * same call run once eagerly first makes its capture succeed.  A workspace
+ * that a later eager call grows gets a new buffer; the old one stays
+ * allocated while any graph made by fh3_hip_graph_end exists (graphs keep
+ * their buffer addresses), and is freed when fh3_hip_graph_destroy destroys
+ * the last of them.  Graphs therefore stay valid across workspace growth;
+ * replays of graphs that share a workspace buffer must not overlap. */
 int fh3_hip_graph_begin(void *stream);
 int fh3_hip_graph_end(void *stream, void **graph_exec);
 int fh3_hip_graph_launch(void *graph_exec, void *stream);
 int fh3_hip_graph_destroy(void *graph_exec);
+
+/* Bytes of library workspace a product allocates (0 when none): the prepared
+ * activations of fh3_hip_matmul_dev / fh3_hip_matmul_epi_dev (prepared = 0)
+ * plus the partial sums of the split-K kernels; with prepared = 1 the same for
+ * fh3_hip_matmul_prepared_dev / _prepared_epi_dev.  epi as below.  Under the
+ * current fh3_hip_set_path setting. */
+size_t fh3_hip_matmul_workspace_bytes(const Fh3W *w, int n_tok, int epi, int prepared);
 
 /* Kernel selection for fh3_hip_matmul_dev: FH3_HIP_PATH_AUTO picks
  *   - FH3_HIP_PATH_GEMV8 for n_tok <= 2 when its LDS fits (in <= 17920 for one

@@ -139,6 +139,40 @@ def test_swiglu_epilogue(gpu, oracle, M, use_bias):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("M,K,Fd,n_sample", [(300, 512, 192, None), (300, 768, 256, None), (4096, 1024, 1024, 96)])
+def test_swiglu_epilogue_direct_store(gpu, oracle, M, K, Fd, n_sample):
+    """SwiGLU written by k_gemm's own epilogue (no split of K, so no k_midm_sum):
+    full 256-token tiles and a partial last tile, through both the staged
+    16-byte stores (aligned output) and the scalar stores (output 4 bytes off)."""
+    F = gpu
+    N = 2 * Fd
+    assert F.matmul_path(M, K) == F.PATH_GEMM
+    assert F.matmul_workspace_bytes(K, N, M, F.EPI_SWIGLU, prepared=True) == 0, "the product would split K"
+    rng = np.random.default_rng(500 + M + K)
+    raw = F.synth_q4k_weights(M + K, 1, N, K, 0.05, 0.0)
+    x = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    dwt, dx, db = F.DeviceBuffer.from_array(raw), _buf(F, x), _buf(F, bias)
+    outs = []
+    for off in (0, 4):
+        _say("swiglu direct store M=%d K=%d F=%d out offset %d" % (M, K, Fd, off))
+        dout = F.DeviceBuffer(M * Fd * 4 + 16)
+        F.matmul_epi_dev(dwt, K, N, dx, M, F.EPI_SWIGLU, dout.ptr + off, None, db)
+        F.synchronize()
+        o = np.empty((M, Fd), np.float32)
+        F._check(F.lib().fh3_hip_memcpy_dtoh(o.ctypes.data, dout.ptr + off, o.nbytes), "dtoh")
+        outs.append(o)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    rows = np.arange(M) if n_sample is None else np.unique(np.concatenate(
+        [rng.choice(M, n_sample, replace=False), [0, 255, 256, M - 1]]))
+    y = H.oracle_matmul(oracle, raw, K, N, x[rows], bias)
+    ref = np.zeros((len(rows), Fd), np.float32)
+    H.elementwise(oracle, "fh3_oracle_", "swiglu", y, ref, len(rows), Fd)
+    err = H.rel_fro(outs[0][rows], ref)
+    _say("  rel_fro = %.3e" % err)
+    assert err <= TOL
+
+
 def test_epilogue_argument_errors(gpu):
     F = gpu
     dw = F.DeviceBuffer(144 * 256)

@@ -56,6 +56,9 @@ struct State {
 
 State g;
 thread_local char g_err[512] = "";
+// Device address of the fixed scratch array of fh3_kernels.hip, per device
+// (bound once per device by fh3_hip_init).
+void *g_scratch[64];
 
 int set_err(int code, const char *fmt, ...) {
     va_list ap;
@@ -229,6 +232,15 @@ extern "C" int fh3_hip_init(int device) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return set_err(FH3_ERR, "fh3_hip_init: device %d is %s; this library is built for gfx950", device,
                        prop.gcnArchName);
+    if (device >= (int)(sizeof g_scratch / sizeof g_scratch[0]))
+        return set_err(FH3_E_INVALID, "fh3_hip_init: device %d beyond the %d this library tracks", device,
+                       (int)(sizeof g_scratch / sizeof g_scratch[0]));
+    if (!g_scratch[device]) {
+        // the device's own copy of the fixed scratch array (this device is current)
+        void *p = nullptr;
+        FH3_HIPCALL(fh3k_scratch_bind(&p));
+        g_scratch[device] = p;
+    }
     FH3_HIPCALL(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
     g.device = device;
     g.init = true;
@@ -612,6 +624,39 @@ extern "C" size_t fh3_hip_matmul_workspace_bytes(const Fh3W *w, int n_tok, int e
     return (prepared || gemv8 ? 0 : prep) + part_bytes(w, n_tok, epi);
 }
 
+// The no-allocation product: fh3_hip_matmul_dev's kernels with their
+// workspace (prepared activations, then partial sums at a 256-byte aligned
+// offset) in the fixed scratch array bound by fh3_hip_init.
+extern "C" int fh3_hip_matmul_noalloc_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok,
+                                          const float *d_bias_or_null, void *stream) {
+    const char *fn = "fh3_hip_matmul_noalloc_dev";
+    int rc = check_weights(w, fn);
+    if (rc != FH3_OK) return rc;
+    if (w->type != FH3_QUANT_Q4_K) return set_err(FH3_E_INVALID, "%s: Q4_K weights only (type %d)", fn, w->type);
+    if (!d_x || !d_y || n_tok <= 0) return set_err(FH3_E_INVALID, "%s: NULL pointer or n_tok <= 0", fn);
+    if ((uintptr_t)d_x & 15u) return set_err(FH3_E_INVALID, "%s: x must be 16-byte aligned", fn);
+    if (!g.init || !g_scratch[g.device])
+        return set_err(FH3_E_INVALID, "%s: call fh3_hip_init first (it binds the scratch memory)", fn);
+    hipStream_t st = stream ? (hipStream_t)stream : g.stream;
+    const int path = choose_path(n_tok, w->in);
+    if (path == FH3_HIP_PATH_GEMV8) {  // this kernel needs no workspace
+        FH3_HIPCALL(fh3k_gemv8_epi(w->data, (int64_t)fh3_row_bytes(w->type, w->in), (int)w->out, (int)w->in, d_x,
+                                   d_bias_or_null, d_y, n_tok, FH3_EPI_NONE, nullptr, st));
+        return FH3_OK;
+    }
+    const size_t part_off = (size_t)round_up((int64_t)fh3_hip_prepared_bytes(n_tok, w->in), 256);
+    const size_t need = part_off + part_bytes(w, n_tok, FH3_EPI_NONE);
+    if (need > (size_t)FH3_HIP_NOALLOC_SCRATCH_BYTES)
+        return set_err(FH3_E_INVALID, "%s: n_tok=%d in=%lld out=%lld needs %zu bytes of scratch; the fixed scratch "
+                                      "holds %zu (use fh3_hip_matmul_dev)", fn, n_tok, (long long)w->in,
+                       (long long)w->out, need, (size_t)FH3_HIP_NOALLOC_SCRATCH_BYTES);
+    uint8_t *scr = (uint8_t *)g_scratch[g.device];
+    const int64_t rows =
+        path == FH3_HIP_PATH_SKINNY || path == FH3_HIP_PATH_MIDM ? round_up(n_tok, 32) : prep_rows(n_tok);
+    rc = prepare(d_x, n_tok, w->in, scr, rows, st);
+    if (rc != FH3_OK) return rc;
+    return product(w, scr, n_tok, d_bias_or_null, d_y, st, FH3_EPI_NONE, nullptr, (float *)(scr + part_off));
+}
 
 extern "C" int fh3_hip_prepare_x_norm_dev(const float *d_x, int n_tok, int64_t in, const float *d_norm_w, float eps,
                                           const float *d_shift, const float *d_scale, void *d_prep, void *stream) {

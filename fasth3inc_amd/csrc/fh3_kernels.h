@@ -118,6 +118,11 @@ hipError_t fh3k_vsa_attention(const float *q, const float *k, const float *v, in
 // Largest in-dimension (K) the activation preparation handles.
 int fh3k_max_in(void);
 
+// Device address, on the current device, of the fixed scratch array of
+// FH3_HIP_NOALLOC_SCRATCH_BYTES (fh3_hip.h) that the no-allocation entry point
+// uses as its workspace.
+hipError_t fh3k_scratch_bind(void **ptr);
+
 int fh3k_gemm_row_pad(void);
 
 #ifdef __cplusplus

@@ -24,6 +24,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fh3/fh3_hip.h"
 #include "fh3_kernels.h"
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -1769,6 +1770,17 @@ extern "C" hipError_t fh3k_rownorm_f32(const float *x, int M, int K, float *y, c
 }
 
 extern "C" int fh3k_max_in(void) { return 32768; }
+
+// Workspace of the no-allocation entry point (fh3_hip_matmul_noalloc_dev):
+// each device that loads this library holds its own copy until the process
+// ends.  Host code must never pass `scratch` itself to a kernel: its host-side
+// name is a stand-in, not a device address; fh3k_scratch_bind gives the
+// current device's address of it.
+static __device__ __align__(256) uint8_t scratch[FH3_HIP_NOALLOC_SCRATCH_BYTES];
+
+extern "C" hipError_t fh3k_scratch_bind(void **ptr) {
+    return hipGetSymbolAddress(ptr, HIP_SYMBOL(scratch));
+}
 
 // Super-blocks per wavefront C (compile-time, C <= nsb) and wavefronts per
 // workgroup NW (<= 8, runtime) for K/256 = nsb super-blocks: the fewest

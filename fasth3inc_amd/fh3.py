@@ -184,6 +184,8 @@ SIGNATURES = {
     "fh3_hip_graph_launch": (_c_int, [_c_void_p, _c_void_p]),
     "fh3_hip_graph_destroy": (_c_int, [_c_void_p]),
     "fh3_hip_matmul_workspace_bytes": (_c_size, [ctypes.POINTER(Fh3W), _c_int, _c_int, _c_int]),
+    "fh3_hip_matmul_noalloc_dev": (_c_int, [ctypes.POINTER(Fh3W), _c_void_p, _c_void_p, _c_int, _c_void_p,
+                                            _c_void_p]),
     "fh3_hip_set_path": (_c_int, [_c_int]),
     "fh3_hip_skinny_max": (_c_int, []),
     "fh3_hip_matmul_path": (_c_int, [_c_int, _c_i64]),
@@ -368,6 +370,15 @@ def matmul_workspace_bytes(K, N, n_tok, epi=0, prepared=False, qtype=FH3_QUANT_Q
     return lib().fh3_hip_matmul_workspace_bytes(ctypes.byref(w), n_tok, epi, int(prepared))
 
 
+NOALLOC_SCRATCH_BYTES = 64 << 20   # FH3_HIP_NOALLOC_SCRATCH_BYTES
+
+
+def matmul_noalloc_dev(d_w, K, N, d_x, d_y, n_tok, d_bias=None, stream_ptr=None, qtype=FH3_QUANT_Q4_K):
+    """fh3_hip_matmul_noalloc_dev: fh3_hip_matmul_dev with its workspace in the
+    library's fixed scratch array (allocates nothing)."""
+    w = Fh3W(qtype, K, N, _ptr_of(d_w))
+    _check(lib().fh3_hip_matmul_noalloc_dev(ctypes.byref(w), _ptr_of(d_x), _ptr_of(d_y), n_tok, _ptr_of(d_bias),
+                                            stream_ptr), "fh3_hip_matmul_noalloc_dev")
 
 
 def prepared_bytes(n_tok, K):

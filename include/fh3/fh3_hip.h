@@ -212,6 +212,24 @@ int fh3_hip_graph_destroy(void *graph_exec);
  * current fh3_hip_set_path setting. */
 size_t fh3_hip_matmul_workspace_bytes(const Fh3W *w, int n_tok, int epi, int prepared);
 
+/* The no-allocation product, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels and bit-identical results as
+ * fh3_hip_matmul_dev with Q4_K weights and no epilogue, but its workspace is
+ * a fixed array of FH3_HIP_NOALLOC_SCRATCH_BYTES in device memory that the
+ * library binds in fh3_hip_init (each device holds its own copy until the
+ * process ends).  The call allocates and frees nothing; it returns
+ * FH3_E_INVALID when the library is not initialised, for another weight
+ * type, or when the shape needs more workspace than the array holds (the
+ * message gives the size): every n_tok <= 64 at in <= 32768, and more tokens
+ * while prepared activations (about 2 * round_up(n_tok, 256) * in bytes) plus
+ * partial sums fit.  The array keeps the last call's contents; every call on
+ * a device shares it, so calls that overlap on one device (different streams,
+ * threads, or graph replays) race and must be serialised by the caller. */
+#define FH3_HIP_NOALLOC_SCRATCH_BYTES (64u << 20)
+int fh3_hip_matmul_noalloc_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok,
+                               const float *d_bias_or_null, void *stream);
+
 /* Kernel selection for fh3_hip_matmul_dev: FH3_HIP_PATH_AUTO picks
  *   - FH3_HIP_PATH_GEMV8 for n_tok <= 2 when its LDS fits (in <= 17920 for one
  *     token, in <= 8960 for two): activations quantised to int16 (two int8

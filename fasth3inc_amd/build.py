@@ -73,17 +73,34 @@ def build_lib(check=False, quiet=False):
         _run([HIPCC] + HIP_FLAGS + extra + ["-c", os.path.join(CSRC, src), "-o", obj], quiet)
         objs.append(obj)
     tmp = LIB + ".tmp"
+    # exports: exactly the header API (libfh3hip.map); -Bsymbolic binds the
+    # library's calls between its own exported functions inside it
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs +
-         ["-lgomp", "-lpthread", "-Wl,--no-undefined", "-Wl,-soname,libfh3hip.so"], quiet)
+         ["-lgomp", "-lpthread", "-Wl,--no-undefined", "-Wl,-soname,libfh3hip.so", "-Wl,-Bsymbolic",
+          "-Wl,--version-script=" + os.path.join(CSRC, "libfh3hip.map")], quiet)
     os.replace(tmp, LIB)
     return LIB
+
+
+C_CALLER_SRC = os.path.join(ROOT, "tests", "c", "fh3_c_caller.c")
+C_CALLER = os.path.join(ROOT, "tests", "c", "fh3_c_caller")
+
+
+def build_c_caller(quiet=False):
+    """The C99 caller the GPU tests run: compiled against include/fh3/*.h
+    only and linked to the library, as a C program of the reference would be."""
+    _run([CC, "-std=gnu99", "-O2", "-Wall", "-Wextra", "-Werror", "-D_GNU_SOURCE", "-I" + INC, C_CALLER_SRC,
+          "-o", C_CALLER, "-L" + LIBDIR, "-lfh3hip", "-Wl,-rpath,$ORIGIN/../../fasth3inc_amd/lib", "-lm"], quiet)
+    return C_CALLER
 
 
 def build(check=False, quiet=False):
     if shutil.which(HIPCC) is None and not os.path.exists(HIPCC):
         raise RuntimeError("hipcc not found; the HIP library cannot be built")
     build_oracle(quiet)
-    return build_lib(check, quiet)
+    lib = build_lib(check, quiet)
+    build_c_caller(quiet)
+    return lib
 
 
 if __name__ == "__main__":

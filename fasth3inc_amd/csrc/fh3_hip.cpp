@@ -143,22 +143,22 @@ int choose_path(int n_tok, int64_t in) {
 // ---------------------------------------------------------------------------
 // Internal helpers shared with the C trunk streamer (fh3_hip_internal.h)
 // ---------------------------------------------------------------------------
-extern "C" int fh3_hip_set_error(int code, const char *msg) { return set_err(code, "%s", msg); }
+extern "C" int fh3i_set_error(int code, const char *msg) { return set_err(code, "%s", msg); }
 
-extern "C" int fh3_hip_host_alloc(void **p, size_t bytes) {
+extern "C" int fh3i_host_alloc(void **p, size_t bytes) {
     int rc = ensure_init();
     if (rc != FH3_OK) return rc;
     FH3_HIPCALL(hipHostMalloc(p, bytes, hipHostMallocDefault));
     return FH3_OK;
 }
 
-extern "C" int fh3_hip_host_free(void *p) {
+extern "C" int fh3i_host_free(void *p) {
     if (!p) return FH3_OK;
     FH3_HIPCALL(hipHostFree(p));
     return FH3_OK;
 }
 
-extern "C" int fh3_hip_stream_create(void **st) {
+extern "C" int fh3i_stream_create(void **st) {
     int rc = ensure_init();
     if (rc != FH3_OK) return rc;
     hipStream_t s = nullptr;
@@ -167,23 +167,23 @@ extern "C" int fh3_hip_stream_create(void **st) {
     return FH3_OK;
 }
 
-extern "C" int fh3_hip_stream_destroy(void *st) {
+extern "C" int fh3i_stream_destroy(void *st) {
     if (!st) return FH3_OK;
     FH3_HIPCALL(hipStreamDestroy((hipStream_t)st));
     return FH3_OK;
 }
 
-extern "C" int fh3_hip_stream_sync(void *st) {
+extern "C" int fh3i_stream_sync(void *st) {
     FH3_HIPCALL(hipStreamSynchronize(st ? (hipStream_t)st : g.stream));
     return FH3_OK;
 }
 
-extern "C" int fh3_hip_copy_async(void *dst, const void *src, size_t bytes, void *st) {
+extern "C" int fh3i_copy_async(void *dst, const void *src, size_t bytes, void *st) {
     FH3_HIPCALL(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, st ? (hipStream_t)st : g.stream));
     return FH3_OK;
 }
 
-extern "C" int fh3_hip_event_create(void **ev) {
+extern "C" int fh3i_event_create(void **ev) {
     int rc = ensure_init();
     if (rc != FH3_OK) return rc;
     hipEvent_t e = nullptr;
@@ -192,23 +192,23 @@ extern "C" int fh3_hip_event_create(void **ev) {
     return FH3_OK;
 }
 
-extern "C" int fh3_hip_event_destroy(void *ev) {
+extern "C" int fh3i_event_destroy(void *ev) {
     if (!ev) return FH3_OK;
     FH3_HIPCALL(hipEventDestroy((hipEvent_t)ev));
     return FH3_OK;
 }
 
-extern "C" int fh3_hip_event_record(void *ev, void *st) {
+extern "C" int fh3i_event_record(void *ev, void *st) {
     FH3_HIPCALL(hipEventRecord((hipEvent_t)ev, st ? (hipStream_t)st : g.stream));
     return FH3_OK;
 }
 
-extern "C" int fh3_hip_stream_wait(void *st, void *ev) {
+extern "C" int fh3i_stream_wait(void *st, void *ev) {
     FH3_HIPCALL(hipStreamWaitEvent(st ? (hipStream_t)st : g.stream, (hipEvent_t)ev, 0));
     return FH3_OK;
 }
 
-extern "C" int fh3_hip_event_sync(void *ev) {
+extern "C" int fh3i_event_sync(void *ev) {
     FH3_HIPCALL(hipEventSynchronize((hipEvent_t)ev));
     return FH3_OK;
 }

@@ -14,18 +14,18 @@
 extern "C" {
 #endif
 
-int fh3_hip_set_error(int code, const char *msg);
-int fh3_hip_host_alloc(void **p, size_t bytes);   /* pinned, page aligned */
-int fh3_hip_host_free(void *p);
-int fh3_hip_stream_create(void **st);             /* default priority, non-blocking */
-int fh3_hip_stream_destroy(void *st);
-int fh3_hip_stream_sync(void *st);
-int fh3_hip_copy_async(void *dst, const void *src, size_t bytes, void *st);
-int fh3_hip_event_create(void **ev);
-int fh3_hip_event_destroy(void *ev);
-int fh3_hip_event_record(void *ev, void *st);
-int fh3_hip_stream_wait(void *st, void *ev);
-int fh3_hip_event_sync(void *ev);
+int fh3i_set_error(int code, const char *msg);
+int fh3i_host_alloc(void **p, size_t bytes);   /* pinned, page aligned */
+int fh3i_host_free(void *p);
+int fh3i_stream_create(void **st);             /* default priority, non-blocking */
+int fh3i_stream_destroy(void *st);
+int fh3i_stream_sync(void *st);
+int fh3i_copy_async(void *dst, const void *src, size_t bytes, void *st);
+int fh3i_event_create(void **ev);
+int fh3i_event_destroy(void *ev);
+int fh3i_event_record(void *ev, void *st);
+int fh3i_stream_wait(void *st, void *ev);
+int fh3i_event_sync(void *ev);
 
 #ifdef __cplusplus
 }

@@ -46,13 +46,13 @@ static int pack_fail(Fh3Pack *p, int code) {
 int fh3_pack_open(const char *path, Fh3Pack *p) {
     if (!path || !p) return FH3_ERR;
     memset(p, 0, sizeof(*p));
-    p->fd = open(path, O_RDONLY | O_CLOEXEC);
-    if (p->fd < 0) return FH3_E_IO;
+    p->file.fd = open(path, O_RDONLY | O_CLOEXEC);
+    if (p->file.fd < 0) return FH3_E_IO;
     struct stat st;
-    if (fstat(p->fd, &st) != 0) return pack_fail(p, FH3_E_IO);
-    p->file_size = (uint64_t)st.st_size;
-    if (p->file_size < sizeof(Fh3PackHeader)) return pack_fail(p, FH3_E_TRUNCATED);
-    if (read_at(p->fd, &p->header, sizeof(p->header), 0) != (int64_t)sizeof(p->header))
+    if (fstat(p->file.fd, &st) != 0) return pack_fail(p, FH3_E_IO);
+    p->file.size = (uint64_t)st.st_size;
+    if (p->file.size < sizeof(Fh3PackHeader)) return pack_fail(p, FH3_E_TRUNCATED);
+    if (read_at(p->file.fd, &p->header, sizeof(p->header), 0) != (int64_t)sizeof(p->header))
         return pack_fail(p, FH3_E_IO);
 
     const Fh3PackHeader *h = &p->header;
@@ -60,8 +60,8 @@ int fh3_pack_open(const char *path, Fh3Pack *p) {
     if (h->version != FH3_PACK_VERSION) return pack_fail(p, FH3_E_BAD_VERSION);
     if (h->layer_alignment != FH3_PACK_ALIGNMENT || h->num_layers == 0) return pack_fail(p, FH3_E_INVALID);
     const uint64_t stride = h->index_bytes / h->num_layers;
-    if (stride < DESC_HEAD_BYTES || h->index_offset > p->file_size ||
-        h->index_bytes > p->file_size - h->index_offset)
+    if (stride < DESC_HEAD_BYTES || h->index_offset > p->file.size ||
+        h->index_bytes > p->file.size - h->index_offset)
         return pack_fail(p, FH3_E_TRUNCATED);
 
     p->layers = (Fh3PackLayerDesc *)calloc(h->num_layers, sizeof(Fh3PackLayerDesc));
@@ -73,7 +73,7 @@ int fh3_pack_open(const char *path, Fh3Pack *p) {
     const uint32_t room = (uint32_t)((take - DESC_HEAD_BYTES) / sizeof(Fh3PackTensorDesc));
     for (uint32_t L = 0; L < h->num_layers; L++) {
         Fh3PackLayerDesc *ld = &p->layers[L];
-        if (read_at(p->fd, ld, take, h->index_offset + (uint64_t)L * stride) != (int64_t)take)
+        if (read_at(p->file.fd, ld, take, h->index_offset + (uint64_t)L * stride) != (int64_t)take)
             return pack_fail(p, FH3_E_IO);
         /* tensors beyond what the descriptor holds stay zero */
         uint32_t nt = ld->n_tensors < room ? ld->n_tensors : room;
@@ -83,10 +83,10 @@ int fh3_pack_open(const char *path, Fh3Pack *p) {
     p->num_layers = (int)h->num_layers;
 
     /* Map the file for callers that want views without a copy (optional). */
-    void *m = mmap(NULL, (size_t)p->file_size, PROT_READ, MAP_SHARED, p->fd, 0);
+    void *m = mmap(NULL, (size_t)p->file.size, PROT_READ, MAP_SHARED, p->file.fd, 0);
     if (m != MAP_FAILED) {
         p->mapped_base = (const uint8_t *)m;
-        p->mapped_size = (size_t)p->file_size;
+        p->mapped_size = (size_t)p->file.size;
     }
     return FH3_OK;
 }
@@ -98,8 +98,8 @@ void fh3_pack_close(Fh3Pack *p) {
     p->mapped_size = 0;
     free(p->layers);
     p->layers = NULL;
-    if (p->fd >= 0) close(p->fd);
-    p->fd = -1;
+    if (p->file.fd >= 0) close(p->file.fd);
+    p->file.fd = -1;
     p->num_layers = 0;
 }
 

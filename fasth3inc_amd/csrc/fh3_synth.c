@@ -53,7 +53,7 @@ static void box_muller(uint32_t a, uint32_t b, float *z0, float *z1) {
     *z1 = (float)(r * sin(th));
 }
 
-void fh3_rng_normal(uint64_t seed, uint64_t stream, float *out, size_t n) {
+void fh3_synth_rng_normal(uint64_t seed, uint64_t stream, float *out, size_t n) {
     if (!out || n == 0) return;
     const int64_t nb = (int64_t)((n + 3) / 4);
     #pragma omp parallel for schedule(static) if (nb > 4096)
@@ -248,12 +248,12 @@ int fh3_synth_q4k_weights(uint64_t seed, uint64_t stream, int64_t rows, int64_t 
 }
 
 void fh3_synth_x_normal(uint64_t seed, uint64_t stream, float *x, size_t count) {
-    fh3_rng_normal(seed, stream, x, count);
+    fh3_synth_rng_normal(seed, stream, x, count);
 }
 
 void fh3_synth_x_outliers(uint64_t seed, uint64_t stream, float *x, size_t count, float frac) {
     if (!x || count == 0) return;
-    fh3_rng_normal(seed, stream, x, count);
+    fh3_synth_rng_normal(seed, stream, x, count);
     const double thr = (double)frac * 4294967296.0;
     const int64_t nb = (int64_t)((count + 1) / 2);
     #pragma omp parallel for schedule(static) if (nb > 4096)

@@ -38,6 +38,72 @@ static size_t page_up(uint64_t n) { return (size_t)((n + PAGE - 1) & ~(uint64_t)
 
 static size_t run_bytes(const Fh3Trunk *t, int L) { return (size_t)t->pack.layers[L].size_bytes; }
 
+/* ------------------------------------------------------------------------- */
+/* per-trunk state beyond the reference's struct                            */
+/* ------------------------------------------------------------------------- */
+
+/* Fh3Trunk has the reference's layout, so what this library adds lives here,
+ * one record per open trunk, found by the trunk's address.  Created by
+ * fh3_trunk_open, freed by fh3_trunk_close. */
+typedef struct TrunkExt {
+    const Fh3Trunk *t;
+    struct TrunkExt *next;
+    bool sync_init;               /* t->mutex and conditions initialised */
+    int worker_errno;             /* errno of the last job's failed read, or 0 */
+    bool host_pinned;             /* pinned_layers / ring_buf from hipHostMalloc */
+    /* device extension (zero until fh3_trunk_attach_device) */
+    bool device;
+    int dpin;                     /* device-resident prefix layers */
+    size_t dev_slot_size;
+    void *compute_stream;         /* hipStream_t the matmuls run on */
+    void *upload_stream;          /* hipStream_t of the slot uploads */
+    uint8_t *dev_resident;        /* one allocation for the resident prefix */
+    uint8_t **dev_layers;         /* [dpin] pointers into dev_resident */
+    uint8_t *dev_slot[2];
+    int dev_layer[2];             /* layer uploaded (or enqueued) into slot s, or -1 */
+    bool dev_fresh[2];            /* upload not yet consumed by an acquire */
+    int dev_active;               /* -1 before the first streamed acquire */
+    void *ev_uploaded[2];         /* hipEvent_t */
+    void *ev_slot_free[2];
+    void *ev_host_read[2];
+    Fh3TrunkDevStats dev_stats;
+} TrunkExt;
+
+static pthread_mutex_t g_ext_mu = PTHREAD_MUTEX_INITIALIZER;
+static TrunkExt *g_ext;
+
+static TrunkExt *ext_of(const Fh3Trunk *t) {
+    pthread_mutex_lock(&g_ext_mu);
+    TrunkExt *x = g_ext;
+    while (x && x->t != t) x = x->next;
+    pthread_mutex_unlock(&g_ext_mu);
+    return x;
+}
+
+static TrunkExt *ext_new(const Fh3Trunk *t) {
+    TrunkExt *x = (TrunkExt *)calloc(1, sizeof(TrunkExt));
+    if (!x) return NULL;
+    x->t = t;
+    x->dev_layer[0] = x->dev_layer[1] = -1;
+    x->dev_active = -1;
+    pthread_mutex_lock(&g_ext_mu);
+    x->next = g_ext;
+    g_ext = x;
+    pthread_mutex_unlock(&g_ext_mu);
+    return x;
+}
+
+/* Unlink t's record (NULL when t has none: never opened, or closed). */
+static TrunkExt *ext_take(const Fh3Trunk *t) {
+    pthread_mutex_lock(&g_ext_mu);
+    TrunkExt **pp = &g_ext;
+    while (*pp && (*pp)->t != t) pp = &(*pp)->next;
+    TrunkExt *x = *pp;
+    if (x) *pp = x->next;
+    pthread_mutex_unlock(&g_ext_mu);
+    return x;
+}
+
 /* Read n bytes of the file at off (clamped to the file end) into dst.  The
  * O_DIRECT descriptor is used when dst, off and n are page aligned and dst is
  * ordinary memory; anything else goes through the buffered descriptor, and so
@@ -45,21 +111,22 @@ static size_t run_bytes(const Fh3Trunk *t, int L) { return (size_t)t->pack.layer
  * O_DIRECT, or a destination the kernel cannot pin for DMA: page-locked
  * memory mapped by the GPU driver gives EFAULT).  Returns the bytes read, or
  * FH3_E_IO with *err set to errno. */
-static int64_t read_run(Fh3Trunk *t, void *dst, size_t n, uint64_t off, int *err) {
-    const uint64_t size = t->pack.file_size;
+static int64_t read_run(Fh3Trunk *t, const TrunkExt *x, void *dst, size_t n, uint64_t off, int *err) {
+    const uint64_t size = t->pack.file.size;
     if (off >= size) return 0;
     if (n > size - off) n = (size_t)(size - off);
-    int fd = t->pack.fd;
-    if (t->direct && !t->host_pinned && (uintptr_t)dst % PAGE == 0 && off % PAGE == 0 && n % PAGE == 0)
-        fd = t->direct_fd;
+    int fd = t->pack.file.fd;
+    if (t->direct_file.is_direct && !x->host_pinned && (uintptr_t)dst % PAGE == 0 && off % PAGE == 0 &&
+        n % PAGE == 0)
+        fd = t->direct_file.fd;
     size_t got = 0;
     while (got < n) {
         ssize_t r = pread(fd, (uint8_t *)dst + got, n - got, (off_t)(off + got));
         if (r < 0) {
             if (errno == EINTR) continue;
-            if (fd == t->direct_fd) {
-                t->direct = false;
-                fd = t->pack.fd;
+            if (fd == t->direct_file.fd) {
+                t->direct_file.is_direct = false;
+                fd = t->pack.file.fd;
                 continue;
             }
             if (err) *err = errno;
@@ -105,22 +172,23 @@ static void plan_prefix(const Fh3Pack *p, uint64_t budget, int *n_out, size_t *s
 /* ------------------------------------------------------------------------- */
 
 static void *worker_main(void *arg) {
-    Fh3Trunk *t = (Fh3Trunk *)arg;
+    TrunkExt *x = (TrunkExt *)arg;
+    Fh3Trunk *t = (Fh3Trunk *)x->t;
     pthread_mutex_lock(&t->mutex);
     for (;;) {
         while (!t->worker_has_work && !t->worker_stop) pthread_cond_wait(&t->start_cond, &t->mutex);
         if (t->worker_stop) break;
         const int L = t->worker_req_layer, s = t->worker_req_slot;
-        void *host_read = t->device ? t->ev_host_read[s] : NULL;
+        void *host_read = x->device ? x->ev_host_read[s] : NULL;
         pthread_mutex_unlock(&t->mutex);
 
         int64_t got = FH3_ERR;
         int err = 0;
         double io = 0.0;
         /* an upload enqueued earlier may still be reading host slot s */
-        if (!host_read || fh3_hip_event_sync(host_read) == FH3_OK) {
+        if (!host_read || fh3i_event_sync(host_read) == FH3_OK) {
             const double t0 = now_s();
-            got = read_run(t, t->ring_buf[s], run_bytes(t, L), t->pack.layers[L].file_offset, &err);
+            got = read_run(t, x, t->ring_buf[s], run_bytes(t, L), t->pack.layers[L].file_offset, &err);
             io = now_s() - t0;
         } else {
             err = -1; /* the wait for the previous upload failed */
@@ -128,7 +196,7 @@ static void *worker_main(void *arg) {
 
         pthread_mutex_lock(&t->mutex);
         t->worker_read_bytes = got;
-        t->worker_errno = err;
+        x->worker_errno = err;
         t->prefetch_io_time = io;
         t->worker_has_work = false;
         t->worker_done = true;
@@ -160,9 +228,9 @@ static bool settle_job(Fh3Trunk *t) {
 /* open / close                                                              */
 /* ------------------------------------------------------------------------- */
 
-static void free_host(const Fh3Trunk *t, void *p) {
+static void free_host(const TrunkExt *x, void *p) {
     if (!p) return;
-    if (t->host_pinned) fh3_hip_host_free(p);
+    if (x->host_pinned) fh3i_host_free(p);
     else free(p);
 }
 
@@ -179,18 +247,22 @@ static int open_fail(Fh3Trunk *t, int code) {
 int fh3_trunk_open(const char *path, uint64_t budget_bytes, Fh3Trunk *t) {
     if (!path || !t) return FH3_ERR;
     memset(t, 0, sizeof(*t));
-    t->direct_fd = -1;
+    t->direct_file.fd = -1;
     int rc = fh3_pack_open(path, &t->pack);
-    if (rc != FH3_OK) return rc;
+    if (rc != FH3_OK) return rc;  /* the reader has released what it opened */
+    TrunkExt *x = ext_new(t);
+    if (!x) {
+        fh3_pack_close(&t->pack);
+        return FH3_E_NOMEM;
+    }
     t->num_layers = t->pack.num_layers;
     t->budget_bytes = budget_bytes;
     t->ring_layer[0] = t->ring_layer[1] = -1;
     t->active_slot = t->prefetch_layer = t->prefetch_slot = -1;
-    t->dev_layer[0] = t->dev_layer[1] = -1;
-    t->dev_active = -1;
 
-    t->direct_fd = open(path, O_RDONLY | O_CLOEXEC | O_DIRECT);
-    t->direct = t->direct_fd >= 0;
+    t->direct_file.fd = open(path, O_RDONLY | O_CLOEXEC | O_DIRECT);
+    t->direct_file.is_direct = t->direct_file.fd >= 0;
+    t->direct_file.size = t->pack.file.size;
 
     plan_prefix(&t->pack, budget_bytes, &t->npin, &t->slot_size);
 
@@ -200,7 +272,7 @@ int fh3_trunk_open(const char *path, uint64_t budget_bytes, Fh3Trunk *t) {
         for (int L = 0; L < t->npin; L++) {
             const size_t n = run_bytes(t, L);
             if (!(t->pinned_layers[L] = (uint8_t *)alloc_page_aligned(page_up(n)))) return open_fail(t, FH3_E_NOMEM);
-            if (read_run(t, t->pinned_layers[L], n, t->pack.layers[L].file_offset, NULL) != (int64_t)n)
+            if (read_run(t, x, t->pinned_layers[L], n, t->pack.layers[L].file_offset, NULL) != (int64_t)n)
                 return open_fail(t, FH3_E_IO);
         }
     }
@@ -210,37 +282,39 @@ int fh3_trunk_open(const char *path, uint64_t budget_bytes, Fh3Trunk *t) {
     pthread_mutex_init(&t->mutex, NULL);
     pthread_cond_init(&t->start_cond, NULL);
     pthread_cond_init(&t->done_cond, NULL);
-    t->sync_init = true;
-    if (pthread_create(&t->thread, NULL, worker_main, t) != 0) return open_fail(t, FH3_ERR);
+    x->sync_init = true;
+    if (pthread_create(&t->thread, NULL, worker_main, x) != 0) return open_fail(t, FH3_ERR);
     t->thread_created = true;
     return FH3_OK;
 }
 
-static void detach_device(Fh3Trunk *t) {
+static void detach_device(TrunkExt *x) {
     /* kernels and uploads may still read the buffers freed below */
-    if (t->upload_stream) fh3_hip_stream_sync(t->upload_stream);
-    if (t->device || t->upload_stream) fh3_hip_stream_sync(t->compute_stream);
+    if (x->upload_stream) fh3i_stream_sync(x->upload_stream);
+    if (x->device || x->upload_stream) fh3i_stream_sync(x->compute_stream);
     for (int s = 0; s < 2; s++) {
-        fh3_hip_free(t->dev_slot[s]);
-        fh3_hip_event_destroy(t->ev_uploaded[s]);
-        fh3_hip_event_destroy(t->ev_slot_free[s]);
-        fh3_hip_event_destroy(t->ev_host_read[s]);
-        t->dev_slot[s] = NULL;
-        t->ev_uploaded[s] = t->ev_slot_free[s] = t->ev_host_read[s] = NULL;
-        t->dev_layer[s] = -1;
+        fh3_hip_free(x->dev_slot[s]);
+        fh3i_event_destroy(x->ev_uploaded[s]);
+        fh3i_event_destroy(x->ev_slot_free[s]);
+        fh3i_event_destroy(x->ev_host_read[s]);
+        x->dev_slot[s] = NULL;
+        x->ev_uploaded[s] = x->ev_slot_free[s] = x->ev_host_read[s] = NULL;
+        x->dev_layer[s] = -1;
     }
-    fh3_hip_free(t->dev_resident);
-    t->dev_resident = NULL;
-    free(t->dev_layers);
-    t->dev_layers = NULL;
-    fh3_hip_stream_destroy(t->upload_stream);
-    t->upload_stream = NULL;
-    t->device = false;
-    t->dpin = 0;
+    fh3_hip_free(x->dev_resident);
+    x->dev_resident = NULL;
+    free(x->dev_layers);
+    x->dev_layers = NULL;
+    fh3i_stream_destroy(x->upload_stream);
+    x->upload_stream = NULL;
+    x->device = false;
+    x->dpin = 0;
 }
 
 void fh3_trunk_close(Fh3Trunk *t) {
     if (!t) return;
+    TrunkExt *x = ext_take(t);
+    if (!x) return;  /* not open */
     if (t->thread_created) {
         if (t->prefetch_in_flight) wait_job(t);
         pthread_mutex_lock(&t->mutex);
@@ -250,26 +324,27 @@ void fh3_trunk_close(Fh3Trunk *t) {
         pthread_join(t->thread, NULL);
         t->thread_created = false;
     }
-    if (t->sync_init) {
+    if (x->sync_init) {
         pthread_mutex_destroy(&t->mutex);
         pthread_cond_destroy(&t->start_cond);
         pthread_cond_destroy(&t->done_cond);
-        t->sync_init = false;
     }
-    detach_device(t);
+    detach_device(x);
     if (t->pinned_layers) {
-        for (int i = 0; i < t->npin; i++) free_host(t, t->pinned_layers[i]);
+        for (int i = 0; i < t->npin; i++) free_host(x, t->pinned_layers[i]);
         free(t->pinned_layers);
         t->pinned_layers = NULL;
     }
     t->npin = 0;
     for (int s = 0; s < 2; s++) {
-        free_host(t, t->ring_buf[s]);
+        free_host(x, t->ring_buf[s]);
         t->ring_buf[s] = NULL;
     }
-    if (t->direct_fd >= 0) close(t->direct_fd);
-    t->direct_fd = -1;
+    if (t->direct_file.fd >= 0) close(t->direct_file.fd);
+    t->direct_file.fd = -1;
+    t->direct_file.is_direct = false;
     fh3_pack_close(&t->pack);
+    free(x);
 }
 
 /* ------------------------------------------------------------------------- */
@@ -292,6 +367,7 @@ void fh3_trunk_prefetch(Fh3Trunk *t, int L) {
     t->prefetch_layer = L;
     t->prefetch_slot = idle;
     t->prefetch_in_flight = true;
+    t->prefetch_start_time = now_s();
     pthread_mutex_lock(&t->mutex);
     t->worker_req_layer = L;
     t->worker_req_slot = idle;
@@ -348,17 +424,17 @@ const Fh3Pack *fh3_trunk_pack(const Fh3Trunk *t) { return t ? &t->pack : NULL; }
 /* ------------------------------------------------------------------------- */
 
 /* Move the host prefix and ring slots to page-locked memory (all or nothing). */
-static int pin_host_copies(Fh3Trunk *t) {
+static int pin_host_copies(Fh3Trunk *t, TrunkExt *x) {
     const int n = t->npin + 2;
     void **fresh = (void **)calloc((size_t)n, sizeof(void *));
     if (!fresh) return FH3_E_NOMEM;
     int rc = FH3_OK;
     for (int i = 0; i < n && rc == FH3_OK; i++) {
         const size_t bytes = i < t->npin ? page_up(run_bytes(t, i)) : t->slot_size;
-        rc = fh3_hip_host_alloc(&fresh[i], bytes);
+        rc = fh3i_host_alloc(&fresh[i], bytes);
     }
     if (rc != FH3_OK) {
-        for (int i = 0; i < n; i++) fh3_hip_host_free(fresh[i]);
+        for (int i = 0; i < n; i++) fh3i_host_free(fresh[i]);
         free(fresh);
         return rc;
     }
@@ -369,23 +445,23 @@ static int pin_host_copies(Fh3Trunk *t) {
         *slot = (uint8_t *)fresh[i];
     }
     free(fresh);
-    t->host_pinned = true;
+    x->host_pinned = true;
     return FH3_OK;
 }
 
 /* Copy the device-resident prefix into HBM, reading from disk what the host
  * does not hold. */
-static int fill_resident(Fh3Trunk *t) {
+static int fill_resident(Fh3Trunk *t, TrunkExt *x) {
     uint64_t total = 0;
-    for (int L = 0; L < t->dpin; L++) total += page_up(run_bytes(t, L));
+    for (int L = 0; L < x->dpin; L++) total += page_up(run_bytes(t, L));
     if (!total) return FH3_OK;
-    t->dev_layers = (uint8_t **)calloc((size_t)t->dpin, sizeof(uint8_t *));
-    if (!t->dev_layers) return FH3_E_NOMEM;
-    int rc = fh3_hip_malloc((void **)&t->dev_resident, (size_t)total);
+    x->dev_layers = (uint8_t **)calloc((size_t)x->dpin, sizeof(uint8_t *));
+    if (!x->dev_layers) return FH3_E_NOMEM;
+    int rc = fh3_hip_malloc((void **)&x->dev_resident, (size_t)total);
     if (rc != FH3_OK) return rc;
     uint8_t *bounce = NULL;
     uint64_t at = 0;
-    for (int L = 0; L < t->dpin && rc == FH3_OK; L++) {
+    for (int L = 0; L < x->dpin && rc == FH3_OK; L++) {
         const size_t n = run_bytes(t, L);
         const uint8_t *src = L < t->npin ? t->pinned_layers[L] : NULL;
         if (!src) {
@@ -393,47 +469,48 @@ static int fill_resident(Fh3Trunk *t) {
                 rc = FH3_E_NOMEM;
                 break;
             }
-            if (read_run(t, bounce, n, t->pack.layers[L].file_offset, NULL) != (int64_t)n) {
-                rc = fh3_hip_set_error(FH3_E_IO, "fh3_trunk_attach_device: short read of a resident layer");
+            if (read_run(t, x, bounce, n, t->pack.layers[L].file_offset, NULL) != (int64_t)n) {
+                rc = fh3i_set_error(FH3_E_IO, "fh3_trunk_attach_device: short read of a resident layer");
                 break;
             }
             src = bounce;
         }
-        t->dev_layers[L] = t->dev_resident + at;
-        rc = fh3_hip_memcpy_htod(t->dev_layers[L], src, n);
+        x->dev_layers[L] = x->dev_resident + at;
+        rc = fh3_hip_memcpy_htod(x->dev_layers[L], src, n);
         at += page_up(n);
     }
     free(bounce);
-    t->dev_stats.resident_bytes = rc == FH3_OK ? total : 0;
+    x->dev_stats.resident_bytes = rc == FH3_OK ? total : 0;
     return rc;
 }
 
 int fh3_trunk_attach_device(Fh3Trunk *t, uint64_t dev_budget_bytes, void *compute_stream) {
-    if (!t || !t->thread_created) return fh3_hip_set_error(FH3_E_INVALID, "fh3_trunk_attach_device: trunk not open");
-    if (t->device) return fh3_hip_set_error(FH3_E_INVALID, "fh3_trunk_attach_device: already attached");
+    TrunkExt *x = t ? ext_of(t) : NULL;
+    if (!x || !t->thread_created) return fh3i_set_error(FH3_E_INVALID, "fh3_trunk_attach_device: trunk not open");
+    if (x->device) return fh3i_set_error(FH3_E_INVALID, "fh3_trunk_attach_device: already attached");
     if (t->prefetch_in_flight) {
         wait_job(t);
         settle_job(t);
     }
-    int rc = t->host_pinned ? FH3_OK : pin_host_copies(t);
+    int rc = x->host_pinned ? FH3_OK : pin_host_copies(t, x);
     if (rc != FH3_OK) return rc;
 
-    t->compute_stream = compute_stream;
-    plan_prefix(&t->pack, dev_budget_bytes, &t->dpin, &t->dev_slot_size);
-    rc = fill_resident(t);
-    if (rc == FH3_OK) rc = fh3_hip_stream_create(&t->upload_stream);
+    x->compute_stream = compute_stream;
+    plan_prefix(&t->pack, dev_budget_bytes, &x->dpin, &x->dev_slot_size);
+    rc = fill_resident(t, x);
+    if (rc == FH3_OK) rc = fh3i_stream_create(&x->upload_stream);
     for (int s = 0; s < 2 && rc == FH3_OK; s++) {
-        if (t->dpin < t->num_layers) rc = fh3_hip_malloc((void **)&t->dev_slot[s], t->dev_slot_size);
-        if (rc == FH3_OK) rc = fh3_hip_event_create(&t->ev_uploaded[s]);
-        if (rc == FH3_OK) rc = fh3_hip_event_create(&t->ev_slot_free[s]);
-        if (rc == FH3_OK) rc = fh3_hip_event_create(&t->ev_host_read[s]);
+        if (x->dpin < t->num_layers) rc = fh3_hip_malloc((void **)&x->dev_slot[s], x->dev_slot_size);
+        if (rc == FH3_OK) rc = fh3i_event_create(&x->ev_uploaded[s]);
+        if (rc == FH3_OK) rc = fh3i_event_create(&x->ev_slot_free[s]);
+        if (rc == FH3_OK) rc = fh3i_event_create(&x->ev_host_read[s]);
     }
     if (rc != FH3_OK) {
-        detach_device(t);
+        detach_device(x);
         return rc;
     }
     pthread_mutex_lock(&t->mutex);
-    t->device = true;
+    x->device = true;
     pthread_mutex_unlock(&t->mutex);
     return FH3_OK;
 }
@@ -441,85 +518,89 @@ int fh3_trunk_attach_device(Fh3Trunk *t, uint64_t dev_budget_bytes, void *comput
 /* Enqueue "device slot s <- src" behind the compute work already enqueued
  * (which may still read slot s).  host_slot >= 0 names the host ring slot
  * src lies in, so the worker will not overwrite it before the copy ends. */
-static int upload(Fh3Trunk *t, int s, int L, const uint8_t *src, int host_slot) {
+static int upload(const Fh3Trunk *t, TrunkExt *x, int s, int L, const uint8_t *src, int host_slot) {
     const size_t n = run_bytes(t, L);
-    t->dev_layer[s] = -1;
-    int rc = fh3_hip_event_record(t->ev_slot_free[s], t->compute_stream);
-    if (rc == FH3_OK) rc = fh3_hip_stream_wait(t->upload_stream, t->ev_slot_free[s]);
-    if (rc == FH3_OK) rc = fh3_hip_copy_async(t->dev_slot[s], src, n, t->upload_stream);
-    if (rc == FH3_OK) rc = fh3_hip_event_record(t->ev_uploaded[s], t->upload_stream);
-    if (rc == FH3_OK && host_slot >= 0) rc = fh3_hip_event_record(t->ev_host_read[host_slot], t->upload_stream);
+    x->dev_layer[s] = -1;
+    int rc = fh3i_event_record(x->ev_slot_free[s], x->compute_stream);
+    if (rc == FH3_OK) rc = fh3i_stream_wait(x->upload_stream, x->ev_slot_free[s]);
+    if (rc == FH3_OK) rc = fh3i_copy_async(x->dev_slot[s], src, n, x->upload_stream);
+    if (rc == FH3_OK) rc = fh3i_event_record(x->ev_uploaded[s], x->upload_stream);
+    if (rc == FH3_OK && host_slot >= 0) rc = fh3i_event_record(x->ev_host_read[host_slot], x->upload_stream);
     if (rc != FH3_OK) return rc;
-    t->dev_layer[s] = L;
-    t->dev_fresh[s] = true;
-    t->dev_stats.uploads++;
-    t->dev_stats.bytes_uploaded += n;
+    x->dev_layer[s] = L;
+    x->dev_fresh[s] = true;
+    x->dev_stats.uploads++;
+    x->dev_stats.bytes_uploaded += n;
     return FH3_OK;
 }
 
 void fh3_trunk_prefetch_dev(Fh3Trunk *t, int L) {
-    if (!t || !t->device || L < 0 || L >= t->num_layers || L < t->dpin) return;
-    if (t->dev_active >= 0 && t->dev_layer[t->dev_active] == L) return;
-    const int idle = t->dev_active == 0 ? 1 : 0;
-    if (t->dev_layer[idle] == L) return;
+    TrunkExt *x = t ? ext_of(t) : NULL;
+    if (!x || !x->device || L < 0 || L >= t->num_layers || L < x->dpin) return;
+    if (x->dev_active >= 0 && x->dev_layer[x->dev_active] == L) return;
+    const int idle = x->dev_active == 0 ? 1 : 0;
+    if (x->dev_layer[idle] == L) return;
     if (L < t->npin)
-        (void)upload(t, idle, L, t->pinned_layers[L], -1);
+        (void)upload(t, x, idle, L, t->pinned_layers[L], -1);
     else
         fh3_trunk_prefetch(t, L); /* read ahead; the acquire uploads it */
 }
 
 const uint8_t *fh3_trunk_acquire_dev(Fh3Trunk *t, int L) {
-    if (!t || !t->device || L < 0 || L >= t->num_layers) return NULL;
-    if (L < t->dpin) {
-        t->dev_stats.hits++;
-        return t->dev_layers[L];
+    TrunkExt *x = t ? ext_of(t) : NULL;
+    if (!x || !x->device || L < 0 || L >= t->num_layers) return NULL;
+    if (L < x->dpin) {
+        x->dev_stats.hits++;
+        return x->dev_layers[L];
     }
     int s = -1;
-    if (t->dev_active >= 0 && t->dev_layer[t->dev_active] == L)
-        s = t->dev_active;
-    else if (t->dev_layer[t->dev_active == 0 ? 1 : 0] == L)
-        s = t->dev_active == 0 ? 1 : 0;
+    if (x->dev_active >= 0 && x->dev_layer[x->dev_active] == L)
+        s = x->dev_active;
+    else if (x->dev_layer[x->dev_active == 0 ? 1 : 0] == L)
+        s = x->dev_active == 0 ? 1 : 0;
     if (s < 0) {
-        s = t->dev_active == 0 ? 1 : 0;
+        s = x->dev_active == 0 ? 1 : 0;
         const uint8_t *src = fh3_trunk_acquire(t, L); /* host prefix or a host ring slot */
         if (!src) {
             char msg[160];
             snprintf(msg, sizeof msg, "fh3_trunk_acquire_dev: layer %d: read %lld of %zu bytes (%s)", L,
                      (long long)t->worker_read_bytes, run_bytes(t, L),
-                     t->worker_errno > 0 ? strerror(t->worker_errno)
-                                         : t->worker_errno < 0 ? "waiting for an upload failed" : "short file");
-            fh3_hip_set_error(FH3_E_IO, msg);
+                     x->worker_errno > 0 ? strerror(x->worker_errno)
+                                         : x->worker_errno < 0 ? "waiting for an upload failed" : "short file");
+            fh3i_set_error(FH3_E_IO, msg);
             return NULL;
         }
-        if (upload(t, s, L, src, L < t->npin ? -1 : t->active_slot) != FH3_OK) return NULL;
+        if (upload(t, x, s, L, src, L < t->npin ? -1 : t->active_slot) != FH3_OK) return NULL;
     }
-    if (fh3_hip_stream_wait(t->compute_stream, t->ev_uploaded[s]) != FH3_OK) return NULL;
-    t->dev_active = s;
-    if (t->dev_fresh[s]) {
-        t->dev_fresh[s] = false;
-        t->dev_stats.misses++;
+    if (fh3i_stream_wait(x->compute_stream, x->ev_uploaded[s]) != FH3_OK) return NULL;
+    x->dev_active = s;
+    if (x->dev_fresh[s]) {
+        x->dev_fresh[s] = false;
+        x->dev_stats.misses++;
     } else {
-        t->dev_stats.hits++;
+        x->dev_stats.hits++;
     }
-    return t->dev_slot[s];
+    return x->dev_slot[s];
 }
 
 Fh3TrunkDevStats fh3_trunk_dev_stats(const Fh3Trunk *t) {
     Fh3TrunkDevStats z;
     memset(&z, 0, sizeof(z));
-    return t ? t->dev_stats : z;
+    const TrunkExt *x = t ? ext_of(t) : NULL;
+    return x ? x->dev_stats : z;
 }
 
 size_t fh3_trunk_struct_bytes(void) { return sizeof(Fh3Trunk); }
 
 int fh3_trunk_info(const Fh3Trunk *t, Fh3TrunkInfo *out) {
-    if (!t || !out) return FH3_ERR;
+    const TrunkExt *x = t ? ext_of(t) : NULL;
+    if (!x || !out) return FH3_ERR;
     memset(out, 0, sizeof(*out));
     out->num_layers = t->num_layers;
     out->npin = t->npin;
     out->slot_size = t->slot_size;
-    out->dpin = t->device ? t->dpin : 0;
-    out->dev_slot_size = t->dev_slot[0] ? t->dev_slot_size : 0;
+    out->dpin = x->device ? x->dpin : 0;
+    out->dev_slot_size = x->dev_slot[0] ? x->dev_slot_size : 0;
     return FH3_OK;
 }
 

@@ -95,8 +95,12 @@ class Fh3PackHeader(ctypes.Structure):
                 ("total_bytes", ctypes.c_uint64), ("reserved", ctypes.c_uint8 * 80)]
 
 
-class Fh3Pack(ctypes.Structure):
-    _fields_ = [("fd", ctypes.c_int), ("file_size", ctypes.c_uint64), ("header", Fh3PackHeader),
+class Fh3File(ctypes.Structure):         # reference src/io/fh3_portable_io.h:220-224
+    _fields_ = [("fd", ctypes.c_int), ("size", ctypes.c_uint64), ("is_direct", ctypes.c_bool)]
+
+
+class Fh3Pack(ctypes.Structure):         # reference src/io/fh3_pack.h:91-101
+    _fields_ = [("file", Fh3File), ("header", Fh3PackHeader),
                 ("num_layers", ctypes.c_int), ("layers", ctypes.POINTER(Fh3PackLayerDesc)),
                 ("mapped_base", ctypes.c_void_p), ("mapped_size", ctypes.c_size_t)]
 
@@ -137,7 +141,6 @@ SIGNATURES = {
     "fh3_matmul": (None, [ctypes.POINTER(Fh3W), _c_void_p, _c_void_p, _c_int, _c_void_p]),
     "fh3_matmul_scalar": (None, [ctypes.POINTER(Fh3W), _c_void_p, _c_void_p, _c_int, _c_void_p]),
     "fh3_matmul_avx2": (None, [ctypes.POINTER(Fh3W), _c_void_p, _c_void_p, _c_int, _c_void_p]),
-    "fh3_rng_normal": (None, [_c_u64, _c_u64, _c_void_p, _c_size]),
     "fh3_attention": (None, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int]),
     "fh3_vsa_attention": (None, [ctypes.POINTER(Fh3VsaCfg), _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                  ctypes.POINTER(Fh3Seq), _c_int, _c_int]),
@@ -190,6 +193,7 @@ SIGNATURES = {
     "fh3_hip_skinny_max": (_c_int, []),
     "fh3_hip_matmul_path": (_c_int, [_c_int, _c_i64]),
     # fh3_synth.h
+    "fh3_synth_rng_normal": (None, [_c_u64, _c_u64, _c_void_p, _c_size]),
     "fh3_philox4x32_10": (None, [_c_void_p, _c_void_p, _c_void_p]),
     "fh3_rng_uniform": (None, [_c_u64, _c_u64, _c_void_p, _c_size]),
     "fh3_q4k_quantize": (_c_int, [_c_void_p, _c_i64, _c_i64, _c_void_p]),
@@ -278,7 +282,7 @@ def matmul(w_bytes, K, N, x, bias=None, qtype=FH3_QUANT_Q4_K, variant="fh3_matmu
 
 def rng_normal(seed, stream, n):
     out = np.empty(n, dtype=np.float32)
-    lib().fh3_rng_normal(seed, stream, _p(out), n)
+    lib().fh3_synth_rng_normal(seed, stream, _p(out), n)
     return out
 
 

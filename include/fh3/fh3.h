@@ -152,12 +152,6 @@ void fh3_attention(const float *q, const float *k, const float *v, float *o, int
 void fh3_vsa_attention(const Fh3VsaCfg *c, const float *q, const float *k, const float *v, const float *gate,
                        float *o, const Fh3Seq *seq, int heads, int head_dim);
 
-/* Seeded N(0,1) fp32 generator: Philox4x32-10 (Salmon et al., SC'11) with
- * Box-Muller, one counter per 4 outputs.  Same stream layout as the
- * reference's fh3_rng_normal (src/model/fh3_sched.c:110-159); used to build
- * seeded synthetic inputs on the host. */
-void fh3_rng_normal(uint64_t seed, uint64_t stream, float *out, size_t n);
-
 #ifdef __cplusplus
 }
 #endif

@@ -22,7 +22,14 @@ extern "C" {
  * out = philox(ctr, key) with 10 rounds and Weyl key schedule. */
 void fh3_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
 
-/* Uniform (0,1) fp32 from the same counter stream layout as fh3_rng_normal:
+/* Seeded N(0,1) fp32 generator: Philox4x32-10 (Salmon et al., SC'11) with
+ * Box-Muller, one counter per 4 outputs; the same stream, bit for bit, as the
+ * reference's fh3_rng_normal (src/model/fh3_sched.c:110-159).  Exported under
+ * its own name so that it never interposes on the reference's symbol when
+ * both are linked into one program. */
+void fh3_synth_rng_normal(uint64_t seed, uint64_t stream, float *out, size_t n);
+
+/* Uniform (0,1) fp32 from the same counter stream layout as fh3_synth_rng_normal:
  * block b of stream s yields 4 values (word + 0.5) / 2^32. */
 void fh3_rng_uniform(uint64_t seed, uint64_t stream, float *out, size_t n);
 

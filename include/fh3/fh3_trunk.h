@@ -89,9 +89,25 @@ typedef struct Fh3PackHeader {
 } Fh3PackHeader;
 #pragma pack(pop)
 
-typedef struct Fh3Pack {
+/* The structs below have the reference's exact layout (its POSIX build), so
+ * that callers which hold them by value -- the reference CLI keeps an
+ * Fh3Trunk on its stack (src/cli/fh3_cli.c:750,963) -- link against this
+ * library unchanged:
+ *   Fh3File  src/io/fh3_portable_io.h:220-224
+ *   Fh3Pack  src/io/fh3_pack.h:91-101
+ *   Fh3Trunk src/io/fh3_trunk.h:26-68
+ * State the reference does not have (the device extension, page-locked host
+ * copies, the worker's errno) lives in a separate record that the library
+ * keys by the Fh3Trunk's address; Fh3Trunk itself only holds the reference's
+ * fields. */
+typedef struct Fh3File {
     int fd;
-    uint64_t file_size;
+    uint64_t size;
+    bool is_direct;
+} Fh3File;
+
+typedef struct Fh3Pack {
+    Fh3File file;
     Fh3PackHeader header;
     int num_layers;
     Fh3PackLayerDesc *layers;
@@ -133,53 +149,33 @@ typedef struct Fh3TrunkDevStats {
 
 typedef struct Fh3Trunk {
     Fh3Pack pack;
-    int direct_fd;                /* O_DIRECT descriptor, or buffered fallback */
-    bool direct;
+    Fh3File direct_file;          /* O_DIRECT descriptor (is_direct), else fd -1 */
     int num_layers;
     uint64_t budget_bytes;
     int npin;                     /* pinned prefix layers */
     size_t slot_size;             /* 4096-aligned ring slot size */
     uint8_t **pinned_layers;      /* [npin] host copies */
     uint8_t *ring_buf[2];         /* host ring slots */
-    bool ring_pinned;             /* ring slots come from hipHostMalloc */
     int ring_layer[2];            /* layer resident in each slot, or -1 */
     int active_slot;              /* -1 before the first acquire */
     int prefetch_layer;
     int prefetch_slot;
     bool prefetch_in_flight;
+    double prefetch_start_time;
     double prefetch_io_time;
     /* worker thread */
     pthread_t thread;
     pthread_mutex_t mutex;
     pthread_cond_t start_cond;
     pthread_cond_t done_cond;
-    bool sync_init;               /* mutex and conditions initialised */
-    bool thread_created;
     bool worker_has_work;
     bool worker_done;
+    bool thread_created;
     bool worker_stop;
     int worker_req_layer;
     int worker_req_slot;
     int64_t worker_read_bytes;
-    int worker_errno;             /* errno of the last job's failed read, or 0 */
     Fh3TrunkStats stats;
-    /* device extension (zero until fh3_trunk_attach_device) */
-    bool device;
-    bool host_pinned;             /* pinned_layers / ring_buf from hipHostMalloc */
-    int dpin;                     /* device-resident prefix layers */
-    size_t dev_slot_size;
-    void *compute_stream;         /* hipStream_t the matmuls run on */
-    void *upload_stream;          /* hipStream_t of the slot uploads */
-    uint8_t *dev_resident;        /* one allocation for the resident prefix */
-    uint8_t **dev_layers;         /* [dpin] pointers into dev_resident */
-    uint8_t *dev_slot[2];
-    int dev_layer[2];             /* layer uploaded (or enqueued) into slot s, or -1 */
-    bool dev_fresh[2];            /* upload not yet consumed by an acquire */
-    int dev_active;               /* -1 before the first streamed acquire */
-    void *ev_uploaded[2];         /* hipEvent_t */
-    void *ev_slot_free[2];
-    void *ev_host_read[2];
-    Fh3TrunkDevStats dev_stats;
 } Fh3Trunk;
 
 int fh3_trunk_open(const char *path, uint64_t budget_bytes, Fh3Trunk *t);

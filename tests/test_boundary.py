@@ -39,6 +39,36 @@ def test_library_exports_every_declared_symbol(fh3):
     assert not missing, missing
 
 
+def _dynsyms(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", lib], capture_output=True, text=True, check=True).stdout
+    return {l.split()[-1] for l in out.splitlines() if len(l.split()) == 3 and l.split()[1] in "TtWw"}
+
+
+LIB = os.path.join(ROOT, "fasth3inc_amd", "lib", "libfh3hip.so")
+
+
+def test_library_exports_exactly_the_headers():
+    """Nothing beyond the header API is exported: no kernel launcher
+    (fh3k_*), no internal helper (fh3i_*)."""
+    assert _dynsyms(LIB) == declared_functions()
+
+
+def test_library_calls_between_its_own_functions_are_not_interposable():
+    """The library's calls to its own exported functions (fh3_matmul ->
+    fh3_hip_matmul_dev, fh3_trunk_acquire_dev -> fh3_trunk_acquire, ...) bind
+    inside it (-Bsymbolic): no PLT slot names a symbol the library defines, so
+    a program that also defines fh3_trunk_acquire or fh3_pack_open (the
+    reference's fh3_core) cannot redirect them."""
+    rel = subprocess.run(["readelf", "-r", "--wide", LIB], capture_output=True, text=True, check=True).stdout
+    own = declared_functions()
+    slots = set()
+    for line in rel.splitlines():
+        parts = line.split()
+        if len(parts) >= 5 and "JUMP_SLOT" in parts[2]:
+            slots.add(parts[4].split("@")[0])
+    assert not (slots & own), sorted(slots & own)
+
+
 def test_binding_table_matches_headers(fh3):
     declared = declared_functions()
     extra = [n for n in fh3.SIGNATURES if n not in declared]

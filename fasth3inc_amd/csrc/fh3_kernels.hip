@@ -24,6 +24,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "fh3/fh3_hip.h"
 #include "fh3_kernels.h"
 
@@ -792,44 +794,54 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) vo
 }
 
 // ---------------------------------------------------------------------------
-// One- and two-token kernel (k_gemv8): integer MFMA on the raw 4-bit weights,
+// One- to four-token kernel (k_gemv8): integer MFMA on the raw 4-bit weights,
 // activations quantised inside the kernel (no preparation launch).
 //
 // Activations.  Each wavefront quantises the fp32 activations of its own
-// window of super-blocks: x_q = rne(x * 2^e), e per (token, wavefront) so that
-// max|x| * 2^e lies in [2^13, 2^14), split as x_q = 256*hi + lo with hi, lo
-// signed bytes (two int8 planes).  x * 2^e + (1.5*2^23 + 128) puts
+// window of C super-blocks once: x_q = rne(x * 2^e), e per (token, wavefront)
+// so that max|x| * 2^e lies in [2^13, 2^14) (subnormal windows included), split as x_q = 256*hi + lo with
+// hi, lo signed bytes (two int8 planes).  x * 2^e + (1.5*2^23 + 128) puts
 // x_q + 128 in the low 16 bits of the fp32 result (round to nearest even):
-// byte 1 is hi, byte 0 xor 0x80 is lo.  Non-finite activations in a window make
-// that token's output NaN.
+// byte 1 is hi, byte 0 xor 0x80 is lo, and the float minus the constant is x_q
+// itself, so the exact group sums X_g = sum of x_q over each 32-weight group
+// come from the same values (a DPP sum over the 8 lanes of a group).
+// Non-finite activations in a window make that token's outputs NaN.
 //
-// Products.  v_mfma_i32_16x16x64_i8, B = 16 weight rows: lane (row r = l%16,
-// k-block qd = l/16) holds 8 bytes of chunk qd of row r as 16 nibbles, the low
-// nibbles (group 2qd) in bytes 0-7 and the high ones (group 2qd+1) in bytes
-// 8-15.  A = "group slots": A row i = (token i/8, group i%8) is non-zero only in
-// the k-block of its group and only in the half that holds that group, so
-// output row i collects sum_k q_k x_k over exactly one group (32 weights) of
-// one token, exact in int32.  Four MFMAs (one per 8-byte piece of the chunks)
-// cover a super-block; each runs on both activation planes, and on B = ones
-// for the group sums of x_q (the dmin*m term).  Per super-block, lane l holds
-// groups 4*((l/16)&1)+v (v = 0..3) of token l/32 for row r:
-//   T = sum_v sc_v * (256*S_hi + S_lo),  Mt = sum_v m_v * (256*X_hi + X_lo)
+// LDS record of (super-block, token, plane): the 256 x_q bytes in k order,
+// then 32 zero bytes; then the 8 group sums (int32) of each (super-block,
+// token).  The records stay for the whole launch.
+//
+// Products.  v_mfma_i32_16x16x64_i8, B = 16 weight rows; lane (row r = l%16,
+// k-block qd = l/16) holds chunk qd of its row (groups 2qd and 2qd+1), and
+// one MFMA "piece" (part pt, half hs) takes from it the nibbles hs of bytes
+// 16pt..16pt+15: elements 16pt..16pt+15 of group 2qd+hs, as bytes.  A = group
+// slots: A row i = (token 2a + i/8, group g = i%8) is the 16 activation bytes
+// of its group's part in k-block g/2 for the piece with hs = g%2, zero
+// elsewhere (the lane reads the record's zero bytes), so output row i collects
+// sum_k q_k x_q over exactly one group of one token, exact in int32.  Four
+// pieces per plane cover a super-block; tile a holds tokens 2a, 2a+1.  Per
+// super-block, lane l holds groups 4*((l/16)&1)+v (v = 0..3) of token
+// 2a + l/32 for row r:
+//   T = sum_v sc_v * (256*S_hi + S_lo),  Mt = sum_v m_v * X_v
 // in 24-bit integer multiply-adds (|S| < 2^23, |T| < 2^31), then
 //   acc += d * T - dmin * Mt   in fp32,
 // the reference's w = (d*sc)*q - dmin*m with all integer parts exact.
 //
-// LDS record of (super-block, token, plane): 32 slots of 16 bytes, slot g*4+p
-// holding x_q[32g + 8p .. +7] in its low half (even g) or high half (odd g) and
-// zeros in the other half, then 4 zero slots for lanes whose A operand is zero;
-// every A operand is one ds_read_b128 with a compile-time offset.
-// Workgroup and window split as in k_skinny (NW wavefronts x C super-blocks
-// over 16 weight rows, last window moved inside the row, partial sums added in
-// wave order: deterministic).
+// Work.  A workgroup of NW wavefronts covers the K/256 super-blocks of 16
+// weight rows, wavefront w its window of C (the last window moved back inside
+// the row; super-blocks it shares with its neighbour count as padding, zero);
+// partial sums are added in wave order through LDS: deterministic.  The
+// workgroup walks row blocks blockIdx.x, +gridDim.x, ... and its weight ring
+// (one slot per super-block of the window) is refilled with the next block's
+// super-block as soon as a slot is consumed, so weight loads stay in flight
+// across blocks; the operands of each block's epilogue are loaded before that
+// block's refills (a load issued after them would make its wait cover them).
 // ---------------------------------------------------------------------------
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int G8_REC = 576;        // bytes of one (super-block, token, plane) record
-constexpr int G8_MAX_TOKENS = 2;
+constexpr int G8_REC = 288;        // x_q bytes of one (super-block, token, plane) + 32 zero bytes
+constexpr int G8_XS = 32;          // eight int32 group sums per (super-block, token)
+constexpr int G8_MAX_TOKENS = 4;
 
 // Maximum over the wavefront (DPP within rows of 16, then row broadcasts),
 // read from lane 63.
@@ -848,55 +860,75 @@ __device__ __forceinline__ float wave_max_f32(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 63));
 }
 
-template <int MT, int C, int RMAX = 4>
-__global__ __launch_bounds__(512) void k_gemv8(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int K,
-                                               const float *__restrict__ X, const float *__restrict__ bias,
-                                               float *__restrict__ Y, int M, int epi, const float *__restrict__ aux) {
-    constexpr int WAVE_LDS = C * MT * 2 * G8_REC;
-    constexpr int RING = C < RMAX ? C : RMAX;
+// Sum over each aligned group of 8 lanes (every lane of the group gets it).
+__device__ __forceinline__ float sum8_f32(float v) {
+    int iv = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(iv, iv, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+    iv = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(iv, iv, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+    iv = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(iv, iv, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    return v;
+}
+
+template <int MT, int C, int LB, int EPI>
+__global__ __launch_bounds__(LB) void k_gemv8(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int K,
+                                              const float *__restrict__ X, const float *__restrict__ bias,
+                                              float *__restrict__ Y, int M, const float *__restrict__ aux, int nblk) {
+    constexpr int TILES = MT > 1 ? MT / 2 : 1;
+    constexpr int WAVE_LDS = C * MT * (2 * G8_REC + G8_XS);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
     const int NW = blockDim.x >> 6;
+    float *red = reinterpret_cast<float *>(lds8 + NW * WAVE_LDS);  // [2][NW][TILES][64]
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, qd = lane >> 4;
     const int F = N >> 1;
-    const int o0 = epi == EPI_SWIGLU ? blockIdx.x * 8 : blockIdx.x * 16;
-    const int orow = epi == EPI_SWIGLU ? (r < 8 ? o0 + r : F + o0 + r - 8) : (o0 + r < N ? o0 + r : N - 1);
     const int nsb = K >> 8;
     const int own = wave * C;
     const int s0 = own < nsb - C ? own : nsb - C;
-    const uint8_t *wh = W + (size_t)orow * row_bytes + (size_t)s0 * 144;
-    const uint8_t *wc = wh + 16 + 32 * qd;
     uint8_t *my = lds8 + wave * WAVE_LDS;
+    uint8_t *xsb = my + C * MT * 2 * G8_REC;  // group sums [C][MT][8]
+    const int nit = (nblk - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    constexpr int ROWS = EPI == EPI_SWIGLU ? 8 : 16;  // output columns per block
 
-    // activations first: the quantisation waits only for them, not for the
-    // weights issued after them (loads of a wavefront complete in order)
+    // weight row of this lane in block it: rows o0..o0+15, or (SwiGLU) val
+    // rows o0..o0+7 and gate rows F+o0..F+o0+7
+    auto wptr = [&](int it) {
+        const int o0 = ((int)blockIdx.x + it * (int)gridDim.x) * ROWS;
+        int orow = EPI == EPI_SWIGLU ? (r < 8 ? o0 + r : F + o0 + r - 8) : o0 + r;
+        orow = orow < N ? orow : N - 1;
+        return W + (size_t)orow * row_bytes + (size_t)s0 * 144;
+    };
+
+    // activations of the window first: the quantisation waits only for them,
+    // not for the weights issued after them (loads complete in order)
     f32x4 xv[MT][C];
 #pragma unroll
-    for (int t = 0; t < MT; t++) {
+    for (int t = 0; t < MT; t++)
         if (t < M) {
             const f32x4 *xr = reinterpret_cast<const f32x4 *>(X + (size_t)t * K + (size_t)s0 * 256) + lane;
 #pragma unroll
             for (int i = 0; i < C; i++) xv[t][i] = xr[i * 64];
         }
-    }
-    u32x4 hv[RING], ca[RING], cb[RING];
+    u32x4 hv[C], ca[C], cb[C];
+    {
+        const uint8_t *wh = wptr(0), *wc = wh + 16 + 32 * qd;
 #pragma unroll
-    for (int s = 0; s < RING; s++) {
-        hv[s] = ld16(wh + s * 144);
-        ca[s] = ld16(wc + s * 144);
-        cb[s] = ld16(wc + s * 144 + 16);
+        for (int s = 0; s < C; s++) {
+            hv[s] = ld16(wh + s * 144);
+            ca[s] = ld16(wc + s * 144);
+            cb[s] = ld16(wc + s * 144 + 16);
+        }
     }
 
-    // quantise into the records: lane l holds k = 4l..4l+3 of a super-block,
-    // group l/8, piece (l%8)/2, bytes 4*(l&1).. of the slot half
-    const int pg = lane >> 3, pp = (lane & 7) >> 1;
-    const int wdat = (pg * 4 + pp) * 16 + (pg & 1) * 8 + 4 * (lane & 1);
-    const int wzero = (pg * 4 + pp) * 16 + (1 - (pg & 1)) * 8 + 4 * (lane & 1);
-    float inv[MT];
+    // quantise into the records: lane l holds k = 4l..4l+3 of a super-block
+    // (group l/8)
+    float inv[MT], inv2[MT];
 #pragma unroll
     for (int t = 0; t < MT; t++) {
         inv[t] = 0.f;
+        inv2[t] = 1.f;
         if (t < M) {
             float mx = 0.f, chk = 0.f;
 #pragma unroll
@@ -907,118 +939,175 @@ __global__ __launch_bounds__(512) void k_gemv8(const uint8_t *__restrict__ W, in
             }
             mx = wave_max_f32(mx);
             const bool bad = __builtin_amdgcn_ballot_w64(!__builtin_isfinite(chk)) != 0;
+            // 2^e = 2^e1 * 2^e2, both factors normal: e <= 162 for subnormal
+            // windows, e >= -114 (largest finite max)
             int e = 0;
             if (mx > 0.f) {
                 int E;
                 (void)frexpf(mx, &E);
                 e = 14 - E;
-                e = e > 126 ? 126 : (e < -126 ? -126 : e);
             }
-            const float sc = ldexpf(1.0f, e);
-            inv[t] = bad ? __builtin_nanf("") : ldexpf(1.0f, -e);
+            const int e1 = e < 126 ? e : 126, e2 = e - e1;
+            const float sc = ldexpf(1.0f, e1), sc2 = ldexpf(1.0f, e2);
+            inv[t] = bad ? __builtin_nanf("") : ldexpf(1.0f, -e1);
+            inv2[t] = ldexpf(1.0f, -e2);
 #pragma unroll
             for (int i = 0; i < C; i++) {
-                const f32x4 v = xv[t][i];
-                const uint32_t v0 = __builtin_bit_cast(uint32_t, __builtin_fmaf(v.x, sc, 12583040.0f));
-                const uint32_t v1 = __builtin_bit_cast(uint32_t, __builtin_fmaf(v.y, sc, 12583040.0f));
-                const uint32_t v2 = __builtin_bit_cast(uint32_t, __builtin_fmaf(v.z, sc, 12583040.0f));
-                const uint32_t v3 = __builtin_bit_cast(uint32_t, __builtin_fmaf(v.w, sc, 12583040.0f));
+                const f32x4 v = xv[t][i] * sc;  // exact
+                const float f0 = __builtin_fmaf(v.x, sc2, 12583040.0f), f1 = __builtin_fmaf(v.y, sc2, 12583040.0f);
+                const float f2 = __builtin_fmaf(v.z, sc2, 12583040.0f), f3 = __builtin_fmaf(v.w, sc2, 12583040.0f);
+                const uint32_t v0 = __builtin_bit_cast(uint32_t, f0), v1 = __builtin_bit_cast(uint32_t, f1);
+                const uint32_t v2 = __builtin_bit_cast(uint32_t, f2), v3 = __builtin_bit_cast(uint32_t, f3);
                 const uint32_t p01 = __builtin_amdgcn_perm(v1, v0, 0x05040100u);  // v0.b0 v0.b1 v1.b0 v1.b1
                 const uint32_t p23 = __builtin_amdgcn_perm(v3, v2, 0x05040100u);
-                const uint32_t hi4 = __builtin_amdgcn_perm(p23, p01, 0x07050301u);
-                const uint32_t lo4 = __builtin_amdgcn_perm(p23, p01, 0x06040200u) ^ 0x80808080u;
-                uint8_t *rec = my + ((i * MT + t) * 2) * G8_REC;
-                *reinterpret_cast<uint32_t *>(rec + wdat) = hi4;
-                *reinterpret_cast<uint32_t *>(rec + wzero) = 0u;
-                *reinterpret_cast<uint32_t *>(rec + G8_REC + wdat) = lo4;
-                *reinterpret_cast<uint32_t *>(rec + G8_REC + wzero) = 0u;
+                uint8_t *rec = my + (i * MT + t) * 2 * G8_REC + 4 * lane;
+                *reinterpret_cast<uint32_t *>(rec) = __builtin_amdgcn_perm(p23, p01, 0x07050301u);
+                *reinterpret_cast<uint32_t *>(rec + G8_REC) =
+                    __builtin_amdgcn_perm(p23, p01, 0x06040200u) ^ 0x80808080u;
+                // f - (1.5*2^23 + 128) = x_q exactly; a group's 32 of them sum to
+                // less than 2^19 in magnitude, exact in fp32
+                const float gs = sum8_f32(((f0 - 12583040.0f) + (f1 - 12583040.0f)) +
+                                          ((f2 - 12583040.0f) + (f3 - 12583040.0f)));
+                if ((lane & 7) == 0) reinterpret_cast<int *>(xsb)[(i * MT + t) * 8 + (lane >> 3)] = (int)gs;
+            }
+        } else {  // padding token of the tile: zero records (its outputs are not stored)
+#pragma unroll
+            for (int i = 0; i < C; i++) {
+                uint8_t *rec = my + (i * MT + t) * 2 * G8_REC + 4 * lane;
+                *reinterpret_cast<uint32_t *>(rec) = 0u;
+                *reinterpret_cast<uint32_t *>(rec + G8_REC) = 0u;
+                if (lane < 8) reinterpret_cast<int *>(xsb)[(i * MT + t) * 8 + lane] = 0;
             }
         }
     }
-    for (int z = lane; z < C * MT * 2 * 4; z += 64)
-        *reinterpret_cast<u32x4 *>(my + (z >> 2) * G8_REC + 512 + 16 * (z & 3)) = u32x4{0u, 0u, 0u, 0u};
-    // the records are read back by other lanes of the same wavefront only:
-    // LDS operations of a wavefront execute in order
+    for (int z = lane; z < C * MT * 2 * 2; z += 64)  // the 32 zero bytes after every record
+        *reinterpret_cast<u32x4 *>(my + (z >> 1) * G8_REC + 256 + 16 * (z & 1)) = u32x4{0u, 0u, 0u, 0u};
+    // the records are read back by lanes of the same wavefront only: LDS
+    // operations of a wavefront execute in order
     __builtin_amdgcn_wave_barrier();
 
-    // A operand of lane (row i = r: token r/8, group r%8; k-block qd): the
-    // group's slot when qd == g/2 and the token exists, else a zero slot
+    // A operand of lane (row r: token 2a + r/8, group g = r%8; k-block qd):
+    // its group's 16 bytes for the piece with hs == g%2 when qd == g/2, else
+    // the record's zero bytes
     const int g = r & 7;
-    const bool dl = qd == (g >> 1) && (r >> 3) < MT;
-    const uint8_t *aop = my + (dl ? (r >> 3) * 2 * G8_REC + g * 64 : 512);
+    int aoff[TILES][2];
+#pragma unroll
+    for (int a = 0; a < TILES; a++) {
+        const int tt = 2 * a + (r >> 3);
+        const bool in = qd == (g >> 1) && tt < MT;
+#pragma unroll
+        for (int hs = 0; hs < 2; hs++)
+            aoff[a][hs] = (in && (g & 1) == hs) ? tt * 2 * G8_REC + 32 * g : (tt < MT ? tt : 0) * 2 * G8_REC + 256;
+    }
+    // group sums of the lane's (token 2a + l/32, groups 4hh..4hh+3)
     const int hh = qd & 1;
     const uint32_t mA = hh ? 0x0F0F0F0Fu : 0x3F3F3F3Fu, mB = hh ? 0x30303030u : 0u;
-    const i32x4 ones = i32x4{0x01010101, 0x01010101, 0x01010101, 0x01010101};
-    float acc = 0.f;
-    __builtin_amdgcn_sched_barrier(0);
-
+    int xoff[TILES];
 #pragma unroll
-    for (int i = 0; i < C; i++) {
-        const int s = i % RING;
-        const u32x4 h = hv[s];
-        const uint32_t cw[8] = {ca[s].x, ca[s].y, ca[s].z, ca[s].w, cb[s].x, cb[s].y, cb[s].z, cb[s].w};
-        i32x4 cwh = {0, 0, 0, 0}, cwl = cwh, coh = cwh, col = cwh;
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            const uint32_t u0 = cw[2 * p], u1 = cw[2 * p + 1];
-            const i32x4 b = i32x4{(int)(u0 & 0x0F0F0F0Fu), (int)(u1 & 0x0F0F0F0Fu), (int)((u0 >> 4) & 0x0F0F0F0Fu),
-                                  (int)((u1 >> 4) & 0x0F0F0F0Fu)};
-            const int im = i * MT * 2 * G8_REC + 16 * p;
-            const i32x4 ah = *reinterpret_cast<const i32x4 *>(aop + im);
-            const i32x4 al = *reinterpret_cast<const i32x4 *>(aop + im + G8_REC);
-            cwh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, cwh, 0, 0, 0);
-            cwl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, cwl, 0, 0, 0);
-            coh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, ones, coh, 0, 0, 0);
-            col = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, ones, col, 0, 0, 0);
-        }
-        // 6-bit scales and mins of groups 4hh..4hh+3 of row r, one per byte
-        // (reference src/core/fh3_quant.c:168-177)
-        const uint32_t sc4 = ((hh ? h.w : h.y) & mA) | ((h.y >> 2) & mB);
-        const uint32_t m4 = ((hh ? (h.w >> 4) : h.z) & mA) | ((h.z >> 2) & mB);
-        const bool valid = s0 + i >= own;
-        const float d = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xFFFFu)) : 0.f;
-        const float dmin = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x >> 16)) : 0.f;
-        int T = 0, Mt = 0;
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const int S = (cwh[v] << 8) + cwl[v];
-            const int Xs = (coh[v] << 8) + col[v];
-            T += (int)((sc4 >> (8 * v)) & 63u) * ((S << 8) >> 8);    // 24-bit multiply-add
-            Mt += (int)((m4 >> (8 * v)) & 63u) * ((Xs << 8) >> 8);
-        }
-        acc = __builtin_fmaf(d, (float)T, __builtin_fmaf(-dmin, (float)Mt, acc));
-        if (i + RING < C) {
-            hv[s] = ld16(wh + (i + RING) * 144);
-            ca[s] = ld16(wc + (i + RING) * 144);
-            cb[s] = ld16(wc + (i + RING) * 144 + 16);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+    for (int a = 0; a < TILES; a++) {
+        const int tt = 2 * a + (lane >> 5);
+        xoff[a] = ((tt < MT ? tt : 0) * 8 + 4 * hh) * 4;
     }
+    // the output (token, column) this thread stores after each block, if any:
+    // lanes l and l+16 hold the two group halves of (token, row r)
+    const int st_a = (int)threadIdx.x >> 5, st_tl = ((int)threadIdx.x >> 4) & 1, st_rr = (int)threadIdx.x & 15;
+    const int st_t = 2 * st_a + st_tl, st_l = st_tl * 32 + st_rr;
+    const bool storer = (int)threadIdx.x < TILES * 32 && st_t < M && (EPI != EPI_SWIGLU || st_rr < 8);
 
-    // lanes l and l+16 hold the two group halves of (token l/32, row r)
-    float v = acc + __shfl_down(acc, 16);
-    v *= (lane >> 5) ? (MT > 1 ? inv[MT - 1] : 0.f) : inv[0];
-    float *red = reinterpret_cast<float *>(my);  // this wavefront's records are no longer read
-    red[lane] = v;
-    __syncthreads();
-    if (threadIdx.x < 32) {
-        const int tl = threadIdx.x >> 4, rr = threadIdx.x & 15;
-        const int l = tl * 32 + rr;
-        float sum = 0.f;
-        for (int w = 0; w < NW; w++) sum += reinterpret_cast<const float *>(lds8 + w * WAVE_LDS)[l];
-        if (epi == EPI_SWIGLU) {
-            if (rr < 8 && tl < M) {  // gate of column rr is row rr + 8 of this block
-                float sg = 0.f;
-                for (int w = 0; w < NW; w++) sg += reinterpret_cast<const float *>(lds8 + w * WAVE_LDS)[l + 8];
-                const int o = o0 + rr;
-                const float bv = bias ? bias[o] : 0.f, bg = bias ? bias[F + o] : 0.f;
-                Y[(size_t)tl * F + o] = (sum + bv) * silu_f32(sg + bg);
+    auto block = [&](int it, auto more_tag) {
+        constexpr bool MORE = decltype(more_tag)::value;
+        const int o0 = ((int)blockIdx.x + it * (int)gridDim.x) * ROWS;
+        const int st_o = o0 + st_rr;
+        const bool st_ok = storer && st_o < N;
+        float e_b = 0.f, e_bg = 0.f, e_aux = 0.f, e_y = 0.f;
+        if (st_ok) {
+            if (bias) {
+                e_b = bias[st_o];
+                if (EPI == EPI_SWIGLU) e_bg = bias[F + st_o];
             }
-        } else {
-            const int o = o0 + rr;
-            if (tl < M && o < N) epi_store(Y, aux, epi, (size_t)tl * N + o, sum + (bias ? bias[o] : 0.f));
+            if (EPI == EPI_GATE_RES) {
+                e_aux = aux[(size_t)st_t * N + st_o];
+                e_y = Y[(size_t)st_t * N + st_o];
+            }
         }
-    }
+        float acc[TILES];
+#pragma unroll
+        for (int a = 0; a < TILES; a++) acc[a] = 0.f;
+        const uint8_t *nh = wptr(MORE ? it + 1 : it), *nc = nh + 16 + 32 * qd;
+#pragma unroll
+        for (int i = 0; i < C; i++) {
+            const u32x4 h = hv[i];
+            i32x4 dh[TILES], dl[TILES];
+#pragma unroll
+            for (int a = 0; a < TILES; a++) dh[a] = dl[a] = i32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int pc = 0; pc < 4; pc++) {
+                const int pt = pc >> 1, hs = pc & 1;
+                const u32x4 src = pt ? cb[i] : ca[i];
+                const i32x4 b = hs ? i32x4{(int)((src.x >> 4) & 0x0F0F0F0Fu), (int)((src.y >> 4) & 0x0F0F0F0Fu),
+                                           (int)((src.z >> 4) & 0x0F0F0F0Fu), (int)((src.w >> 4) & 0x0F0F0F0Fu)}
+                                   : i32x4{(int)(src.x & 0x0F0F0F0Fu), (int)(src.y & 0x0F0F0F0Fu),
+                                           (int)(src.z & 0x0F0F0F0Fu), (int)(src.w & 0x0F0F0F0Fu)};
+#pragma unroll
+                for (int a = 0; a < TILES; a++) {
+                    const uint8_t *ap = my + i * MT * 2 * G8_REC + aoff[a][hs] + 16 * pt;
+                    const i32x4 ah = *reinterpret_cast<const i32x4 *>(ap);
+                    const i32x4 al = *reinterpret_cast<const i32x4 *>(ap + G8_REC);
+                    dh[a] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, dh[a], 0, 0, 0);
+                    dl[a] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, dl[a], 0, 0, 0);
+                }
+            }
+            // 6-bit scales and mins of groups 4hh..4hh+3 of row r, one per byte
+            // (reference src/core/fh3_quant.c:168-177)
+            const uint32_t sc4 = ((hh ? h.w : h.y) & mA) | ((h.y >> 2) & mB);
+            const uint32_t m4 = ((hh ? (h.w >> 4) : h.z) & mA) | ((h.z >> 2) & mB);
+            const bool valid = s0 + i >= own;
+            const float d = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xFFFFu)) : 0.f;
+            const float dmin = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x >> 16)) : 0.f;
+#pragma unroll
+            for (int a = 0; a < TILES; a++) {
+                const i32x4 xs = *reinterpret_cast<const i32x4 *>(xsb + i * MT * G8_XS + xoff[a]);
+                int T = 0, Mt = 0;
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int S = (dh[a][v] << 8) + dl[a][v];
+                    T += (int)((sc4 >> (8 * v)) & 63u) * ((S << 8) >> 8);  // 24-bit multiply-add
+                    Mt += (int)((m4 >> (8 * v)) & 63u) * ((xs[v] << 8) >> 8);
+                }
+                acc[a] = __builtin_fmaf(d, (float)T, __builtin_fmaf(-dmin, (float)Mt, acc[a]));
+            }
+            if (MORE) {
+                hv[i] = ld16(nh + i * 144);
+                ca[i] = ld16(nc + i * 144);
+                cb[i] = ld16(nc + i * 144 + 16);
+            }
+        }
+        float *rb = red + (it & 1) * NW * TILES * 64;  // alternate buffers: one barrier per block
+#pragma unroll
+        for (int a = 0; a < TILES; a++) {
+            const int tt = 2 * a + (lane >> 5);
+            float v = acc[a] + __shfl_down(acc[a], 16);
+            v = (v * inv[tt < MT ? tt : 0]) * inv2[tt < MT ? tt : 0];
+            rb[(wave * TILES + a) * 64 + lane] = v;
+        }
+        __syncthreads();
+        if (st_ok) {
+            float sum = 0.f;
+            for (int w = 0; w < NW; w++) sum += rb[(w * TILES + st_a) * 64 + st_l];
+            if (EPI == EPI_SWIGLU) {  // the gate of column st_rr is row st_rr + 8 of the block
+                float sg = 0.f;
+                for (int w = 0; w < NW; w++) sg += rb[(w * TILES + st_a) * 64 + st_l + 8];
+                Y[(size_t)st_t * F + st_o] = (sum + e_b) * silu_f32(sg + e_bg);
+            } else if (EPI == EPI_GATE_RES) {
+                Y[(size_t)st_t * N + st_o] = __builtin_fmaf(e_aux, sum + e_b, e_y);
+            } else {
+                Y[(size_t)st_t * N + st_o] = sum + e_b;
+            }
+        }
+    };
+    // every block but the last refills the ring with the next block's weights
+    for (int it = 0; it + 1 < nit; it++) block(it, std::integral_constant<bool, true>());
+    block(nit - 1, std::integral_constant<bool, false>());
 }
 
 // ---------------------------------------------------------------------------
@@ -1859,58 +1948,97 @@ extern "C" hipError_t fh3k_skinny(const void *W, int64_t row_bytes, int N, int K
 
 extern "C" int fh3k_skinny_max_tokens(void) { return 64; }
 
-// k_gemv8: same window split as k_skinny; LDS = NW * C * MT * 2 records.
-static const size_t kGemv8MaxLds = 80u << 10;  // two workgroups per CU
+// k_gemv8: C = ceil(nsb / 16) super-blocks per wavefront, NW = ceil(nsb / C)
+// <= 16 wavefronts (more, smaller windows measured faster at K = 5120: C = 2,
+// NW = 10 beats C = 4, NW = 5 and C = 5, NW = 4); grid = min(row blocks, CUs),
+// each workgroup walking its row blocks.  At 1024 threads a wavefront has 128
+// VGPRs: C <= 5 (one or two tokens) and C <= 3 (four) compile without spills,
+// so K <= 20480 and K <= 12288; longer rows take the other kernels.
+static const size_t kGemv8MaxLds = 160u << 10;  // one workgroup per CU
 
-static size_t gemv8_lds(int K, int mt, int &C, int &NW) {
-    skinny_split(K / 256, C, NW);
-    return C ? (size_t)NW * C * mt * 2 * G8_REC : 0;
+static int gemv8_mt(int M) { return M == 1 ? 1 : (M == 2 ? 2 : 4); }
+
+static size_t gemv8_lds(int K, int M, int &C, int &NW) {
+    const int nsb = K / 256, mt = gemv8_mt(M), tiles = mt > 1 ? mt / 2 : 1;
+    C = (nsb + 15) / 16;
+    NW = C ? (nsb + C - 1) / C : 0;
+    if (C < 1 || C > (mt == 4 ? 3 : 5)) return 0;
+    return (size_t)NW * C * mt * (2 * G8_REC + G8_XS) + 2 * (size_t)NW * tiles * 64 * sizeof(float);
 }
 
 extern "C" int fh3k_gemv8_max_tokens(void) { return G8_MAX_TOKENS; }
 
 extern "C" int fh3k_gemv8_fits(int K, int M) {
     int C, NW;
-    if (M < 1 || M > G8_MAX_TOKENS || K % 256) return 0;
+    if (M < 1 || M > G8_MAX_TOKENS || K < 256 || K % 256) return 0;
     const size_t lds = gemv8_lds(K, M, C, NW);
     return lds > 0 && lds <= kGemv8MaxLds;
 }
 
-template <int MT, int C>
+static int device_cus(void) {
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    }
+    return cus[dev];
+}
+
+template <int MT, int C, int EPI>
 static hipError_t launch_gemv8_c(const void *W, int64_t rb, int N, int K, const float *x, const float *bias,
-                                 float *y, int M, int NW, int epi, const float *aux, hipStream_t st) {
-    const size_t lds = (size_t)NW * C * MT * 2 * G8_REC;
-    hipLaunchKernelGGL((k_gemv8<MT, C>), dim3(row_blocks16(N, epi)), dim3(NW * 64), lds, st, (const uint8_t *)W, rb,
-                       N, K, x, bias, y, M, epi, aux);
+                                 float *y, int M, int NW, const float *aux, hipStream_t st) {
+    int C_, NW_;
+    const size_t lds = gemv8_lds(K, M, C_, NW_);
+    const int nblk = (int)row_blocks16(N, EPI);
+    const int cus = device_cus();
+    const int grid = nblk < cus ? nblk : cus;
+    hipLaunchKernelGGL((k_gemv8<MT, C, 1024, EPI>), dim3(grid), dim3(NW * 64), lds, st, (const uint8_t *)W, rb, N,
+                       K, x, bias, y, M, aux, nblk);
     return hipGetLastError();
+}
+
+template <int MT, int EPI>
+static hipError_t launch_gemv8_e(const void *W, int64_t rb, int N, int K, const float *x, const float *bias,
+                                 float *y, int M, const float *aux, hipStream_t st) {
+    int C, NW;
+    gemv8_lds(K, M, C, NW);
+    switch (C) {
+        case 1: return launch_gemv8_c<MT, 1, EPI>(W, rb, N, K, x, bias, y, M, NW, aux, st);
+        case 2: return launch_gemv8_c<MT, 2, EPI>(W, rb, N, K, x, bias, y, M, NW, aux, st);
+        case 3: return launch_gemv8_c<MT, 3, EPI>(W, rb, N, K, x, bias, y, M, NW, aux, st);
+        default: break;
+    }
+    if constexpr (MT <= 2) {
+        switch (C) {
+            case 4: return launch_gemv8_c<MT, 4, EPI>(W, rb, N, K, x, bias, y, M, NW, aux, st);
+            case 5: return launch_gemv8_c<MT, 5, EPI>(W, rb, N, K, x, bias, y, M, NW, aux, st);
+            default: break;
+        }
+    }
+    return hipErrorInvalidValue;
 }
 
 template <int MT>
 static hipError_t launch_gemv8(const void *W, int64_t rb, int N, int K, const float *x, const float *bias, float *y,
                                int M, int epi, const float *aux, hipStream_t st) {
-    int C, NW;
-    gemv8_lds(K, MT, C, NW);
-    switch (C) {
-        case 1: return launch_gemv8_c<MT, 1>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
-        case 2: return launch_gemv8_c<MT, 2>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
-        case 3: return launch_gemv8_c<MT, 3>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
-        case 4: return launch_gemv8_c<MT, 4>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
-        case 5: return launch_gemv8_c<MT, 5>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
-        case 6: return launch_gemv8_c<MT, 6>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
-        case 7: return launch_gemv8_c<MT, 7>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
-        case 8: return launch_gemv8_c<MT, 8>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
-        case 10: return launch_gemv8_c<MT, 10>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
-        case 13: return launch_gemv8_c<MT, 13>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
-        case 16: return launch_gemv8_c<MT, 16>(W, rb, N, K, x, bias, y, M, NW, epi, aux, st);
+    switch (epi) {
+        case EPI_NONE: return launch_gemv8_e<MT, EPI_NONE>(W, rb, N, K, x, bias, y, M, aux, st);
+        case EPI_GATE_RES: return launch_gemv8_e<MT, EPI_GATE_RES>(W, rb, N, K, x, bias, y, M, aux, st);
+        case EPI_SWIGLU: return launch_gemv8_e<MT, EPI_SWIGLU>(W, rb, N, K, x, bias, y, M, aux, st);
         default: return hipErrorInvalidValue;
     }
 }
 
 extern "C" hipError_t fh3k_gemv8_epi(const void *W, int64_t row_bytes, int N, int K, const float *x,
                                      const float *bias, float *y, int M, int epi, const float *aux, hipStream_t st) {
-    if (!fh3k_gemv8_fits(K, M) || (epi == EPI_SWIGLU && (N % 16))) return hipErrorInvalidValue;
-    return M == 1 ? launch_gemv8<1>(W, row_bytes, N, K, x, bias, y, M, epi, aux, st)
-                  : launch_gemv8<2>(W, row_bytes, N, K, x, bias, y, M, epi, aux, st);
+    if (!fh3k_gemv8_fits(K, M) || N < 1 || (epi == EPI_SWIGLU && (N % 16))) return hipErrorInvalidValue;
+    switch (gemv8_mt(M)) {
+        case 1: return launch_gemv8<1>(W, row_bytes, N, K, x, bias, y, M, epi, aux, st);
+        case 2: return launch_gemv8<2>(W, row_bytes, N, K, x, bias, y, M, epi, aux, st);
+        default: return launch_gemv8<4>(W, row_bytes, N, K, x, bias, y, M, epi, aux, st);
+    }
 }
 
 extern "C" hipError_t fh3k_gemv8(const void *W, int64_t row_bytes, int N, int K, const float *x, const float *bias,

@@ -10,6 +10,10 @@ Workloads (each launch sequence is preceded by one untimed warmup launch):
          than 256 MB of device copies so they come from HBM
   gemm   the DiT attention shapes (M=8192, K=5120, N in {15360,5120}):
          fh3_hip_matmul_prepared_dev -> k_gemm, and the activation prep k_xprep
+  mlp    the DiT MLP shapes (M=32768: up and gate K=5120 -> N=13824 with a
+         2-decade per-super-block scale spread, down K=13824 -> N=5120 on
+         SiLU-gated activations): fh3_hip_matmul_prepared_dev -> k_gemm, and
+         the activation prep k_xprep_r8
   copy   hipMemcpy device-to-device of 256 MiB: a copy of known size that
          calibrates FETCH_SIZE / WRITE_SIZE against the bytes moved
   attn   the DiT attention branch at n = 16384 tokens, 40 heads of 128
@@ -66,6 +70,22 @@ def gemm(reps):
         dy.close()
 
 
+def mlp(reps):
+    M = 32768
+    for K, N, xkind in ((5120, 13824, "normal"), (13824, 5120, "silu_gated")):
+        dx = F.DeviceBuffer.from_array(F.synth_x(xkind, 1, 400 + K, M, K))
+        prep = F.DeviceBuffer(F.prepared_bytes(M, K))
+        dw = F.DeviceBuffer.from_array(F.synth_q4k_weights(1, 300 + N + K, N, K, 0.02, 2.0))
+        dy = F.DeviceBuffer(M * N * 4)
+        for _ in range(reps + 1):
+            F.prepare_x_dev(dx, M, K, prep)
+            F.matmul_prepared_dev(dw, K, N, prep, dy, M)
+        F.synchronize()
+        print("mlp M=%d N=%d K=%d: %d launches" % (M, N, K, reps), flush=True)
+        for b in (dx, prep, dw, dy):
+            b.close()
+
+
 def copy(reps):
     n = 256 << 20
     a, b = F.DeviceBuffer(n), F.DeviceBuffer(n)
@@ -116,7 +136,7 @@ def vsa(reps, heads=56, hd=128, rot=96):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("workload", choices=("gemv", "gemm", "copy", "attn", "vsa", "all"))
+    ap.add_argument("workload", choices=("gemv", "gemm", "mlp", "copy", "attn", "vsa", "all"))
     ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args(argv)
     F.init(0)

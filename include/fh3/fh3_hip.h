@@ -57,7 +57,7 @@ int fh3_hip_dequant_dev(int type, const void *d_src, float *d_dst, int64_t rows,
  * value rounded once; F16 used as it is) into a library buffer of
  * out * in * 2 bytes, then multiplied with the same activation handling and
  * fp32 accumulation.  Work is enqueued on `stream` and the call
- * returns without synchronising.  For one or two tokens (FH3_HIP_PATH_GEMV8
+ * returns without synchronising.  For one to four tokens (FH3_HIP_PATH_GEMV8
  * below) activations are quantised to int16 inside the product kernel and
  * weights enter an integer MFMA exactly; otherwise activations are converted to
  * fp16 with a per-row power-of-two scale and weights enter an fp16 MFMA (exact
@@ -231,8 +231,9 @@ int fh3_hip_matmul_noalloc_dev(const Fh3W *w, const float *d_x, float *d_y, int 
                                const float *d_bias_or_null, void *stream);
 
 /* Kernel selection for fh3_hip_matmul_dev: FH3_HIP_PATH_AUTO picks
- *   - FH3_HIP_PATH_GEMV8 for n_tok <= 2 when its LDS fits (in <= 17920 for one
- *     token, in <= 8960 for two): activations quantised to int16 (two int8
+ *   - FH3_HIP_PATH_GEMV8 for n_tok <= 4 when its window fits (in <= 20480 for
+ *     one or two tokens, in <= 12288 for three or four): activations
+ *     quantised to int16 (two int8
  *     planes, one power-of-two scale per token and wavefront window) inside
  *     the kernel, integer MFMA on the raw 4-bit weights, no preparation launch
  *     and no workspace;

@@ -107,15 +107,18 @@ def test_row_bytes_matches_reference_build(fh3, ref):
 
 def test_matmul_path_selection(fh3):
     """Kernel family per shape (host-side decision, no GPU call): the int8
-    kernel takes one or two tokens while its LDS fits, the fp16 GEMV up to
-    64 tokens, the GEMM above; a forced path that cannot take a shape falls
-    back to the automatic choice."""
+    kernel takes one to four tokens while its window fits (K <= 20480 for one
+    or two tokens, K <= 12288 for three or four), the fp16 GEMV up to 64
+    tokens, the GEMM above; a forced path that cannot take a shape falls back
+    to the automatic choice."""
     F = fh3
     G8, SK, GM = F.PATH_GEMV8, F.PATH_SKINNY, F.PATH_GEMM
     assert F.matmul_path(1, 5120) == G8 and F.matmul_path(2, 5120) == G8
-    assert F.matmul_path(1, 17920) == G8 and F.matmul_path(1, 18176) == SK
-    assert F.matmul_path(2, 8960) == G8 and F.matmul_path(2, 9216) == SK
-    assert F.matmul_path(3, 5120) == SK and F.matmul_path(64, 5120) == SK
+    assert F.matmul_path(1, 20480) == G8 and F.matmul_path(1, 20736) == SK
+    assert F.matmul_path(2, 20480) == G8 and F.matmul_path(2, 20736) == SK
+    assert F.matmul_path(3, 12288) == G8 and F.matmul_path(4, 12288) == G8 and F.matmul_path(4, 12544) == SK
+    assert F.matmul_path(4, 13824) == SK and F.matmul_path(1, 200) == SK
+    assert F.matmul_path(5, 5120) == SK and F.matmul_path(64, 5120) == SK
     assert F.matmul_path(65, 5120) == GM
     MD = F.PATH_MIDM
     assert F.matmul_path(17, 8192) == MD and F.matmul_path(64, 13824) == MD
@@ -126,7 +129,7 @@ def test_matmul_path_selection(fh3):
         F.set_path(SK)
         assert F.matmul_path(1, 5120) == SK
         F.set_path(G8)
-        assert F.matmul_path(1, 5120) == G8 and F.matmul_path(3, 5120) == SK
+        assert F.matmul_path(4, 5120) == G8 and F.matmul_path(5, 5120) == SK
         F.set_path(GM)
         assert F.matmul_path(1, 5120) == GM
     finally:

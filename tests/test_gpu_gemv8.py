@@ -1,4 +1,4 @@
-"""GPU parity of the one- and two-token kernel (FH3_HIP_PATH_GEMV8: int16
+"""GPU parity of the one- to four-token kernel (FH3_HIP_PATH_GEMV8: int16
 activations quantised inside the kernel, integer MFMA on the raw Q4_K
 nibbles) against the CPU oracle, through the C-ABI.
 
@@ -55,6 +55,13 @@ CASES = [
     (2, 8960, 48, "outliers", 0.0, False),
     (1, 13824, 96, "silu_gated", 0.0, False),
     (1, 17920, 64, "normal", 0.0, True),
+    (2, 20480, 80, "outliers", 2.0, True),
+    (3, 256, 16, "normal", 0.0, True),
+    (3, 5120, 333, "outliers", 2.0, False),
+    (4, 768, 100, "silu_gated", 0.0, True),
+    (4, 5120, 5120, "normal", 0.0, False),
+    (3, 8192, 200, "silu_gated", 2.0, True),
+    (4, 12288, 64, "outliers", 0.0, False),
 ]
 
 
@@ -90,7 +97,7 @@ def test_gemv8_more_accurate_than_fp16_paths(gpu, oracle):
 def test_gemv8_deterministic(gpu):
     K, N = 5120, 300
     raw = gpu.synth_q4k_weights(9, 1, N, K, 0.02, 0.0)
-    for M in (1, 2):
+    for M in (1, 2, 3, 4):
         x = gpu.synth_x("outliers", 9, 2, M, K)
         a = _dev(gpu, raw, K, N, x)
         b = _dev(gpu, raw, K, N, x)
@@ -104,13 +111,15 @@ def test_gemv8_extreme_magnitudes_and_zero_rows(gpu, oracle):
     K, N = 1024, 128
     raw = H.random_q4k(rng, N, K)
     bias = rng.standard_normal(N).astype(np.float32)
-    x = rng.standard_normal((2, K)).astype(np.float32)
+    x = rng.standard_normal((4, K)).astype(np.float32)
     x[0] *= 1e-30
     x[1] *= 1e4
-    y = _dev(gpu, raw, K, N, x)
-    yo = H.oracle_matmul(oracle, raw, K, N, x)
-    for r in (0, 1):
-        assert H.rel_fro(y[r], yo[r]) <= TOL
+    x[3] *= 1e-38    # subnormal inputs
+    for M in (2, 4):
+        y = _dev(gpu, raw, K, N, x[:M])
+        yo = H.oracle_matmul(oracle, raw, K, N, x[:M])
+        for r in range(M):
+            assert H.rel_fro(y[r], yo[r]) <= TOL, (M, r)
     # a single large value among small ones in one window
     x = (rng.standard_normal((1, K)) * 1e-3).astype(np.float32)
     x[0, 77] = 50.0
@@ -124,11 +133,12 @@ def test_gemv8_non_finite_activations_give_nan(gpu, bad):
     rng = np.random.default_rng(4)
     K, N = 2048, 64
     raw = H.random_q4k(rng, N, K)
-    x = rng.standard_normal((2, K)).astype(np.float32)
+    x = rng.standard_normal((4, K)).astype(np.float32)
     x[1, 1500] = bad
-    y = _dev(gpu, raw, K, N, x)
-    assert np.isfinite(y[0]).all()
-    assert np.isnan(y[1]).all()
+    for M in (2, 3, 4):
+        y = _dev(gpu, raw, K, N, x[:M])
+        assert np.isnan(y[1]).all()
+        assert np.isfinite(np.delete(y, 1, axis=0)).all()
 
 
 def test_gemv8_prepared_two_stage_equals_one_call(gpu):
@@ -136,7 +146,7 @@ def test_gemv8_prepared_two_stage_equals_one_call(gpu):
     K, N = 4096, 200
     raw = F.synth_q4k_weights(21, 1, N, K, 0.02, 0.0)
     dw = F.DeviceBuffer.from_array(raw)
-    for M in (1, 2):
+    for M in (1, 2, 3, 4):
         x = F.synth_x("normal", 21, 2, M, K)
         dx = F.DeviceBuffer.from_array(x)
         prep = F.DeviceBuffer(F.prepared_bytes(M, K))

@@ -38,12 +38,13 @@ MALL_BYTES = 256 << 20   # Infinity Cache
 METRIC = "Q4_K GEMM TFLOP/s + GEMV weight GB/s (% roofline); DiT block linear ms"
 
 # HBM bytes per launch, measured with rocprofv3 --pmc FETCH_SIZE and --pmc
-# WRITE_SIZE (one run each) over `python3 -m fasth3inc_amd.profile_kernels all
-# --reps 5`, scaled by 2.0 and 1.0: a 256 MiB device-to-device copy reads
-# FETCH_SIZE = 128 MiB and WRITE_SIZE = 256 MiB.  Summaries:
-# profiles/k_skinny_gemv_m1-16_k5120.md, profiles/k_gemm_dit_attention_m8192_k5120.md,
-# profiles/hbm_counters_copy_256MiB.md.  Re-measure when the kernels change.
-TRAFFIC_GEMV_MEAN = 33604030        # mean over the six GEMV shapes (algorithmic mean 32899072)
+# WRITE_SIZE (one run each) over `python3 -m fasth3inc_amd.profile_kernels gemv
+# --reps 5` (and `gemm` for the GEMM figures), scaled by 2.0 and 1.0: a 256 MiB
+# device-to-device copy reads FETCH_SIZE = 128 MiB and WRITE_SIZE = 256 MiB.
+# Summaries: profiles/gemv_k_gemv8_k_skinny_m1-16_k5120.md,
+# profiles/k_gemm_dit_attention_m8192_k5120.md, profiles/hbm_counters_copy_256MiB.md.
+# Re-measure when the kernels change.
+TRAFFIC_GEMV_MEAN = 33611999        # mean over the six GEMV shapes (algorithmic mean 32899072)
 TRAFFIC_GEMM = {"attn_qkv": 2324594574, "attn_out": 703181960}
 
 
@@ -326,7 +327,23 @@ def dit_vsa(ev, st, heads=56, hd=128, rot=96, sparsity=0.8):
 # ---------------------------------------------------------------------------
 # CPU baseline
 # ---------------------------------------------------------------------------
-def cpu_baseline(cases, iters=3):
+def _time_cpu(H, lib, fn, raw, K, N, x, iters):
+    H.matmul_with(lib, fn, raw, K, N, x)  # warmup
+    ts = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        H.matmul_with(lib, fn, raw, K, N, x)
+        ts.append(time.perf_counter() - t0)
+    return min(ts), sum(ts) / len(ts)
+
+
+def cpu_baseline(cases, iters=5, big_iters=2, sample_rows=256):
+    """fh3's CPU matmul on this host's cores, as benchmarks/bench_matmul.c
+    times it (1 warmup, then best and mean of N runs): the six GEMV shapes and
+    the 64 x 4096 x 4096 product with N = 5; the DiT GEMMs (M = 8192 and
+    32768) on the first `sample_rows` token rows of the same seeded
+    activations with N = 2, reported as GFLOP/s and the full-M time that rate
+    implies."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import helpers as H
     ref = H.load_ref()
@@ -336,16 +353,34 @@ def cpu_baseline(cases, iters=3):
         lib, fn, kind = H.load_oracle(), "fh3_oracle_matmul", "port"
     total_w, total_t, per = 0, 0.0, []
     for c in cases:
-        H.matmul_with(lib, fn, c.raw, c.K, c.N, c.x)  # warmup
-        best = 1e30
-        for _ in range(iters):
-            t0 = time.perf_counter()
-            H.matmul_with(lib, fn, c.raw, c.K, c.N, c.x)
-            best = min(best, time.perf_counter() - t0)
+        best, mean = _time_cpu(H, lib, fn, c.raw, c.K, c.N, c.x, iters)
         total_w += c.wbytes
         total_t += best
-        per.append({"M": c.M, "N": c.N, "K": c.K, "ms": round(best * 1e3, 3),
+        per.append({"M": c.M, "N": c.N, "K": c.K, "ms": round(best * 1e3, 3), "mean_ms": round(mean * 1e3, 3),
                     "weight_GBps": round(c.wbytes / best / 1e9, 2)})
+    configs = {}
+    # single 64 x 4096 x 4096 product (same seeds as the GPU leg)
+    raw = F.synth_q4k_weights(0, 300 + 4096 + 4096, 4096, 4096, 0.02, 0.0)
+    x = F.synth_x("normal", 0, 400 + 4096, 64, 4096)
+    best, mean = _time_cpu(H, lib, fn, raw, 4096, 4096, x, iters)
+    flop = 2.0 * 64 * 4096 * 4096
+    configs["single_64x4096x4096"] = {"ms": round(best * 1e3, 3), "mean_ms": round(mean * 1e3, 3),
+                                      "GFLOPs": round(flop / best / 1e9, 1),
+                                      "weight_GBps": round(q4k_bytes(4096, 4096) / best / 1e9, 2)}
+    # DiT GEMMs on sampled token rows (same weights and activation seeds as the GPU leg)
+    big = [("attn_qkv", 8192, 5120, 15360, "outliers", 0.0), ("attn_out", 8192, 5120, 5120, "outliers", 0.0),
+           ("mlp_up_gate", 32768, 5120, 13824, "normal", 2.0), ("mlp_down", 32768, 13824, 5120, "silu_gated", 2.0)]
+    rows = []
+    for name, M, K, N, xk, spread in big:
+        raw = F.synth_q4k_weights(1, 300 + N + K, N, K, 0.02, spread)
+        x = F.synth_x(xk, 1, 400 + K, sample_rows, K)
+        best, mean = _time_cpu(H, lib, fn, raw, K, N, x, big_iters)
+        flop = 2.0 * sample_rows * N * K
+        rows.append({"name": name, "M": M, "K": K, "N": N, "sample_rows": sample_rows,
+                     "sample_ms": round(best * 1e3, 2), "sample_mean_ms": round(mean * 1e3, 2),
+                     "GFLOPs": round(flop / best / 1e9, 1), "full_M_ms": round(best * M / sample_rows * 1e3, 1)})
+        del raw, x
+    configs["dit_gemms_sampled"] = rows
     threads = H.load_oracle().fh3_oracle_threads()
     cpu = ""
     try:
@@ -356,10 +391,13 @@ def cpu_baseline(cases, iters=3):
     except OSError:
         pass
     return {"value": round(total_w / total_t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": "the six GEMV shapes once each (best of %d after 1 warmup), one weight copy, "
-                      "fh3_matmul with OMP_NUM_THREADS=%d; nproc=%d; %s; built -O3 -mavx2 -mfma -mf16c "
-                      "-ffp-contract=off -fopenmp (no -march=native)" % (iters, threads, os.cpu_count(), cpu),
-            "per_case": per}
+            "sample": "the six GEMV shapes (best of %d after 1 warmup; value = their weight bytes over the sum "
+                      "of best times), one weight copy; fh3_matmul from the reference's own fh3_quant.c and "
+                      "fh3_ops.c with OMP_NUM_THREADS=%d; nproc=%d; %s; built -O3 -mavx2 -mfma -mf16c "
+                      "-ffp-contract=off -fopenmp (no -march=native). configs: the 64x4096x4096 product "
+                      "(best of %d) and the DiT GEMMs on %d sampled token rows (best of %d)"
+                      % (iters, threads, os.cpu_count(), cpu, iters, sample_rows, big_iters),
+            "per_case": per, "configs": configs}
 
 
 # ---------------------------------------------------------------------------

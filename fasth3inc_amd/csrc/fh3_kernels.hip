@@ -414,28 +414,30 @@ __global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ X, int 
     }
 }
 
-// Large-M preparation: 8 consecutive rows per 1024-thread workgroup.  Thread
-// (r = lane % 8, cc = tid / 8) owns row t0 + r and its 8-float chunks
-// c = cc + 128 i (V per thread, K <= 1024 V).  The 8 lanes that share a chunk
-// hold the 8 rows' 16-byte slots of fragment c/2, lane half c%2: one aligned
-// 128-byte line per store, where k_xprep's rows each write 16 of a line's 128
+// Large-M preparation: RW = 8 (or 4) consecutive rows per 1024-thread
+// workgroup.  Thread (r = lane % RW, cc = tid / RW) owns row t0 + r and its
+// 8-float chunks c = cc + (1024/RW) i (V per thread, K <= 8 V (1024/RW)).  The
+// 8 lanes that share a chunk hold the 8 rows' 16-byte slots of fragment c/2,
+// lane half c%2: one aligned 128-byte line per store (64 bytes with RW = 4, used
+// at K > 8192, where 8 rows would need 112 VGPRs of activations per thread), where k_xprep's rows each write 16 of a line's 128
 // bytes and rely on the L2 to merge them (measured at M = 32768: 5.2 against
 // 3.5 TB/s at K = 5120, 4.4 against 3.0 at K = 13824).  Same scale rule and
 // rounding as k_xprep; with NORM the row sum of squares is added in another
 // order (lanes, then the 16 wavefronts).
-template <int V, bool NORM>
+template <int V, bool NORM, int RW = 8>
 __global__ __launch_bounds__(1024) void k_xprep_r8(const float *__restrict__ X, int M, int K,
                                                    half8 *__restrict__ X16, float *__restrict__ xs_inv, RowNorm nm) {
-    __shared__ float s_red[16][8];
+    constexpr int CPI = 1024 / RW;  // chunks per pass
+    __shared__ float s_red[16][RW];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r = lane & 7, cc = tid >> 3;
-    const int t = (int)blockIdx.x * 8 + r;
+    const int r = lane & (RW - 1), cc = tid / RW;
+    const int t = (int)blockIdx.x * RW + r;
     const int n8 = K / 8;
     const f32x4 *xr = reinterpret_cast<const f32x4 *>(X + (size_t)t * K);
     f32x4 v[V][2];
 #pragma unroll
     for (int i = 0; i < V; i++) {
-        const int c = cc + 128 * i;
+        const int c = cc + CPI * i;
         v[i][0] = v[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (t < M && c < n8) {
             v[i][0] = xr[2 * c];
@@ -450,10 +452,9 @@ __global__ __launch_bounds__(1024) void k_xprep_r8(const float *__restrict__ X, 
             for (int j = 0; j < 2; j++)
                 ss = __builtin_fmaf(v[i][j].w, v[i][j].w, __builtin_fmaf(v[i][j].z, v[i][j].z,
                      __builtin_fmaf(v[i][j].y, v[i][j].y, __builtin_fmaf(v[i][j].x, v[i][j].x, ss))));
-        ss += __shfl_xor(ss, 8);
-        ss += __shfl_xor(ss, 16);
-        ss += __shfl_xor(ss, 32);
-        if (lane < 8) s_red[wave][lane] = ss;
+#pragma unroll
+        for (int o = RW; o < 64; o <<= 1) ss += __shfl_xor(ss, o);
+        if (lane < RW) s_red[wave][lane] = ss;
         __syncthreads();
         ss = s_red[0][r];
 #pragma unroll
@@ -466,7 +467,7 @@ __global__ __launch_bounds__(1024) void k_xprep_r8(const float *__restrict__ X, 
             const f32x4 *sc4 = reinterpret_cast<const f32x4 *>(nm.scale ? nm.scale + (size_t)t * K : nullptr);
 #pragma unroll
             for (int i = 0; i < V; i++) {
-                const int c = cc + 128 * i;
+                const int c = cc + CPI * i;
                 if (c < n8) {
 #pragma unroll
                     for (int j = 0; j < 2; j++) {
@@ -489,10 +490,9 @@ __global__ __launch_bounds__(1024) void k_xprep_r8(const float *__restrict__ X, 
 #pragma unroll
         for (int j = 0; j < 2; j++)
             mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i][j].x), fabsf(v[i][j].y)), fmaxf(fabsf(v[i][j].z), fabsf(v[i][j].w))));
-    mx = fmaxf(mx, __shfl_xor(mx, 8));
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    if (lane < 8) s_red[wave][lane] = mx;
+#pragma unroll
+    for (int o = RW; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane < RW) s_red[wave][lane] = mx;
     __syncthreads();
     mx = s_red[0][r];
 #pragma unroll
@@ -509,7 +509,7 @@ __global__ __launch_bounds__(1024) void k_xprep_r8(const float *__restrict__ X, 
     half8 *dst = X16 + (size_t)(t >> 5) * (K / 16) * 64 + (t & 31);
 #pragma unroll
     for (int i = 0; i < V; i++) {
-        const int c = cc + 128 * i;
+        const int c = cc + CPI * i;
         if (c < n8) {
             const f32x4 a = v[i][0], b = v[i][1];
             const half8 h = {(_Float16)(a.x * s), (_Float16)(a.y * s), (_Float16)(a.z * s), (_Float16)(a.w * s),
@@ -1816,8 +1816,9 @@ extern "C" hipError_t fh3k_xprep_norm(const float *x, int M, int K, int Mpad, vo
                 hipLaunchKernelGGL((k_xprep_r8<4, false>), g8, b8, 0, st, x, M, K, (half8 *)x16, xs_inv, nm);
             else if (K <= 8192)
                 hipLaunchKernelGGL((k_xprep_r8<8, false>), g8, b8, 0, st, x, M, K, (half8 *)x16, xs_inv, nm);
-            else
-                hipLaunchKernelGGL((k_xprep_r8<14, false>), g8, b8, 0, st, x, M, K, (half8 *)x16, xs_inv, nm);
+            else  // 4 rows per workgroup: 7 chunks of 8 per thread fit the 128 VGPRs of 1024 threads
+                hipLaunchKernelGGL((k_xprep_r8<7, false, 4>), dim3((unsigned)(Mpad / 4)), b8, 0, st, x, M, K,
+                                   (half8 *)x16, xs_inv, nm);
         }
         return hipGetLastError();
     }

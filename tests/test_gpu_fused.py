@@ -88,7 +88,7 @@ def test_prepare_norm_then_product(gpu, oracle, M, modulate):
     assert err <= TOL
 
 
-@pytest.mark.parametrize("M", [1, 2, 7, 300])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 7, 300])
 @pytest.mark.parametrize("prepared", [False, True])
 def test_gate_residual_epilogue(gpu, oracle, M, prepared):
     F = gpu
@@ -115,7 +115,7 @@ def test_gate_residual_epilogue(gpu, oracle, M, prepared):
     assert H.rel_fro(out, href) <= TOL
 
 
-@pytest.mark.parametrize("M", [1, 2, 7, 300])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 7, 300])
 @pytest.mark.parametrize("use_bias", [False, True])
 def test_swiglu_epilogue(gpu, oracle, M, use_bias):
     F = gpu

@@ -62,6 +62,11 @@ CASES = [
     (4, 5120, 5120, "normal", 0.0, False),
     (3, 8192, 200, "silu_gated", 2.0, True),
     (4, 12288, 64, "outliers", 0.0, False),
+    # blocks left after the full rounds split into parts (N = 4103: one block of
+    # 7 rows over 16 workgroups; N = 9000: 51 blocks in quarters)
+    (2, 3072, 4103, "normal", 1.0, True),
+    (4, 2048, 9000, "outliers", 0.0, True),
+    (1, 5120, 17408, "silu_gated", 0.0, False),
 ]
 
 

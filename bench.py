@@ -478,7 +478,7 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK, 4), "traffic": TRAFFIC_GEMV_MEAN,
                 "traffic_over_algorithmic": round(TRAFFIC_GEMV_MEAN / (k_bytes / len(gemv)), 3),
-                "kernel": "k_gemv8 (n_tok<=4) and k_skinny (n_tok<=64), fh3_hip_matmul_prepared_dev",
+                "kernel": "k_gemv8 (n_tok<=4) and k_sweep (n_tok<=16), fh3_hip_matmul_prepared_dev",
                 "note": "algorithmic bytes N*K/256*144 + 4MK + 4MN per launch over the mean launch time "
                         "(graph of 64 back-to-back launches, rotating weight copies) of the six shapes"}
 

@@ -126,11 +126,17 @@ int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 // A forced path that cannot take the shape falls back to the automatic choice.
 int choose_path(int n_tok, int64_t in) {
     const bool g8 = in <= fh3k_max_in() && fh3k_gemv8_fits((int)in, n_tok);
+    const bool sw = in <= fh3k_max_in() && fh3k_sweep_fits((int)in, n_tok);
     if (g.path == FH3_HIP_PATH_GEMV8 && g8) return FH3_HIP_PATH_GEMV8;
+    if (g.path == FH3_HIP_PATH_SWEEP && sw) return FH3_HIP_PATH_SWEEP;
     if (g.path == FH3_HIP_PATH_SKINNY && n_tok <= fh3k_skinny_max_tokens()) return FH3_HIP_PATH_SKINNY;
     if (g.path == FH3_HIP_PATH_MIDM && n_tok <= fh3k_midm_max_tokens()) return FH3_HIP_PATH_MIDM;
     if (g.path == FH3_HIP_PATH_GEMM) return FH3_HIP_PATH_GEMM;
     if (g8) return FH3_HIP_PATH_GEMV8;
+    // up to 16 tokens on rows of at most 6144: the persistent kernel that keeps
+    // the activations in registers (measured 10-20 % faster than k_skinny at
+    // M = 16, K = 5120)
+    if (sw) return FH3_HIP_PATH_SWEEP;
     // long rows (K >= 8192) with 17..64 tokens: the split-K kernel reads the
     // activations once per 128 rows instead of once per 16 (measured 25-45 %
     // faster at K = 13824; slower than k_skinny at K <= 5120)
@@ -369,7 +375,7 @@ extern "C" int fh3_hip_graph_destroy(void *graph_exec) {
 }
 
 extern "C" int fh3_hip_set_path(int path) {
-    if (path < FH3_HIP_PATH_AUTO || path > FH3_HIP_PATH_MIDM)
+    if (path < FH3_HIP_PATH_AUTO || path > FH3_HIP_PATH_SWEEP)
         return set_err(FH3_E_INVALID, "fh3_hip_set_path: bad path %d", path);
     g.path = path;
     return FH3_OK;
@@ -412,27 +418,50 @@ static int check_weights(const Fh3W *w, const char *fn) {
 }
 
 // Prepared-activation layout: fragments of Mpad = round_up(n_tok, 256) rows,
-// then Mpad fp32 inverse scales at a 256-byte aligned offset.
+// then Mpad fp32 inverse scales at a 256-byte aligned offset, then (up to 16
+// tokens) the fp32 sums of each 32-value group, [n_tok][in / 32], at the next
+// 256-byte boundary: the FH3_HIP_PATH_SWEEP kernel's offsets.
 static int64_t prep_rows(int n_tok) { return round_up(n_tok, fh3k_gemm_row_pad()); }
 static size_t prep_scale_offset(int n_tok, int64_t in) {
     return (size_t)round_up(prep_rows(n_tok) * in * 2, 256);
 }
+static size_t prep_sum_offset(int n_tok, int64_t in) {
+    return (size_t)round_up((int64_t)(prep_scale_offset(n_tok, in) + (size_t)prep_rows(n_tok) * sizeof(float)), 256);
+}
 
 extern "C" size_t fh3_hip_prepared_bytes(int n_tok, int64_t in) {
     if (n_tok <= 0 || in <= 0) return 0;
-    return prep_scale_offset(n_tok, in) + (size_t)prep_rows(n_tok) * sizeof(float);
+    const size_t sums = n_tok <= fh3k_sweep_max_tokens() ? (size_t)n_tok * (size_t)(in / 32) * sizeof(float) : 0;
+    return prep_sum_offset(n_tok, in) + sums;
+}
+
+// the prepared form's parts
+static const float *prep_scales(const void *prep, int n_tok, int64_t in) {
+    return (const float *)((const char *)prep + prep_scale_offset(n_tok, in));
+}
+static const float *prep_sums(const void *prep, int n_tok, int64_t in) {
+    return (const float *)((const char *)prep + prep_sum_offset(n_tok, in));
 }
 
 static int prepare(const float *d_x, int n_tok, int64_t in, void *d_prep, int64_t rows, hipStream_t st) {
-    if (choose_path(n_tok, in) == FH3_HIP_PATH_GEMV8) {
+    const int path = choose_path(n_tok, in);
+    if (path == FH3_HIP_PATH_GEMV8) {
         // that kernel quantises fp32 activations itself: the prepared form is x
         FH3_HIPCALL(hipMemcpyAsync(d_prep, d_x, (size_t)n_tok * (size_t)in * sizeof(float),
                                    hipMemcpyDeviceToDevice, st));
         return FH3_OK;
     }
-    float *xs_inv = (float *)((char *)d_prep + prep_scale_offset(n_tok, in));
-    FH3_HIPCALL(fh3k_xprep(d_x, n_tok, (int)in, (int)rows, d_prep, xs_inv, st));
+    float *xs_inv = (float *)prep_scales(d_prep, n_tok, in);
+    float *xsum = path == FH3_HIP_PATH_SWEEP ? (float *)prep_sums(d_prep, n_tok, in) : nullptr;
+    FH3_HIPCALL(fh3k_xprep(d_x, n_tok, (int)in, (int)rows, d_prep, xs_inv, xsum, st));
     return FH3_OK;
+}
+
+// prepared rows the kernels of `path` read
+static int64_t kernel_rows(int path, int n_tok) {
+    return path == FH3_HIP_PATH_SKINNY || path == FH3_HIP_PATH_MIDM || path == FH3_HIP_PATH_SWEEP
+               ? round_up(n_tok, 32)
+               : prep_rows(n_tok);
 }
 
 extern "C" int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, void *d_prep, void *stream) {
@@ -489,19 +518,22 @@ static int product(const Fh3W *w, const void *prep, int n_tok, const float *bias
             // the prepared form is then a copy of x: make the fragments here
             int rc = grow(g.ws2, fh3_hip_prepared_bytes(n_tok, w->in), st);
             if (rc != FH3_OK) return rc;
-            float *xs = (float *)((char *)g.ws2.p + prep_scale_offset(n_tok, w->in));
-            FH3_HIPCALL(fh3k_xprep((const float *)prep, n_tok, (int)w->in, (int)prep_rows(n_tok), g.ws2.p, xs, st));
+            float *xs = (float *)prep_scales(g.ws2.p, n_tok, w->in);
+            FH3_HIPCALL(fh3k_xprep((const float *)prep, n_tok, (int)w->in, (int)prep_rows(n_tok), g.ws2.p, xs,
+                                   nullptr, st));
             return product16(w, g.ws2.p, xs, n_tok, bias, d_y, st);
         }
-        return product16(w, prep, (const float *)((const char *)prep + prep_scale_offset(n_tok, w->in)), n_tok,
-                         bias, d_y, st);
+        return product16(w, prep, prep_scales(prep, n_tok, w->in), n_tok, bias, d_y, st);
     }
     const int K = (int)w->in, N = (int)w->out;
     const int64_t row_bytes = (int64_t)fh3_row_bytes(w->type, w->in);
-    const float *xs_inv = (const float *)((const char *)prep + prep_scale_offset(n_tok, w->in));
+    const float *xs_inv = prep_scales(prep, n_tok, w->in);
     const int path = choose_path(n_tok, w->in);
     if (path == FH3_HIP_PATH_GEMV8) {
         FH3_HIPCALL(fh3k_gemv8_epi(w->data, row_bytes, N, K, (const float *)prep, bias, d_y, n_tok, epi, aux, st));
+    } else if (path == FH3_HIP_PATH_SWEEP) {
+        FH3_HIPCALL(fh3k_sweep_epi(w->data, row_bytes, N, K, prep, xs_inv, prep_sums(prep, n_tok, w->in), bias, d_y,
+                                   n_tok, epi, aux, st));
     } else if (path == FH3_HIP_PATH_SKINNY) {
         FH3_HIPCALL(fh3k_skinny_epi(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, epi, aux, st));
     } else {
@@ -565,8 +597,8 @@ static int matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok, co
         const int64_t rows = path16(n_tok) == FH3_HIP_PATH_SKINNY ? round_up(n_tok, 32) : prep_rows(n_tok);
         rc = grow(g.ws, fh3_hip_prepared_bytes(n_tok, w->in), st);
         if (rc != FH3_OK) return rc;
-        float *xs = (float *)((char *)g.ws.p + prep_scale_offset(n_tok, w->in));
-        FH3_HIPCALL(fh3k_xprep(d_x, n_tok, (int)w->in, (int)rows, g.ws.p, xs, st));
+        float *xs = (float *)prep_scales(g.ws.p, n_tok, w->in);
+        FH3_HIPCALL(fh3k_xprep(d_x, n_tok, (int)w->in, (int)rows, g.ws.p, xs, nullptr, st));
         return product16(w, g.ws.p, xs, n_tok, d_bias_or_null, d_y, st);
     }
     const int path = choose_path(n_tok, w->in);
@@ -577,8 +609,7 @@ static int matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok, co
     }
     std::lock_guard<std::recursive_mutex> lk(g.mu);
     // the small- and middle-M kernels only read round_up(n_tok, 32) prepared rows
-    const int64_t rows =
-        path == FH3_HIP_PATH_SKINNY || path == FH3_HIP_PATH_MIDM ? round_up(n_tok, 32) : prep_rows(n_tok);
+    const int64_t rows = kernel_rows(path, n_tok);
     rc = grow(g.ws, fh3_hip_prepared_bytes(n_tok, w->in), st);
     if (rc != FH3_OK) return rc;
     rc = prepare(d_x, n_tok, w->in, g.ws.p, rows, st);
@@ -651,8 +682,7 @@ extern "C" int fh3_hip_matmul_noalloc_dev(const Fh3W *w, const float *d_x, float
                                       "holds %zu (use fh3_hip_matmul_dev)", fn, n_tok, (long long)w->in,
                        (long long)w->out, need, (size_t)FH3_HIP_NOALLOC_SCRATCH_BYTES);
     uint8_t *scr = (uint8_t *)g_scratch[g.device];
-    const int64_t rows =
-        path == FH3_HIP_PATH_SKINNY || path == FH3_HIP_PATH_MIDM ? round_up(n_tok, 32) : prep_rows(n_tok);
+    const int64_t rows = kernel_rows(path, n_tok);
     rc = prepare(d_x, n_tok, w->in, scr, rows, st);
     if (rc != FH3_OK) return rc;
     return product(w, scr, n_tok, d_bias_or_null, d_y, st, FH3_EPI_NONE, nullptr, (float *)(scr + part_off));
@@ -674,9 +704,10 @@ extern "C" int fh3_hip_prepare_x_norm_dev(const float *d_x, int n_tok, int64_t i
         FH3_HIPCALL(fh3k_rownorm_f32(d_x, n_tok, (int)in, (float *)d_prep, d_norm_w, eps, d_shift, d_scale, st));
         return FH3_OK;
     }
-    float *xs_inv = (float *)((char *)d_prep + prep_scale_offset(n_tok, in));
+    float *xs_inv = (float *)prep_scales(d_prep, n_tok, in);
+    float *xsum = choose_path(n_tok, in) == FH3_HIP_PATH_SWEEP ? (float *)prep_sums(d_prep, n_tok, in) : nullptr;
     FH3_HIPCALL(fh3k_xprep_norm(d_x, n_tok, (int)in, (int)prep_rows(n_tok), d_prep, xs_inv, d_norm_w, eps, d_shift,
-                                d_scale, st));
+                                d_scale, xsum, st));
     return FH3_OK;
 }
 

@@ -27,8 +27,10 @@ hipError_t fh3k_dequant_f32(int type, const void *src, int64_t row_bytes, int64_
                             float *dst, hipStream_t st);
 
 // x[M][K] fp32 -> x16 fragments (Mpad x K fp16, Mpad % 32 == 0, rows >= M zero)
-// and xs_inv[Mpad] (per-row inverse power-of-two scale).
-hipError_t fh3k_xprep(const float *x, int M, int K, int Mpad, void *x16, float *xs_inv,
+// and xs_inv[Mpad] (per-row inverse power-of-two scale); with xsum set (K <=
+// 32768), also xsum[M][K/32]: the sum of each 32-value group of the row's
+// fp16 values (the offsets of fh3k_sweep_epi).
+hipError_t fh3k_xprep(const float *x, int M, int K, int Mpad, void *x16, float *xs_inv, float *xsum,
                       hipStream_t st);
 
 // y = x * W^T (+bias) from prepared fragments, n_tok <= fh3k_skinny_max_tokens();
@@ -62,6 +64,14 @@ hipError_t fh3k_skinny_epi(const void *W, int64_t row_bytes, int N, int K, const
                            const float *bias, float *y, int M, int epi, const float *aux, hipStream_t st);
 hipError_t fh3k_gemv8_epi(const void *W, int64_t row_bytes, int N, int K, const float *x, const float *bias,
                           float *y, int M, int epi, const float *aux, hipStream_t st);
+// Up to fh3k_sweep_max_tokens() tokens from prepared fragments and their group
+// sums (fh3k_xprep with xsum), when fh3k_sweep_fits(K, M); persistent, the
+// activations held in registers.
+hipError_t fh3k_sweep_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16, const float *xs_inv,
+                          const float *xsum, const float *bias, float *y, int M, int epi, const float *aux,
+                          hipStream_t st);
+int fh3k_sweep_fits(int K, int M);
+int fh3k_sweep_max_tokens(void);
 // Large M.  When the 256 x 128 tiles alone would not fill the chip, K is split
 // into windows whose raw sums go to part (fh3k_gemm_part_bytes bytes; 0 = no
 // split) and are added in window order with the epilogue; x16 must hold
@@ -83,7 +93,7 @@ int fh3k_midm_max_tokens(void);
 // fh3k_xprep with the rows first normalised: rmsnorm with weight norm_w and
 // eps, then (shift and scale both set, [M][K]) AdaLN modulate.
 hipError_t fh3k_xprep_norm(const float *x, int M, int K, int Mpad, void *x16, float *xs_inv, const float *norm_w,
-                           float eps, const float *shift, const float *scale, hipStream_t st);
+                           float eps, const float *shift, const float *scale, float *xsum, hipStream_t st);
 // The same normalisation into fp32 rows y[M][K] (y may alias x).
 hipError_t fh3k_rownorm_f32(const float *x, int M, int K, float *y, const float *norm_w, float eps,
                             const float *shift, const float *scale, hipStream_t st);

@@ -12,6 +12,11 @@
 //   k_skinny<TB,C>      small n_tok: one wavefront per 16 weight rows per K slice of
 //                       C super-blocks, exact weights (sc*q in fp16), two
 //                       v_mfma_f32_16x16x32_f16 chains, LDS reduce over the slices
+//   k_sweep<C>          up to 16 tokens: k_skinny's exact weights, persistent
+//                       workgroups with the activations held in registers, the
+//                       offsets from precomputed group sums (f32 MFMA)
+//   k_gemv8<MT,C>       up to 4 tokens: integer MFMA on the raw nibbles, fp32
+//                       activations quantised in the kernel, persistent
 //   k_gemm              large n_tok: 256x128 output tile, Q4_K dequantised into LDS
 //                       as fp16, v_mfma_f32_32x32x16_f16, fp32 accumulation
 //
@@ -315,6 +320,17 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 // (src/core/fh3_ops.c:410-456), then, when shift is set,
 //   x = fma(x, 1 + scale[t], shift[t])   (src/core/fh3_ops.c:529-557),
 // shift / scale being [M][K] rows.
+// Sum over each aligned group of 8 lanes (every lane of the group gets it).
+__device__ __forceinline__ float sum8_f32(float v) {
+    int iv = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(iv, iv, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+    iv = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(iv, iv, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+    iv = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(iv, iv, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    return v;
+}
+
 struct RowNorm {
     const float *w;
     float eps;
@@ -364,7 +380,8 @@ __device__ __forceinline__ void row_norm(f32x4 (&v)[V4], const RowNorm &nm, int 
 
 template <int V4>
 __global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ X, int M, int K,
-                                               half8 *__restrict__ X16, float *__restrict__ xs_inv, RowNorm nm) {
+                                               half8 *__restrict__ X16, float *__restrict__ xs_inv, RowNorm nm,
+                                               float *__restrict__ xsum) {
     __shared__ float s_red[4];
     // Consecutive workgroup ids go to different XCDs; give each XCD a
     // contiguous run of rows instead, so that neighbouring rows, which share
@@ -405,11 +422,18 @@ __global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ X, int 
 #pragma unroll
     for (int i = 0; i < V4; i++) {
         const int k4 = tid + 256 * i;
-        if (k4 < n4) {
+        if (k4 < n4) {  // uniform per wavefront: n4 is a multiple of 64
             const half4 h = {(_Float16)(v[i].x * s), (_Float16)(v[i].y * s), (_Float16)(v[i].z * s),
                              (_Float16)(v[i].w * s)};
             // fragment k4/4, lane half (k4/2)&1, 8-byte half k4&1
             dst[(size_t)(k4 >> 2) * 128 + ((k4 >> 1) & 1) * 64 + (k4 & 1)] = h;
+            if (xsum) {
+                // sums of the 32 fp16 values of each group (the 8 aligned
+                // lanes around this one), as the sweep kernel's offset term
+                // multiplies them
+                const float gs = sum8_f32(((float)h.x + (float)h.y) + ((float)h.z + (float)h.w));
+                if (t < M && (lane & 7) == 0) xsum[(size_t)t * (K / 32) + (k4 >> 3)] = gs;
+            }
         }
     }
 }
@@ -794,6 +818,196 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) vo
 }
 
 // ---------------------------------------------------------------------------
+// Small-M sweep (k_sweep): one token block (M <= 16), persistent.  k_skinny
+// reads a wavefront's activation fragments again for every 16-row block (as
+// many bytes of fp16 activations per super-block as the Q4_K weights it
+// multiplies, 16 tokens x 256 k x 2 B against 144 B x 16 rows); here each
+// wavefront loads the fragments of its window once and keeps them in
+// registers while its workgroup sweeps row blocks blockIdx.x, +gridDim.x, ...
+// Work split and weight ring as k_gemv8: NW = ceil(nsb / C) wavefronts, window
+// [s0, s0 + C) per wavefront (the last one moved back inside the row, shared
+// super-blocks are padding), one ring slot per super-block of the window,
+// refilled with the next block's super-block as soon as it is consumed.
+//
+// Arithmetic.  With w = d*sc*q - dmin*m, a super-block contributes
+//   d * sum_k (sc*q)_k x_k  -  sum_g dmin*m_g * X_g,
+// X_g the sum of the group's fp16 activations (made by the preparation).
+// The first term is eight v_mfma_f32_16x16x32_f16 on B = sc*q, exact in fp16:
+// low nibbles as (1024 + q)*sc - 1024*sc, high nibbles left in place as
+// (1024 + 16q)*(sc/16) - 64*sc, one fused v_pk_fma_f16 per pair (the result is
+// an integer below 2048, hence exact).  The second is two
+// v_mfma_f32_16x16x4_f32 per super-block (A = X_g, B = dmin*m_g of groups c
+// and c+4 for lane (row j, k-block c)), accumulated over the block.  The NW
+// partial sums are added in wave order through LDS (deterministic).  On this
+// GPU the VALU and the matrix core of a SIMD mostly take turns, so both the
+// B-operand VALU work (per weight) and the MFMA count (per super-block) set
+// the time: the offsets cost 2 MFMAs instead of 8.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ half2v magic_fma2(uint32_t a, uint32_t sel, half2v s, half2v ns) {
+    return __builtin_elementwise_fma(q4k_magic_pair(a, sel), s, ns);
+}
+
+// sum_k (sc*q)_k x_k of one super-block for 16 tokens x 16 weight rows (A:
+// skinny_load_a's fragments; lane (row j, chunk c) holds chunk c of row j)
+__device__ __forceinline__ f32x4 sweep_scq(const u32x4 hv, const u32x4 ca, const u32x4 cb, const Q4kField flo,
+                                           const Q4kField fhi, const half8 (&a)[8][1]) {
+    const uint32_t sclo = q4k_sc(hv, flo), schi = q4k_sc(hv, fhi);
+    const half2v s_lo = splat2(sclo), ns_lo = s_lo * (_Float16)-1024.0f;
+    const half2v s_hi = splat2(schi) * (_Float16)0.0625f, ns_hi = splat2(schi) * (_Float16)-64.0f;
+    f32x4 aq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        const int part = m & 3;
+        const bool hi = m >= 4;
+        const u32x4 cv = part < 2 ? ca : cb;
+        const uint32_t msk = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+        const uint32_t u0 = ((part & 1) ? cv.z : cv.x) & msk, u1 = ((part & 1) ? cv.w : cv.y) & msk;
+        const half2v s = hi ? s_hi : s_lo, ns = hi ? ns_hi : ns_lo;
+        const half2v p0 = magic_fma2(u0, 0x04010400u, s, ns), p1 = magic_fma2(u0, 0x04030402u, s, ns);
+        const half2v p2 = magic_fma2(u1, 0x04010400u, s, ns), p3 = magic_fma2(u1, 0x04030402u, s, ns);
+        const half8 b = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+        aq = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][0], b, aq, 0, 0, 0);
+    }
+    return aq;
+}
+
+template <int C, int LB, int EPI>
+__global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int K,
+                                              const half8 *__restrict__ X16, const float *__restrict__ xs_inv,
+                                              const float *__restrict__ xsum, const float *__restrict__ bias,
+                                              float *__restrict__ Y, int M, const float *__restrict__ aux, int nblk) {
+    extern __shared__ f32x4 red[];  // [2][NW][64]
+    const int NW = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = lane & 15, q = lane >> 4;
+    const int F = N >> 1;
+    constexpr int ROWS = EPI == EPI_SWIGLU ? 8 : 16;  // output columns per block
+    const int nsb = K >> 8, kf_n = K >> 4;
+    const int own = wave * C;
+    const int s0 = own < nsb - C ? own : nsb - C;
+    const int nit = (nblk - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+
+    // weight row of this lane in block it: rows o0..o0+15, or (SwiGLU) value
+    // rows o0..o0+7 and gate rows F+o0..F+o0+7
+    auto wptr = [&](int it) {
+        const int o0 = ((int)blockIdx.x + it * (int)gridDim.x) * ROWS;
+        int orow = EPI == EPI_SWIGLU ? (j < 8 ? o0 + j : F + o0 + j - 8) : o0 + j;
+        orow = orow < N ? orow : N - 1;
+        return W + (size_t)orow * row_bytes + (size_t)s0 * 144;
+    };
+    u32x4 hv[C], ca[C], cb[C];
+    {
+        const uint8_t *wh = wptr(0), *wc = wh + 16 + 32 * q;
+#pragma unroll
+        for (int s = 0; s < C; s++) {
+            hv[s] = ld16(wh + s * 144);
+            ca[s] = ld16(wc + s * 144);
+            cb[s] = ld16(wc + s * 144 + 16);
+        }
+    }
+    // A fragments and group sums of the window for token j (padding tokens
+    // re-read the last real row; their outputs are never stored)
+    half8 a[C][8][1];
+    float xg[C][2];
+    {
+        const int t = j < M ? j : M - 1;
+        const half8 *xq[1] = {X16 + ((size_t)(t >> 5) * kf_n + (size_t)s0 * 16 + 4 * q) * 64 + (t & 31)};
+        const float *xs = xsum + (size_t)t * (K >> 5) + (size_t)s0 * 8 + q;
+#pragma unroll
+        for (int i = 0; i < C; i++) {
+            skinny_load_a<1>(xq, i, a[i]);
+            xg[i][0] = xs[i * 8];
+            xg[i][1] = xs[i * 8 + 4];
+        }
+    }
+    // scale fields of groups 2q (low nibbles) and 2q + 1, min fields of groups
+    // q and q + 4 (the offset MFMA's k)
+    const Q4kField flo = q4k_field(2 * q), fhi = q4k_field(2 * q + 1);
+    const Q4kField fm0 = q4k_field(q), fm1 = q4k_field(q + 4);
+
+    // the output this thread stores after each block, if any: lane st_l of
+    // the 16x16 result holds column st_l % 16 and tokens 4 (st_l / 16) + v.
+    // With fewer than four wavefronts (in <= 1536) the threads of the
+    // workgroup take the 256 outputs in turn (st_all).
+    const bool st_all = blockDim.x < 256;
+    const int st_l = (int)threadIdx.x & 63, st_v = (int)threadIdx.x >> 6;
+    const int st_t = 4 * (st_l >> 4) + st_v, st_j = st_l & 15;
+    const bool storer = !st_all && (int)threadIdx.x < 256 && st_t < M && (EPI != EPI_SWIGLU || st_j < 8);
+    const float st_xs = storer ? xs_inv[st_t] : 0.f;
+    // one output (token t, column o = o0 + jj) from the NW partial sums of
+    // result lane l, register v
+    auto store = [&](const f32x4 *rb, int l, int v, int t, int o, float xs, float b, float bg, float ax, float y0) {
+        float s = rb[l][v];
+        for (int w = 1; w < NW; w++) s += rb[w * 64 + l][v];
+        if (EPI == EPI_SWIGLU) {  // the gate of column l % 16 is row l % 16 + 8 of the block
+            float sg = rb[l + 8][v];
+            for (int w = 1; w < NW; w++) sg += rb[w * 64 + l + 8][v];
+            Y[(size_t)t * F + o] = (s * xs + b) * silu_f32(sg * xs + bg);
+        } else if (EPI == EPI_GATE_RES) {
+            Y[(size_t)t * N + o] = __builtin_fmaf(ax, s * xs + b, y0);
+        } else {
+            Y[(size_t)t * N + o] = s * xs + b;
+        }
+    };
+
+    auto block = [&](int it, auto more_tag) {
+        constexpr bool MORE = decltype(more_tag)::value;
+        const int o0 = ((int)blockIdx.x + it * (int)gridDim.x) * ROWS;
+        const int st_o = o0 + st_j;
+        const bool st_ok = storer && st_o < N;
+        float e_b = 0.f, e_bg = 0.f, e_aux = 0.f, e_y = 0.f;
+        if (st_ok) {
+            if (bias) {
+                e_b = bias[st_o];
+                if (EPI == EPI_SWIGLU) e_bg = bias[F + st_o];
+            }
+            if (EPI == EPI_GATE_RES) {
+                e_aux = aux[(size_t)st_t * N + st_o];
+                e_y = Y[(size_t)st_t * N + st_o];
+            }
+        }
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f}, accm = {0.f, 0.f, 0.f, 0.f};
+        const uint8_t *nh = wptr(MORE ? it + 1 : it), *nc = nh + 16 + 32 * q;
+#pragma unroll
+        for (int i = 0; i < C; i++) {
+            const u32x4 h = hv[i];
+            const bool valid = s0 + i >= own;
+            const float d = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xFFFFu)) : 0.f;
+            const float dmin = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x >> 16)) : 0.f;
+            const f32x4 aq = sweep_scq(h, ca[i], cb[i], flo, fhi, a[i]);
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf(d, aq[v], acc[v]);
+            const float bm0 = dmin * (float)q4k_mn(h, fm0), bm1 = dmin * (float)q4k_mn(h, fm1);
+            accm = __builtin_amdgcn_mfma_f32_16x16x4f32(xg[i][0], bm0, accm, 0, 0, 0);
+            accm = __builtin_amdgcn_mfma_f32_16x16x4f32(xg[i][1], bm1, accm, 0, 0, 0);
+            if (MORE) {
+                hv[i] = ld16(nh + i * 144);
+                ca[i] = ld16(nc + i * 144);
+                cb[i] = ld16(nc + i * 144 + 16);
+            }
+        }
+        f32x4 *rb = red + (it & 1) * NW * 64;  // alternate buffers: one barrier per block
+        rb[wave * 64 + lane] = acc - accm;
+        __syncthreads();
+        if (st_ok) store(rb, st_l, st_v, st_t, st_o, st_xs, e_b, e_bg, e_aux, e_y);
+        if (st_all) {
+            for (int idx = (int)threadIdx.x; idx < 256; idx += (int)blockDim.x) {
+                const int l = idx & 63, v = idx >> 6, t = 4 * (l >> 4) + v, o = o0 + (l & 15);
+                if (t >= M || o >= N || (EPI == EPI_SWIGLU && (l & 15) >= 8)) continue;
+                const float b = bias ? bias[o] : 0.f, bg = (bias && EPI == EPI_SWIGLU) ? bias[F + o] : 0.f;
+                const float ax = EPI == EPI_GATE_RES ? aux[(size_t)t * N + o] : 0.f;
+                const float y0 = EPI == EPI_GATE_RES ? Y[(size_t)t * N + o] : 0.f;
+                store(rb, l, v, t, o, xs_inv[t], b, bg, ax, y0);
+            }
+        }
+    };
+    // every block but the last refills the ring with the next block's weights
+    for (int it = 0; it + 1 < nit; it++) block(it, std::integral_constant<bool, true>());
+    block(nit - 1, std::integral_constant<bool, false>());
+}
+
+// ---------------------------------------------------------------------------
 // One- to four-token kernel (k_gemv8): integer MFMA on the raw 4-bit weights,
 // activations quantised inside the kernel (no preparation launch).
 //
@@ -815,16 +1029,19 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) vo
 // k-block qd = l/16) holds chunk qd of its row (groups 2qd and 2qd+1), and
 // one MFMA "piece" (part pt, half hs) takes from it the nibbles hs of bytes
 // 16pt..16pt+15: elements 16pt..16pt+15 of group 2qd+hs, as bytes.  A = group
-// slots: A row i = (token 2a + i/8, group g = i%8) is the 16 activation bytes
-// of its group's part in k-block g/2 for the piece with hs = g%2, zero
-// elsewhere (the lane reads the record's zero bytes), so output row i collects
-// sum_k q_k x_q over exactly one group of one token, exact in int32.  Four
-// pieces per plane cover a super-block; tile a holds tokens 2a, 2a+1.  Per
-// super-block, lane l holds groups 4*((l/16)&1)+v (v = 0..3) of token
-// 2a + l/32 for row r:
-//   T = sum_v sc_v * (256*S_hi + S_lo),  Mt = sum_v m_v * X_v
-// in 24-bit integer multiply-adds (|S| < 2^23, |T| < 2^31), then
-//   acc += d * T - dmin * Mt   in fp32,
+// slots: for the pieces of parity hs, A row i = (token slot i/4, j = i%4) is
+// the 16 activation bytes of group 2j + hs of that token in k-block j, zero
+// in the other k-blocks (the lane reads the record's zero bytes), so output
+// row i collects sum_k q_k x_q over exactly one group of one token, exact in
+// int32, and all 16 rows of every MFMA carry a (token, group) pair: four
+// token slots cost the same eight MFMAs per super-block as one.  Output
+// register v of the parity-hs accumulators of lane l is group 2v + hs of
+// token l/16 for row r, so each lane holds all eight groups of its (token,
+// row):
+//   T_hs = sum over the groups of parity hs of sc_g * (256*S_hi + S_lo),
+//   Mt = sum_g m_g * X_g
+// in 24-bit integer multiply-adds (|S| < 2^23, |T_hs| < 2^31), then
+//   acc += d * T_0 + d * T_1 - dmin * Mt   in fp32,
 // the reference's w = (d*sc)*q - dmin*m with all integer parts exact.
 //
 // Work.  A workgroup of NW wavefronts covers the K/256 super-blocks of 16
@@ -860,26 +1077,14 @@ __device__ __forceinline__ float wave_max_f32(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 63));
 }
 
-// Sum over each aligned group of 8 lanes (every lane of the group gets it).
-__device__ __forceinline__ float sum8_f32(float v) {
-    int iv = __builtin_bit_cast(int, v);
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(iv, iv, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
-    iv = __builtin_bit_cast(int, v);
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(iv, iv, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
-    iv = __builtin_bit_cast(int, v);
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(iv, iv, 0x141, 0xF, 0xF, false));  // row_half_mirror
-    return v;
-}
-
 template <int MT, int C, int LB, int EPI>
 __global__ __launch_bounds__(LB) void k_gemv8(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int K,
                                               const float *__restrict__ X, const float *__restrict__ bias,
                                               float *__restrict__ Y, int M, const float *__restrict__ aux, int nblk) {
-    constexpr int TILES = MT > 1 ? MT / 2 : 1;
     constexpr int WAVE_LDS = C * MT * (2 * G8_REC + G8_XS);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
     const int NW = blockDim.x >> 6;
-    float *red = reinterpret_cast<float *>(lds8 + NW * WAVE_LDS);  // [2][NW][TILES][64]
+    float *red = reinterpret_cast<float *>(lds8 + NW * WAVE_LDS);  // [2][NW][64]
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, qd = lane >> 4;
@@ -986,33 +1191,45 @@ __global__ __launch_bounds__(LB) void k_gemv8(const uint8_t *__restrict__ W, int
     // operations of a wavefront execute in order
     __builtin_amdgcn_wave_barrier();
 
-    // A operand of lane (row r: token 2a + r/8, group g = r%8; k-block qd):
-    // its group's 16 bytes for the piece with hs == g%2 when qd == g/2, else
-    // the record's zero bytes
-    const int g = r & 7;
-    int aoff[TILES][2];
+    // A operand of lane (row i, k-block qd).  Four token slots (MT == 4):
+    // row i = (token slot i/4, j = i%4) holds, for the pieces of parity hs,
+    // group 2j + hs of its token when qd == j (that group's chunk is k-block
+    // j), so all 16 rows of every MFMA carry a (token, group) pair.  One or two
+    // tokens: row i = (token i/8, group g = i%8) holds group g for the pieces
+    // with hs == g%2 when qd == g/2 (half the rows of a piece are zero, but
+    // each lane then combines only four groups).  Other rows read the
+    // record's zero bytes.
+    constexpr bool WIDE = MT == 4;
+    int aoff[2];
+    if constexpr (WIDE) {
+        const int a_tok = r >> 2, a_j = r & 3;
 #pragma unroll
-    for (int a = 0; a < TILES; a++) {
-        const int tt = 2 * a + (r >> 3);
+        for (int hs = 0; hs < 2; hs++)
+            aoff[hs] = (qd == a_j && a_tok < MT) ? a_tok * 2 * G8_REC + 32 * (2 * a_j + hs)
+                                                 : (a_tok < MT ? a_tok : 0) * 2 * G8_REC + 256;
+    } else {
+        const int g = r & 7, tt = r >> 3;
         const bool in = qd == (g >> 1) && tt < MT;
 #pragma unroll
         for (int hs = 0; hs < 2; hs++)
-            aoff[a][hs] = (in && (g & 1) == hs) ? tt * 2 * G8_REC + 32 * g : (tt < MT ? tt : 0) * 2 * G8_REC + 256;
+            aoff[hs] = (in && (g & 1) == hs) ? tt * 2 * G8_REC + 32 * g : (tt < MT ? tt : 0) * 2 * G8_REC + 256;
     }
-    // group sums of the lane's (token 2a + l/32, groups 4hh..4hh+3)
+    // result lane l, weight row r: WIDE, token slot l/16, register v of the
+    // parity-hs accumulators is group 2v + hs (all eight groups in the lane);
+    // otherwise token l/32, register v is group 4*((l/16)&1) + v, and lanes l
+    // and l + 16 hold the two halves
     const int hh = qd & 1;
-    const uint32_t mA = hh ? 0x0F0F0F0Fu : 0x3F3F3F3Fu, mB = hh ? 0x30303030u : 0u;
-    int xoff[TILES];
+    const int otok = WIDE ? qd : lane >> 5;
+    const int otc = otok < MT ? otok : 0;
+    float my_inv = 0.f, my_inv2 = 1.f;
 #pragma unroll
-    for (int a = 0; a < TILES; a++) {
-        const int tt = 2 * a + (lane >> 5);
-        xoff[a] = ((tt < MT ? tt : 0) * 8 + 4 * hh) * 4;
-    }
-    // the output (token, column) this thread stores after each block, if any:
-    // lanes l and l+16 hold the two group halves of (token, row r)
-    const int st_a = (int)threadIdx.x >> 5, st_tl = ((int)threadIdx.x >> 4) & 1, st_rr = (int)threadIdx.x & 15;
-    const int st_t = 2 * st_a + st_tl, st_l = st_tl * 32 + st_rr;
-    const bool storer = (int)threadIdx.x < TILES * 32 && st_t < M && (EPI != EPI_SWIGLU || st_rr < 8);
+    for (int t = 0; t < MT; t++)
+        if (otok == t) my_inv = inv[t], my_inv2 = inv2[t];
+    // the output (token, column) this thread stores after each block, if any,
+    // and the result lane that holds it
+    const int st_t = (int)threadIdx.x >> 4, st_rr = (int)threadIdx.x & 15;
+    const int st_l = WIDE ? (int)threadIdx.x : 32 * st_t + st_rr;
+    const bool storer = (int)threadIdx.x < (WIDE ? 64 : 32) && st_t < M && (EPI != EPI_SWIGLU || st_rr < 8);
 
     auto block = [&](int it, auto more_tag) {
         constexpr bool MORE = decltype(more_tag)::value;
@@ -1030,16 +1247,14 @@ __global__ __launch_bounds__(LB) void k_gemv8(const uint8_t *__restrict__ W, int
                 e_y = Y[(size_t)st_t * N + st_o];
             }
         }
-        float acc[TILES];
-#pragma unroll
-        for (int a = 0; a < TILES; a++) acc[a] = 0.f;
+        float acc = 0.f;
         const uint8_t *nh = wptr(MORE ? it + 1 : it), *nc = nh + 16 + 32 * qd;
 #pragma unroll
         for (int i = 0; i < C; i++) {
             const u32x4 h = hv[i];
-            i32x4 dh[TILES], dl[TILES];
+            i32x4 dh[2], dl[2];
 #pragma unroll
-            for (int a = 0; a < TILES; a++) dh[a] = dl[a] = i32x4{0, 0, 0, 0};
+            for (int hs = 0; hs < 2; hs++) dh[hs] = dl[hs] = i32x4{0, 0, 0, 0};
 #pragma unroll
             for (int pc = 0; pc < 4; pc++) {
                 const int pt = pc >> 1, hs = pc & 1;
@@ -1048,55 +1263,67 @@ __global__ __launch_bounds__(LB) void k_gemv8(const uint8_t *__restrict__ W, int
                                            (int)((src.z >> 4) & 0x0F0F0F0Fu), (int)((src.w >> 4) & 0x0F0F0F0Fu)}
                                    : i32x4{(int)(src.x & 0x0F0F0F0Fu), (int)(src.y & 0x0F0F0F0Fu),
                                            (int)(src.z & 0x0F0F0F0Fu), (int)(src.w & 0x0F0F0F0Fu)};
-#pragma unroll
-                for (int a = 0; a < TILES; a++) {
-                    const uint8_t *ap = my + i * MT * 2 * G8_REC + aoff[a][hs] + 16 * pt;
-                    const i32x4 ah = *reinterpret_cast<const i32x4 *>(ap);
-                    const i32x4 al = *reinterpret_cast<const i32x4 *>(ap + G8_REC);
-                    dh[a] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, dh[a], 0, 0, 0);
-                    dl[a] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, dl[a], 0, 0, 0);
-                }
+                const uint8_t *ap = my + i * MT * 2 * G8_REC + aoff[hs] + 16 * pt;
+                const i32x4 ah = *reinterpret_cast<const i32x4 *>(ap);
+                const i32x4 al = *reinterpret_cast<const i32x4 *>(ap + G8_REC);
+                // one accumulator pair per parity (WIDE), or one for all pieces
+                const int ax = WIDE ? hs : 0;
+                dh[ax] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, dh[ax], 0, 0, 0);
+                dl[ax] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, dl[ax], 0, 0, 0);
             }
-            // 6-bit scales and mins of groups 4hh..4hh+3 of row r, one per byte
+            // 6-bit scales and mins of row r, one per byte: groups 0-3 and 4-7
             // (reference src/core/fh3_quant.c:168-177)
-            const uint32_t sc4 = ((hh ? h.w : h.y) & mA) | ((h.y >> 2) & mB);
-            const uint32_t m4 = ((hh ? (h.w >> 4) : h.z) & mA) | ((h.z >> 2) & mB);
+            const uint32_t sc_a = h.y & 0x3F3F3F3Fu, sc_b = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+            const uint32_t m_a = h.z & 0x3F3F3F3Fu, m_b = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
             const bool valid = s0 + i >= own;
             const float d = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xFFFFu)) : 0.f;
             const float dmin = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x >> 16)) : 0.f;
+            const i32x4 *xs = reinterpret_cast<const i32x4 *>(xsb + (i * MT + otc) * G8_XS);
+            // four groups per sum: |T| <= 4 * 63 * 32 * 15 * 2^14 < 2^31
+            int T[2] = {0, 0}, Mt = 0;
+            if constexpr (WIDE) {
+                const i32x4 xa = xs[0], xb = xs[1];
 #pragma unroll
-            for (int a = 0; a < TILES; a++) {
-                const i32x4 xs = *reinterpret_cast<const i32x4 *>(xsb + i * MT * G8_XS + xoff[a]);
-                int T = 0, Mt = 0;
+                for (int hs = 0; hs < 2; hs++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const int gg = 2 * v + hs;
+                        const uint32_t scw = gg < 4 ? sc_a : sc_b;
+                        const int S = (dh[hs][v] << 8) + dl[hs][v];
+                        T[hs] += __mul24((int)((scw >> (8 * (gg & 3))) & 0xFFu), S);
+                    }
+#pragma unroll
+                for (int gg = 0; gg < 8; gg++) {
+                    const uint32_t mw = gg < 4 ? m_a : m_b;
+                    Mt += __mul24((int)((mw >> (8 * (gg & 3))) & 0xFFu), gg < 4 ? xa[gg] : xb[gg - 4]);
+                }
+            } else {
+                const uint32_t scw = hh ? sc_b : sc_a, mw = hh ? m_b : m_a;
+                const i32x4 xv4 = xs[hh];
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
-                    const int S = (dh[a][v] << 8) + dl[a][v];
-                    T += (int)((sc4 >> (8 * v)) & 63u) * ((S << 8) >> 8);  // 24-bit multiply-add
-                    Mt += (int)((m4 >> (8 * v)) & 63u) * ((xs[v] << 8) >> 8);
+                    const int S = (dh[0][v] << 8) + dl[0][v];
+                    T[0] += __mul24((int)((scw >> (8 * v)) & 0xFFu), S);
+                    Mt += __mul24((int)((mw >> (8 * v)) & 0xFFu), xv4[v]);
                 }
-                acc[a] = __builtin_fmaf(d, (float)T, __builtin_fmaf(-dmin, (float)Mt, acc[a]));
             }
+            acc = __builtin_fmaf(d, (float)T[1], __builtin_fmaf(d, (float)T[0], __builtin_fmaf(-dmin, (float)Mt, acc)));
             if (MORE) {
                 hv[i] = ld16(nh + i * 144);
                 ca[i] = ld16(nc + i * 144);
                 cb[i] = ld16(nc + i * 144 + 16);
             }
         }
-        float *rb = red + (it & 1) * NW * TILES * 64;  // alternate buffers: one barrier per block
-#pragma unroll
-        for (int a = 0; a < TILES; a++) {
-            const int tt = 2 * a + (lane >> 5);
-            float v = acc[a] + __shfl_down(acc[a], 16);
-            v = (v * inv[tt < MT ? tt : 0]) * inv2[tt < MT ? tt : 0];
-            rb[(wave * TILES + a) * 64 + lane] = v;
-        }
+        if constexpr (!WIDE) acc += __shfl_down(acc, 16);  // the other four groups
+        float *rb = red + (it & 1) * NW * 64;  // alternate buffers: one barrier per block
+        rb[wave * 64 + lane] = (acc * my_inv) * my_inv2;
         __syncthreads();
         if (st_ok) {
             float sum = 0.f;
-            for (int w = 0; w < NW; w++) sum += rb[(w * TILES + st_a) * 64 + st_l];
+            for (int w = 0; w < NW; w++) sum += rb[w * 64 + st_l];
             if (EPI == EPI_SWIGLU) {  // the gate of column st_rr is row st_rr + 8 of the block
                 float sg = 0.f;
-                for (int w = 0; w < NW; w++) sg += rb[(w * TILES + st_a) * 64 + st_l + 8];
+                for (int w = 0; w < NW; w++) sg += rb[w * 64 + st_l + 8];
                 Y[(size_t)st_t * F + st_o] = (sum + e_b) * silu_f32(sg + e_bg);
             } else if (EPI == EPI_GATE_RES) {
                 Y[(size_t)st_t * N + st_o] = __builtin_fmaf(e_aux, sum + e_b, e_y);
@@ -1800,11 +2027,11 @@ constexpr int XPREP_R8_MIN_ROWS = 8192;
 
 extern "C" hipError_t fh3k_xprep_norm(const float *x, int M, int K, int Mpad, void *x16, float *xs_inv,
                                       const float *norm_w, float eps, const float *shift, const float *scale,
-                                      hipStream_t st) {
+                                      float *xsum, hipStream_t st) {
     if (Mpad % 8 || Mpad < M || (shift != nullptr) != (scale != nullptr) || (shift && !norm_w))
         return hipErrorInvalidValue;
     const RowNorm nm{norm_w, eps, shift, scale};
-    if (M >= XPREP_R8_MIN_ROWS && K <= (norm_w ? 8192 : 14336)) {
+    if (M >= XPREP_R8_MIN_ROWS && K <= (norm_w ? 8192 : 14336) && !xsum) {
         const dim3 g8((unsigned)(Mpad / 8)), b8(1024);
         if (norm_w) {
             if (K <= 4096)
@@ -1824,21 +2051,21 @@ extern "C" hipError_t fh3k_xprep_norm(const float *x, int M, int K, int Mpad, vo
     }
     const dim3 grid((unsigned)Mpad), block(256);
     if (K <= 4096)
-        hipLaunchKernelGGL(k_xprep<4>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv, nm);
+        hipLaunchKernelGGL(k_xprep<4>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv, nm, xsum);
     else if (K <= 8192)
-        hipLaunchKernelGGL(k_xprep<8>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv, nm);
+        hipLaunchKernelGGL(k_xprep<8>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv, nm, xsum);
     else if (K <= 16384)
-        hipLaunchKernelGGL(k_xprep<16>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv, nm);
+        hipLaunchKernelGGL(k_xprep<16>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv, nm, xsum);
     else if (K <= 32768)
-        hipLaunchKernelGGL(k_xprep<32>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv, nm);
+        hipLaunchKernelGGL(k_xprep<32>, grid, block, 0, st, x, M, K, (half8 *)x16, xs_inv, nm, xsum);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
 extern "C" hipError_t fh3k_xprep(const float *x, int M, int K, int Mpad, void *x16, float *xs_inv,
-                                 hipStream_t st) {
-    return fh3k_xprep_norm(x, M, K, Mpad, x16, xs_inv, nullptr, 0.f, nullptr, nullptr, st);
+                                 float *xsum, hipStream_t st) {
+    return fh3k_xprep_norm(x, M, K, Mpad, x16, xs_inv, nullptr, 0.f, nullptr, nullptr, xsum, st);
 }
 
 extern "C" hipError_t fh3k_rownorm_f32(const float *x, int M, int K, float *y, const float *norm_w, float eps,
@@ -1960,11 +2187,11 @@ static const size_t kGemv8MaxLds = 160u << 10;  // one workgroup per CU
 static int gemv8_mt(int M) { return M == 1 ? 1 : (M == 2 ? 2 : 4); }
 
 static size_t gemv8_lds(int K, int M, int &C, int &NW) {
-    const int nsb = K / 256, mt = gemv8_mt(M), tiles = mt > 1 ? mt / 2 : 1;
+    const int nsb = K / 256, mt = gemv8_mt(M);
     C = (nsb + 15) / 16;
     NW = C ? (nsb + C - 1) / C : 0;
     if (C < 1 || C > (mt == 4 ? 3 : 5)) return 0;
-    return (size_t)NW * C * mt * (2 * G8_REC + G8_XS) + 2 * (size_t)NW * tiles * 64 * sizeof(float);
+    return (size_t)NW * C * mt * (2 * G8_REC + G8_XS) + 2 * (size_t)NW * 64 * sizeof(float);
 }
 
 extern "C" int fh3k_gemv8_max_tokens(void) { return G8_MAX_TOKENS; }
@@ -2047,6 +2274,44 @@ extern "C" hipError_t fh3k_gemv8(const void *W, int64_t row_bytes, int N, int K,
     return fh3k_gemv8_epi(W, row_bytes, N, K, x, bias, y, M, EPI_NONE, nullptr, st);
 }
 
+// k_sweep: C = 2 super-blocks per wavefront, 2 <= nsb <= 24 (NW <= 12: three
+// wavefronts per SIMD at <= 168 VGPRs; C = 3 would spill).
+static int sweep_c(int nsb) { return nsb >= 2 && nsb <= 24 ? 2 : 0; }
+
+extern "C" int fh3k_sweep_max_tokens(void) { return 16; }
+
+extern "C" int fh3k_sweep_fits(int K, int M) {
+    return M >= 1 && M <= 16 && K >= 256 && K % 256 == 0 && sweep_c(K / 256) > 0;
+}
+
+template <int EPI>
+static hipError_t launch_sweep_e(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,
+                                 const float *xsum, const float *bias, float *y, int M, const float *aux,
+                                 hipStream_t st) {
+    constexpr int C = 2;
+    const int nsb = K / 256, NW = (nsb + C - 1) / C;
+    const int nblk = (int)row_blocks16(N, EPI);
+    const int cus = device_cus();
+    const int grid = nblk < cus ? nblk : cus;
+    const size_t lds = 2 * (size_t)NW * 64 * sizeof(f32x4);
+    if (NW * 64 > 768 || nblk < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((k_sweep<C, 768, EPI>), dim3(grid), dim3(NW * 64), lds, st, (const uint8_t *)W, rb, N, K,
+                       (const half8 *)x16, xs_inv, xsum, bias, y, M, aux, nblk);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t fh3k_sweep_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16,
+                                     const float *xs_inv, const float *xsum, const float *bias, float *y, int M,
+                                     int epi, const float *aux, hipStream_t st) {
+    if (!fh3k_sweep_fits(K, M) || N < 1 || !xsum || (epi == EPI_SWIGLU && (N % 16))) return hipErrorInvalidValue;
+    switch (epi) {
+        case EPI_NONE: return launch_sweep_e<EPI_NONE>(W, row_bytes, N, K, x16, xs_inv, xsum, bias, y, M, aux, st);
+        case EPI_GATE_RES:
+            return launch_sweep_e<EPI_GATE_RES>(W, row_bytes, N, K, x16, xs_inv, xsum, bias, y, M, aux, st);
+        case EPI_SWIGLU: return launch_sweep_e<EPI_SWIGLU>(W, row_bytes, N, K, x16, xs_inv, xsum, bias, y, M, aux, st);
+        default: return hipErrorInvalidValue;
+    }
+}
 
 extern "C" int fh3k_gemm_row_pad(void) { return GEMM_BM; }
 

@@ -31,7 +31,7 @@ FH3_E_NOT_FOUND = -6
 FH3_E_NOMEM = -7
 FH3_E_INVALID = -8
 
-PATH_AUTO, PATH_SKINNY, PATH_GEMM, PATH_GEMV8, PATH_MIDM = 0, 1, 2, 3, 4
+PATH_AUTO, PATH_SKINNY, PATH_GEMM, PATH_GEMV8, PATH_MIDM, PATH_SWEEP = 0, 1, 2, 3, 4, 5
 
 Q4K_BLOCK_BYTES = 144
 Q4K_BLOCK_WEIGHTS = 256

@@ -6,7 +6,7 @@
 
 Workloads (each launch sequence is preceded by one untimed warmup launch):
   gemv   the six small-M shapes (M in {1,4,16}, K=5120, N in {5120,17408}):
-         fh3_hip_matmul_prepared_dev -> k_gemv8 (M <= 4) and k_skinny
+         fh3_hip_matmul_prepared_dev -> k_gemv8 (M <= 4) and k_sweep
          (M = 16, after k_xprep), weights rotated over more than 256 MB of
          device copies so they come from HBM
   gemm   the DiT attention shapes (M=8192, K=5120, N in {15360,5120}):

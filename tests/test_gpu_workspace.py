@@ -94,7 +94,7 @@ def test_first_capture_of_unprepared_product_refused(fresh):
     eager run."""
     F = fresh
     K, N, M = 4096, 1024, 8
-    assert F.matmul_path(M, K) == F.PATH_SKINNY
+    assert F.matmul_path(M, K) == F.PATH_SWEEP
     assert F.matmul_workspace_bytes(K, N, M) == F.prepared_bytes(M, K)
     assert F.matmul_workspace_bytes(K, N, M, prepared=True) == 0
     assert F.matmul_workspace_bytes(K, N, 1) == 0          # k_gemv8 quantises in the kernel

@@ -246,6 +246,52 @@ def dit_blocks_streamed(ev, st, n_blocks=8, M=16384, passes=2):
         os.unlink(path)
 
 
+def te_other_types(ev, st, R=64):
+    """The text encoder's Q5_K / Q6_K tensors (K -> N: Q5_K 5120 -> 1024;
+    Q6_K 5120 -> 1024, 8192 -> 5120, 25600 -> 5120) at M = 1, 16 and 64
+    tokens: fh3_hip_matmul_dev, whose Q5_K / Q6_K product reads the blocks in
+    place (k_skinny).  Weights are random blocks with finite scales, rotated
+    over more than 256 MB of device copies; graph of R calls."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import helpers as H
+    rows = []
+    for name, K, N in (("Q5_K", 5120, 1024), ("Q6_K", 5120, 1024), ("Q6_K", 8192, 5120), ("Q6_K", 25600, 5120)):
+        t, _, bb, _ = H.QTYPES[name]
+        rng = np.random.default_rng(t * 100 + K + N)
+        raw = H.random_blocks(rng, name, N, K, scale_lo=-12, scale_hi=-8)
+        wb = raw.nbytes
+        copies = max(2, -(-(MALL_BYTES + (64 << 20)) // wb))
+        ws = [F.DeviceBuffer.from_array(raw)]
+        for _ in range(copies - 1):
+            b = F.DeviceBuffer(wb)
+            F.lib().fh3_hip_memcpy_dtod(b.ptr, ws[0].ptr, wb)
+            ws.append(b)
+        for M in (1, 16, 64):
+            dx = F.DeviceBuffer.from_array(rng.standard_normal((M, K)).astype(np.float32))
+            dy = F.DeviceBuffer(M * N * 4)
+
+            def call(i, dx=dx, dy=dy, M=M):
+                F.matmul_dev(ws[i % copies], K, N, dx, dy, M, qtype=t)
+
+            for i in range(2):
+                call(i)
+            F.synchronize()
+            g = F.capture(lambda: [call(i) for i in range(R)])
+            g.launch()
+            t_c = ev.time_ms(lambda i: g.launch(), 8, st) / R
+            g.close()
+            rows.append({"type": name, "M": M, "K": K, "N": N, "call_us": round(t_c * 1e3, 2),
+                         "weight_GBps": round(wb / (t_c * 1e-3) / 1e9, 1),
+                         "hbm_frac": round((wb + 4 * M * (K + N)) / (t_c * 1e-3) / HBM_PEAK, 4)})
+            log("[bench] %s M=%d K=%d N=%d call %.2f us (%.0f GB/s of weights)"
+                % (name, M, K, N, t_c * 1e3, wb / (t_c * 1e-3) / 1e9))
+            dx.close()
+            dy.close()
+        for b in ws:
+            b.close()
+    return rows
+
+
 def dit_attention(ev, st, n=16384, heads=40, hd=128, rot=96):
     """The DiT block's attention branch at the block shapes (hidden 5120 = 40
     heads of 128, n = 16384 tokens): fh3_hip_attention_qkv_dev reading q, k,
@@ -563,6 +609,12 @@ def main():
     if mlp:
         extra["dit_mlp_linears_ms"] = round(sum(g["call_ms"] for g in mlp), 4)
     extra["gemv"] = per_gemv
+
+    try:
+        extra["te_q5k_q6k"] = te_other_types(ev, st)
+    except Exception as e:  # keep the headline line when this leg fails
+        log("[bench] Q5_K / Q6_K leg failed: %r" % (e,))
+        extra["te_q5k_q6k"] = {"error": repr(e)}
 
     # ---------------- DiT attention branch ---------------------------------
     roofline_attn = None

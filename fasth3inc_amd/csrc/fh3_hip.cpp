@@ -474,8 +474,9 @@ extern "C" int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, vo
     return prepare(d_x, n_tok, in, d_prep, prep_rows(n_tok), stream ? (hipStream_t)stream : g.stream);
 }
 
-// Weights of another type than Q4_K: fp16 rows (the weight itself for F16,
-// else decoded into the library's w16 buffer), then k_skinny16 / k_gemm16.
+// Weights of another type than Q4_K: Q5_K and Q6_K up to 64 tokens are read
+// in place by k_skinny; otherwise fp16 rows (the weight itself for F16, else
+// decoded into the library's w16 buffer), then k_skinny16 / k_gemm16.
 static int path16(int n_tok) {
     if (g.path == FH3_HIP_PATH_GEMM) return FH3_HIP_PATH_GEMM;
     return n_tok <= fh3k_skinny_max_tokens() ? FH3_HIP_PATH_SKINNY : FH3_HIP_PATH_GEMM;
@@ -484,6 +485,11 @@ static int path16(int n_tok) {
 static int product16(const Fh3W *w, const void *x16, const float *xs_inv, int n_tok, const float *bias, float *d_y,
                      hipStream_t st) {
     const int K = (int)w->in, N = (int)w->out;
+    if (path16(n_tok) == FH3_HIP_PATH_SKINNY && fh3k_skinny_q_takes(w->type)) {
+        FH3_HIPCALL(fh3k_skinny_q(w->type, w->data, (int64_t)fh3_row_bytes(w->type, w->in), N, K, x16, xs_inv, bias,
+                                  d_y, n_tok, st));
+        return FH3_OK;
+    }
     const void *w16 = w->data;
     if (w->type != FH3_QUANT_F16) {
         int rc = grow(g.w16, (size_t)w->out * (size_t)w->in * 2, st);

@@ -56,6 +56,12 @@ hipError_t fh3k_skinny16(const void *W16, int N, int K, const void *x16, const f
                          float *y, int M, hipStream_t st);
 hipError_t fh3k_gemm16(const void *W16, int N, int K, const void *x16, const float *xs_inv, const float *bias,
                        float *y, int M, hipStream_t st);
+// Q5_K / Q6_K weights (type FH3K_Q5_K / FH3K_Q6_K) read in place by the
+// small-M kernel, M <= fh3k_skinny_max_tokens(), same fragments as fh3k_skinny;
+// fh3k_skinny_q_takes(type) says whether a type has this kernel.
+hipError_t fh3k_skinny_q(int type, const void *W, int64_t row_bytes, int N, int K, const void *x16,
+                         const float *xs_inv, const float *bias, float *y, int M, hipStream_t st);
+int fh3k_skinny_q_takes(int type);
 
 // Product epilogues (EPI_* of fh3_kernels.hip; FH3_EPI_* of fh3_hip.h): 0 plain
 // store, 1 y[t][o] += aux[t][o] * product (gate residual), 2 SwiGLU (weight of

@@ -9,9 +9,10 @@
 //   k_dequant_blocks<T> bit-exact fp32 dequantisation of Q8_0/Q2_K/Q3_K/Q4_K/Q5_K/Q6_K
 //   k_dequant_half<BF>  bit-exact fp32 from F16 / BF16
 //   k_xprep             fp32 activations -> fp16 MFMA fragments, per-row 2^e scale
-//   k_skinny<TB,C>      small n_tok: one wavefront per 16 weight rows per K slice of
+//   k_skinny<QT,TB,C>   small n_tok: one wavefront per 16 weight rows per K slice of
 //                       C super-blocks, exact weights (sc*q in fp16), two
-//                       v_mfma_f32_16x16x32_f16 chains, LDS reduce over the slices
+//                       v_mfma_f32_16x16x32_f16 chains, LDS reduce over the slices;
+//                       Q4_K, Q5_K or Q6_K blocks read in place
 //   k_sweep<C>          up to 16 tokens: k_skinny's exact weights, persistent
 //                       workgroups with the activations held in registers, the
 //                       offsets from precomputed group sums (f32 MFMA)
@@ -644,12 +645,14 @@ __device__ __forceinline__ half8 q4k_scq8_f16(uint32_t u0, uint32_t u1, bool hi,
 // (token, q): k = sb*256 + (2q + m/4)*32 + 8*(m%4) -> fragment
 // sb*16 + 4q + 2*(m/4) + (m%4)/2, lane half (m % 2) of it.  xq[tb] already
 // points at fragment s0*16 + 4q of the lane's token, so with i a compile-time
-// constant every offset below is one too.
-template <int TB>
+// constant every offset below is one too.  HI is the fragment distance of the
+// MFMAs m >= 4 from the first four: 2 for Q4_K / Q5_K (groups 2q and 2q+1),
+// 4 for Q6_K (k ranges 64 apart, see sk6_superblock).
+template <int TB, int HI = 2>
 __device__ __forceinline__ void skinny_load_a(const half8 *const xq[TB], int i, half8 (&a)[8][TB]) {
 #pragma unroll
     for (int m = 0; m < 8; m++) {
-        const int off = (i * 16 + (m >= 4 ? 2 : 0) + ((m & 3) >> 1)) * 64 + (m & 1) * 32;
+        const int off = (i * 16 + (m >= 4 ? HI : 0) + ((m & 3) >> 1)) * 64 + (m & 1) * 32;
 #pragma unroll
         for (int tb = 0; tb < TB; tb++) a[m][tb] = xq[tb][off];
     }
@@ -699,6 +702,173 @@ __device__ __forceinline__ void skinny_superblock(const u32x4 hv, const u32x4 ca
             acc[tb][v] = __builtin_fmaf(d, aq[tb][v], __builtin_fmaf(-dmin, am[tb][v], acc[tb][v]));
 }
 
+// Raw bytes one lane holds for one super-block in k_skinny, per weight type,
+// and their loads.  wh points at the super-block, wa / wb at this lane's
+// pieces of it (set once per launch, so every load has a compile-time offset).
+//   Q4_K (144 B): header (d, dmin, 12 B of scales/mins), chunk q (32 B).
+//   Q5_K (176 B, src/core/fh3_quant.c:198-237): the same header, the 32
+//     high-bit bytes qh (bit g of byte l = bit 4 of element l of group g),
+//     chunk q of the low nibbles (at 48 + 32q).
+//   Q6_K (210 B, src/core/fh3_quant.c:239-282): ql bytes 32q..32q+31, the 32
+//     qh bytes of half q/2, the 16 int8 scales and d.  Q6_K super-blocks are
+//     only 2-byte aligned; the 16-byte loads of these pieces are unaligned
+//     global loads (supported on this GPU), every byte inside the block.
+template <int QT> struct SkRaw { u32x4 hv, ca, cb; };
+template <> struct SkRaw<FH3K_Q5_K> { u32x4 hv, h0, h1, ca, cb; };
+template <> struct SkRaw<FH3K_Q6_K> { u32x4 l0, l1, h0, h1, sc; uint32_t d; };
+
+template <int QT>
+constexpr int sk_bytes() { return QT == FH3K_Q5_K ? 176 : (QT == FH3K_Q6_K ? 210 : 144); }
+
+typedef uint32_t u32x4u __attribute__((ext_vector_type(4), aligned(2)));
+__device__ __forceinline__ u32x4 ld16u(const uint8_t *p) {
+    return *reinterpret_cast<const u32x4u *>(p);
+}
+
+// lane pointers of super-block s0 for chunk / quarter q
+template <int QT>
+__device__ __forceinline__ void sk_lane_ptrs(const uint8_t *wh, int q, const uint8_t *&wa, const uint8_t *&wb) {
+    if constexpr (QT == FH3K_Q6_K) {
+        wa = wh + 32 * q;                  // ql
+        wb = wh + 128 + 32 * (q >> 1);     // qh of this half
+    } else {
+        wa = wh + (QT == FH3K_Q5_K ? 48 : 16) + 32 * q;  // the chunk
+        wb = wh;
+    }
+}
+
+template <int QT>
+__device__ __forceinline__ void sk_load(SkRaw<QT> &r, const uint8_t *wh, const uint8_t *wa, const uint8_t *wb,
+                                        int s) {
+    constexpr int B = sk_bytes<QT>();
+    if constexpr (QT == FH3K_Q6_K) {
+        r.l0 = ld16u(wa + s * B);
+        r.l1 = ld16u(wa + s * B + 16);
+        r.h0 = ld16u(wb + s * B);
+        r.h1 = ld16u(wb + s * B + 16);
+        r.sc = ld16u(wh + s * B + 192);
+        r.d = ld_u16(wh + s * B + 208);
+    } else {
+        r.hv = ld16(wh + s * B);
+        r.ca = ld16(wa + s * B);
+        r.cb = ld16(wa + s * B + 16);
+        if constexpr (QT == FH3K_Q5_K) {
+            r.h0 = ld16(wh + s * B + 16);
+            r.h1 = ld16(wh + s * B + 32);
+        }
+    }
+}
+
+// Eight fp16 from 8 bytes of small unsigned integers v (a = bytes 0-3, b =
+// bytes 4-7): fma(1024 + v, s, ns) per pair, one rounding.
+__device__ __forceinline__ half8 magic8_fma(uint32_t a, uint32_t b, half2v s, half2v ns) {
+    const half2v p0 = __builtin_elementwise_fma(q4k_magic_pair(a, 0x04010400u), s, ns);
+    const half2v p1 = __builtin_elementwise_fma(q4k_magic_pair(a, 0x04030402u), s, ns);
+    const half2v p2 = __builtin_elementwise_fma(q4k_magic_pair(b, 0x04010400u), s, ns);
+    const half2v p3 = __builtin_elementwise_fma(q4k_magic_pair(b, 0x04030402u), s, ns);
+    return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+// Q5_K super-block: as skinny_superblock with q = low nibble | (high bit << 4)
+// (0..31), so sc*q <= 63*31 = 1953 stays an exact fp16 integer.  MFMA m takes
+// elements 8*(m%4)..+7 of group g = 2q + m/4 of lane (row j, q): chunk bytes
+// and qh bytes 8*(m%4)..+7, bit g of the latter.
+template <int TB>
+__device__ __forceinline__ void sk5_superblock(const SkRaw<FH3K_Q5_K> &r, bool valid, int q, const Q4kField flo,
+                                               const Q4kField fhi, const half8 (&a)[8][TB], f32x4 acc[TB]) {
+    const u32x4 hv = r.hv;
+    const float d = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(hv.x & 0xFFFFu)) : 0.f;
+    const float dmin = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(hv.x >> 16)) : 0.f;
+    const uint32_t sclo = q4k_sc(hv, flo), schi = q4k_sc(hv, fhi);
+    const half2v sc_lo = splat2(sclo), sc_hi = splat2(schi);
+    const half2v nsc_lo = splat2(sclo) * (_Float16)-1024.0f, nsc_hi = splat2(schi) * (_Float16)-1024.0f;
+    const half2v m_lo = splat2(q4k_mn(hv, flo)), m_hi = splat2(q4k_mn(hv, fhi));
+    const half8 bm_lo = half8{m_lo[0], m_lo[1], m_lo[0], m_lo[1], m_lo[0], m_lo[1], m_lo[0], m_lo[1]};
+    const half8 bm_hi = half8{m_hi[0], m_hi[1], m_hi[0], m_hi[1], m_hi[0], m_hi[1], m_hi[0], m_hi[1]};
+    f32x4 aq[TB], am[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++) aq[tb] = am[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        const int part = m & 3;
+        const bool hi = m >= 4;
+        const u32x4 cv = part < 2 ? r.ca : r.cb, hq = part < 2 ? r.h0 : r.h1;
+        const uint32_t u0 = (part & 1) ? cv.z : cv.x, u1 = (part & 1) ? cv.w : cv.y;
+        const uint32_t h0 = (part & 1) ? hq.z : hq.x, h1 = (part & 1) ? hq.w : hq.y;
+        const int g = 2 * q + (hi ? 1 : 0);
+        const uint32_t b0 = ((hi ? u0 >> 4 : u0) & 0x0F0F0F0Fu) | (((h0 >> g) & 0x01010101u) << 4);
+        const uint32_t b1 = ((hi ? u1 >> 4 : u1) & 0x0F0F0F0Fu) | (((h1 >> g) & 0x01010101u) << 4);
+        const half8 b = magic8_fma(b0, b1, hi ? sc_hi : sc_lo, hi ? nsc_hi : nsc_lo);
+#pragma unroll
+        for (int tb = 0; tb < TB; tb++) {
+            aq[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][tb], b, aq[tb], 0, 0, 0);
+            am[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][tb], hi ? bm_hi : bm_lo, am[tb], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++)
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+            acc[tb][v] = __builtin_fmaf(d, aq[tb][v], __builtin_fmaf(-dmin, am[tb][v], acc[tb][v]));
+}
+
+// Q6_K super-block, w = d * sc_g * (q - 32) with q the 6-bit value and sc_g
+// the signed scale of 16-element sub-group g.  Lane (row j, q) holds ql bytes
+// 32q..32q+31 of its row: in half h = q/2 of the block (elements 128h..),
+// low nibbles are elements 128h + 32(q%2) + b and high nibbles elements
+// 128h + 64 + 32(q%2) + b, b = 0..31, whose 2 high bits are bits 2s..2s+1 of
+// qh byte 32h + b (s = (element % 128) / 32).  MFMA m takes b = 8*(m%4)..+7 of
+// the low (m < 4) or high nibbles: k = 128h + 32(q%2) + 64(m/4) + 8(m%4),
+// fragment 8h + 2(q%2) + 4(m/4) + (m%4)/2 (skinny_load_a with HI = 4), and
+// sub-group 8h + 2(q%2) + 4(m/4) + (m%4)/2, i.e. byte 2(q%2) + (m%4)/2 of
+// scale word 2h + m/4.  B = (1024 + q - 1056) * sc: the difference is exact,
+// the product |sc*(q-32)| <= 4096 is rounded once to fp16 (exact below 2048;
+// the same single rounding k_gemm applies to every weight), then scaled by d
+// in fp32.
+template <int TB>
+__device__ __forceinline__ void sk6_superblock(const SkRaw<FH3K_Q6_K> &r, bool valid, int q,
+                                               const half8 (&a)[8][TB], f32x4 acc[TB]) {
+    const float d = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(r.d & 0xFFFFu)) : 0.f;
+    const uint32_t w0 = (q >> 1) ? r.sc.z : r.sc.x, w1 = (q >> 1) ? r.sc.w : r.sc.y;
+    const int sb = 16 * (q & 1);
+    half2v scv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t w = i < 2 ? w0 : w1;
+        const int sv = (int)(int8_t)(uint8_t)((w >> (sb + 8 * (i & 1))) & 0xFFu);
+        const _Float16 h = (_Float16)(float)sv;
+        scv[i] = half2v{h, h};
+    }
+    const half2v off = half2v{(_Float16)-1056.0f, (_Float16)-1056.0f};
+    const int sh = 2 * (q & 1);
+    f32x4 aq[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++) aq[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        const int part = m & 3;
+        const bool hi = m >= 4;
+        const u32x4 lq = part < 2 ? r.l0 : r.l1, hq = part < 2 ? r.h0 : r.h1;
+        const uint32_t u0 = (part & 1) ? lq.z : lq.x, u1 = (part & 1) ? lq.w : lq.y;
+        const uint32_t h0 = (part & 1) ? hq.z : hq.x, h1 = (part & 1) ? hq.w : hq.y;
+        const int hs = sh + (hi ? 4 : 0);
+        const uint32_t b0 = ((hi ? u0 >> 4 : u0) & 0x0F0F0F0Fu) | (((h0 >> hs) & 0x03030303u) << 4);
+        const uint32_t b1 = ((hi ? u1 >> 4 : u1) & 0x0F0F0F0Fu) | (((h1 >> hs) & 0x03030303u) << 4);
+        const half2v s = scv[(hi ? 2 : 0) + (part >> 1)];
+        const half2v p0 = (q4k_magic_pair(b0, 0x04010400u) + off) * s;
+        const half2v p1 = (q4k_magic_pair(b0, 0x04030402u) + off) * s;
+        const half2v p2 = (q4k_magic_pair(b1, 0x04010400u) + off) * s;
+        const half2v p3 = (q4k_magic_pair(b1, 0x04030402u) + off) * s;
+        const half8 b = half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+#pragma unroll
+        for (int tb = 0; tb < TB; tb++) aq[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][tb], b, aq[tb], 0, 0, 0);
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) acc[tb][v] = __builtin_fmaf(d, aq[tb][v], acc[tb][v]);
+}
+
 // ---------------------------------------------------------------------------
 // Small-M kernel.  Workgroup = NW wavefronts (blockDim.x / 64, at most 8) over
 // 16 consecutive weight rows o0..o0+15; wavefront w owns the C contiguous
@@ -718,8 +888,10 @@ __device__ __forceinline__ void skinny_superblock(const u32x4 hv, const u32x4 ca
 // holds the activations of the same k (one 16-byte piece of an X16
 // fragment).  Partial sums of the NW waves are added in wave order through LDS
 // (deterministic).
+// QT selects the weight type: Q4_K, or Q5_K / Q6_K read in place (the lane
+// pieces and products of SkRaw, sk5_superblock, sk6_superblock).
 // ---------------------------------------------------------------------------
-template <int TB, int C, int MAXT = 512, int RMAX = (TB == 1 ? 5 : 3)>
+template <int QT, int TB, int C, int MAXT = 512, int RMAX = (TB == 1 ? 5 : 3)>
 __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_skinny(
     const uint8_t *__restrict__ W, int64_t row_bytes, int N, int K, const half8 *__restrict__ X16,
     const float *__restrict__ xs_inv, const float *__restrict__ bias, float *__restrict__ Y, int M, int epi,
@@ -739,8 +911,11 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) vo
     const int kf_n = K / 16;
     const int own = wave * C;                          // first super-block this wave owns
     const int s0 = own < nsb - C ? own : nsb - C;      // window start, inside the row
-    const uint8_t *wh = W + (size_t)orow * row_bytes + (size_t)s0 * 144;  // header of s0
-    const uint8_t *wc = wh + 16 + 32 * q;                                 // chunk q of s0
+    constexpr int SB = sk_bytes<QT>();
+    const uint8_t *wh = W + (size_t)orow * row_bytes + (size_t)s0 * SB;  // super-block s0
+    const uint8_t *wa, *wb;                                              // this lane's pieces of it
+    sk_lane_ptrs<QT>(wh, q, wa, wb);
+    constexpr int AHI = QT == FH3K_Q6_K ? 4 : 2;       // skinny_load_a's high-half distance
 
     f32x4 acc[TB];
     const half8 *xq[TB];
@@ -751,36 +926,36 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) vo
         // row (their output rows are never stored)
         int t = tb * 16 + j;
         t = t < M ? t : M - 1;
-        xq[tb] = X16 + ((size_t)(t >> 5) * kf_n + (size_t)s0 * 16 + 4 * q) * 64 + (t & 31);
+        // fragment of this lane's first k in super-block s0: 4q (Q4_K, Q5_K: chunk
+        // q), 8(q/2) + 2(q%2) (Q6_K: see sk6_superblock)
+        const int qf = QT == FH3K_Q6_K ? 8 * (q >> 1) + 2 * (q & 1) : 4 * q;
+        xq[tb] = X16 + ((size_t)(t >> 5) * kf_n + (size_t)s0 * 16 + qf) * 64 + (t & 31);
     }
     const Q4kField flo = q4k_field(2 * q), fhi = q4k_field(2 * q + 1);
 
-    u32x4 hv[RING], ca[RING], cb[RING];
+    SkRaw<QT> raw[RING];
 #pragma unroll
-    for (int s = 0; s < RING; s++) {
-        hv[s] = ld16(wh + s * 144);
-        ca[s] = ld16(wc + s * 144);
-        cb[s] = ld16(wc + s * 144 + 16);
-    }
+    for (int s = 0; s < RING; s++) sk_load<QT>(raw[s], wh, wa, wb, s);
     half8 a[AB][8][TB];
-    skinny_load_a<TB>(xq, 0, a[0]);
+    skinny_load_a<TB, AHI>(xq, 0, a[0]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < C; i++) {
         const int s = i % RING;
         const int ab = AB == 2 ? (i & 1) : 0;
         if (AB == 2 && i + 1 < C) {
-            skinny_load_a<TB>(xq, i + 1, a[(i + 1) & 1]);
+            skinny_load_a<TB, AHI>(xq, i + 1, a[(i + 1) & 1]);
         } else if (AB == 1 && i > 0) {
-            skinny_load_a<TB>(xq, i, a[0]);
+            skinny_load_a<TB, AHI>(xq, i, a[0]);
         }
         __builtin_amdgcn_sched_barrier(0);
-        skinny_superblock<TB>(hv[s], ca[s], cb[s], s0 + i >= own, flo, fhi, a[ab], acc);
-        if (i + RING < C) {
-            hv[s] = ld16(wh + (i + RING) * 144);
-            ca[s] = ld16(wc + (i + RING) * 144);
-            cb[s] = ld16(wc + (i + RING) * 144 + 16);
-        }
+        if constexpr (QT == FH3K_Q5_K)
+            sk5_superblock<TB>(raw[s], s0 + i >= own, q, flo, fhi, a[ab], acc);
+        else if constexpr (QT == FH3K_Q6_K)
+            sk6_superblock<TB>(raw[s], s0 + i >= own, q, a[ab], acc);
+        else
+            skinny_superblock<TB>(raw[s].hv, raw[s].ca, raw[s].cb, s0 + i >= own, flo, fhi, a[ab], acc);
+        if (i + RING < C) sk_load<QT>(raw[s], wh, wa, wb, i + RING);
         __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
@@ -2123,34 +2298,34 @@ static unsigned row_blocks16(int N, int epi) {
     return (unsigned)(epi == EPI_SWIGLU ? (N / 2) / 8 : (N + 15) / 16);
 }
 
-template <int TB, int C>
+template <int QT, int TB, int C>
 static hipError_t launch_skinny_c(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,
                                   const float *bias, float *y, int M, int NW, int epi, const float *aux,
                                   hipStream_t st) {
     const size_t lds = (size_t)NW * TB * 64 * sizeof(f32x4);
-    hipLaunchKernelGGL((k_skinny<TB, C>), dim3(row_blocks16(N, epi)), dim3(NW * 64), lds, st, (const uint8_t *)W, rb,
-                       N, K, (const half8 *)x16, xs_inv, bias, y, M, epi, aux);
+    hipLaunchKernelGGL((k_skinny<QT, TB, C>), dim3(row_blocks16(N, epi)), dim3(NW * 64), lds, st, (const uint8_t *)W,
+                       rb, N, K, (const half8 *)x16, xs_inv, bias, y, M, epi, aux);
     return hipGetLastError();
 }
 
-template <int TB>
+template <int TB, int QT = FH3K_Q4_K>
 static hipError_t launch_skinny(const void *W, int64_t rb, int N, int K, const void *x16,
                                 const float *xs_inv, const float *bias, float *y, int M, int epi, const float *aux,
                                 hipStream_t st) {
     int C, NW;
     skinny_split(K / 256, C, NW);
     switch (C) {
-        case 1: return launch_skinny_c<TB, 1>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 2: return launch_skinny_c<TB, 2>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 3: return launch_skinny_c<TB, 3>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 4: return launch_skinny_c<TB, 4>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 5: return launch_skinny_c<TB, 5>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 6: return launch_skinny_c<TB, 6>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 7: return launch_skinny_c<TB, 7>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 8: return launch_skinny_c<TB, 8>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 10: return launch_skinny_c<TB, 10>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 13: return launch_skinny_c<TB, 13>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 16: return launch_skinny_c<TB, 16>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 1: return launch_skinny_c<QT, TB, 1>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 2: return launch_skinny_c<QT, TB, 2>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 3: return launch_skinny_c<QT, TB, 3>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 4: return launch_skinny_c<QT, TB, 4>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 5: return launch_skinny_c<QT, TB, 5>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 6: return launch_skinny_c<QT, TB, 6>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 7: return launch_skinny_c<QT, TB, 7>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 8: return launch_skinny_c<QT, TB, 8>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 10: return launch_skinny_c<QT, TB, 10>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 13: return launch_skinny_c<QT, TB, 13>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        case 16: return launch_skinny_c<QT, TB, 16>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -2175,6 +2350,29 @@ extern "C" hipError_t fh3k_skinny(const void *W, int64_t row_bytes, int N, int K
 }
 
 extern "C" int fh3k_skinny_max_tokens(void) { return 64; }
+
+// Q5_K / Q6_K rows read in place by k_skinny (n_tok <= 64): no decoded copy.
+template <int QT>
+static hipError_t launch_skinny_q(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,
+                                  const float *bias, float *y, int M, hipStream_t st) {
+    switch ((M + 15) / 16) {
+        case 1: return launch_skinny<1, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st);
+        case 2: return launch_skinny<2, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st);
+        case 3: return launch_skinny<3, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st);
+        case 4: return launch_skinny<4, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+extern "C" int fh3k_skinny_q_takes(int type) { return type == FH3K_Q5_K || type == FH3K_Q6_K; }
+
+extern "C" hipError_t fh3k_skinny_q(int type, const void *W, int64_t row_bytes, int N, int K, const void *x16,
+                                    const float *xs_inv, const float *bias, float *y, int M, hipStream_t st) {
+    if (K % 256 || K < 256 || N < 1 || M < 1 || M > 64) return hipErrorInvalidValue;
+    if (type == FH3K_Q5_K) return launch_skinny_q<FH3K_Q5_K>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, st);
+    if (type == FH3K_Q6_K) return launch_skinny_q<FH3K_Q6_K>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, st);
+    return hipErrorInvalidValue;
+}
 
 // k_gemv8: C = ceil(nsb / 16) super-blocks per wavefront, NW = ceil(nsb / C)
 // <= 16 wavefronts (more, smaller windows measured faster at K = 5120: C = 2,

@@ -1,7 +1,9 @@
 """fh3_matmul with weights of the other types the reference accepts (every
 type its fh3_dequant decodes: src/core/fh3_ops.c:317-404), on the GPU through
 the C-ABI, against the CPU oracle.  These weights are decoded per call to fp16
-rows (the exact value rounded once) and multiplied by k_skinny16 / k_gemm16.
+rows (the exact value rounded once) and multiplied by k_skinny16 / k_gemm16,
+except Q5_K and Q6_K up to 64 tokens, which k_skinny reads in place
+(tests/test_gpu_native_q56.py covers that kernel on its own).
 
 Bar: rel-Frobenius <= 2e-3 of the oracle, bitwise reproducible.
 """

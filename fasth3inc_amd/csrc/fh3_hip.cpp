@@ -133,9 +133,9 @@ int choose_path(int n_tok, int64_t in) {
     if (g.path == FH3_HIP_PATH_MIDM && n_tok <= fh3k_midm_max_tokens()) return FH3_HIP_PATH_MIDM;
     if (g.path == FH3_HIP_PATH_GEMM) return FH3_HIP_PATH_GEMM;
     if (g8) return FH3_HIP_PATH_GEMV8;
-    // up to 16 tokens on rows of at most 6144: the persistent kernel that keeps
+    // up to 16 tokens on rows of at most 8192: the persistent kernel that keeps
     // the activations in registers (measured 10-20 % faster than k_skinny at
-    // M = 16, K = 5120)
+    // M = 16, K = 5120 and 6400, 1.5 % at K = 8192, N = 5120)
     if (sw) return FH3_HIP_PATH_SWEEP;
     // long rows (K >= 8192) with 17..64 tokens: the split-K kernel reads the
     // activations once per 128 rows instead of once per 16 (measured 25-45 %

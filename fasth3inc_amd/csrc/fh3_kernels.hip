@@ -2472,9 +2472,10 @@ extern "C" hipError_t fh3k_gemv8(const void *W, int64_t row_bytes, int N, int K,
     return fh3k_gemv8_epi(W, row_bytes, N, K, x, bias, y, M, EPI_NONE, nullptr, st);
 }
 
-// k_sweep: C = 2 super-blocks per wavefront, 2 <= nsb <= 24 (NW <= 12: three
-// wavefronts per SIMD at <= 168 VGPRs; C = 3 would spill).
-static int sweep_c(int nsb) { return nsb >= 2 && nsb <= 24 ? 2 : 0; }
+// k_sweep: C = 2 super-blocks per wavefront, 2 <= nsb <= 32: NW <= 12
+// wavefronts at <= 168 VGPRs (about 160 used), NW = 13..16 at <= 128 (a few
+// registers spilled); C = 3 would spill.
+static int sweep_c(int nsb) { return nsb >= 2 && nsb <= 32 ? 2 : 0; }
 
 extern "C" int fh3k_sweep_max_tokens(void) { return 16; }
 
@@ -2492,9 +2493,13 @@ static hipError_t launch_sweep_e(const void *W, int64_t rb, int N, int K, const 
     const int cus = device_cus();
     const int grid = nblk < cus ? nblk : cus;
     const size_t lds = 2 * (size_t)NW * 64 * sizeof(f32x4);
-    if (NW * 64 > 768 || nblk < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k_sweep<C, 768, EPI>), dim3(grid), dim3(NW * 64), lds, st, (const uint8_t *)W, rb, N, K,
-                       (const half8 *)x16, xs_inv, xsum, bias, y, M, aux, nblk);
+    if (NW * 64 > 1024 || nblk < 1) return hipErrorInvalidValue;
+    if (NW <= 12)
+        hipLaunchKernelGGL((k_sweep<C, 768, EPI>), dim3(grid), dim3(NW * 64), lds, st, (const uint8_t *)W, rb, N, K,
+                           (const half8 *)x16, xs_inv, xsum, bias, y, M, aux, nblk);
+    else
+        hipLaunchKernelGGL((k_sweep<C, 1024, EPI>), dim3(grid), dim3(NW * 64), lds, st, (const uint8_t *)W, rb, N,
+                           K, (const half8 *)x16, xs_inv, xsum, bias, y, M, aux, nblk);
     return hipGetLastError();
 }
 

@@ -237,7 +237,7 @@ int fh3_hip_matmul_noalloc_dev(const Fh3W *w, const float *d_x, float *d_y, int 
  *     planes, one power-of-two scale per token and wavefront window) inside
  *     the kernel, integer MFMA on the raw 4-bit weights, no preparation launch
  *     and no workspace;
- *   - FH3_HIP_PATH_SWEEP for the other n_tok <= 16 when 512 <= in <= 6144:
+ *   - FH3_HIP_PATH_SWEEP for the other n_tok <= 16 when 512 <= in <= 8192:
  *     fp16 activations with their group sums (prepared), exact fp16 sc*q
  *     weights, persistent workgroups that keep each wavefront's activations in
  *     registers while they sweep the weight rows;

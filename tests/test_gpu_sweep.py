@@ -1,5 +1,5 @@
 """GPU parity of the persistent small-M kernel (FH3_HIP_PATH_SWEEP: up to 16
-tokens, 512 <= K <= 6144; fp16 activations held in registers, exact fp16
+tokens, 512 <= K <= 8192; fp16 activations held in registers, exact fp16
 sc*q weights, the offsets dmin*m from the prepared group sums) against the
 CPU oracle, through the C-ABI.
 
@@ -51,6 +51,8 @@ CASES = [
     (8, 2048, 200, "silu_gated", 2.0, True),      # partial last row block
     (9, 5376, 130, "outliers", 0.0, False),       # 21 super-blocks: shared window
     (13, 6144, 640, "normal", 2.0, False),        # 12 wavefronts
+    (16, 6400, 96, "outliers", 1.0, True),        # 13 wavefronts: the 1024-thread instantiation
+    (12, 8192, 300, "silu_gated", 0.0, False),    # 16 wavefronts (the text encoder's o-projection rows)
     (16, 5120, 5120, "normal", 0.0, False),       # text-encoder attention projection
     (16, 5120, 17408, "outliers", 0.0, True),     # text-encoder MLP, several blocks per workgroup
 ]

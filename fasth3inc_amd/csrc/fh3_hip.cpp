@@ -511,6 +511,7 @@ static size_t part_bytes(const Fh3W *w, int n_tok, int epi) {
     const int path = choose_path(n_tok, w->in);
     if (path == FH3_HIP_PATH_MIDM) return fh3k_midm_part_bytes(N, K, n_tok);
     if (path == FH3_HIP_PATH_GEMM) return fh3k_gemm_part_bytes(N, K, n_tok, epi);
+    if (path == FH3_HIP_PATH_SWEEP) return fh3k_sweep_part_bytes(N, K, n_tok);
     return 0;
 }
 
@@ -537,14 +538,11 @@ static int product(const Fh3W *w, const void *prep, int n_tok, const float *bias
     const int path = choose_path(n_tok, w->in);
     if (path == FH3_HIP_PATH_GEMV8) {
         FH3_HIPCALL(fh3k_gemv8_epi(w->data, row_bytes, N, K, (const float *)prep, bias, d_y, n_tok, epi, aux, st));
-    } else if (path == FH3_HIP_PATH_SWEEP) {
-        FH3_HIPCALL(fh3k_sweep_epi(w->data, row_bytes, N, K, prep, xs_inv, prep_sums(prep, n_tok, w->in), bias, d_y,
-                                   n_tok, epi, aux, st));
     } else if (path == FH3_HIP_PATH_SKINNY) {
         FH3_HIPCALL(fh3k_skinny_epi(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, epi, aux, st));
     } else {
-        // the split-K kernels (middle M, and the GEMM with few tiles) need the
-        // partial-sum workspace
+        // the split-K kernels (the sweep on rows of more than 32 super-blocks,
+        // middle M, and the GEMM with few tiles) need the partial-sum workspace
         const size_t pb = part_bytes(w, n_tok, epi);
         std::unique_lock<std::recursive_mutex> lk(g.mu, std::defer_lock);
         float *part = part_ext;
@@ -554,7 +552,10 @@ static int product(const Fh3W *w, const void *prep, int n_tok, const float *bias
             if (rc != FH3_OK) return rc;
             part = (float *)g.part.p;
         }
-        if (path == FH3_HIP_PATH_MIDM)
+        if (path == FH3_HIP_PATH_SWEEP)
+            FH3_HIPCALL(fh3k_sweep_epi(w->data, row_bytes, N, K, prep, xs_inv, prep_sums(prep, n_tok, w->in), bias,
+                                       d_y, n_tok, epi, aux, part, st));
+        else if (path == FH3_HIP_PATH_MIDM)
             FH3_HIPCALL(fh3k_midm_epi(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, epi, aux, part, st));
         else
             FH3_HIPCALL(fh3k_gemm_epi(w->data, row_bytes, N, K, prep, xs_inv, bias, d_y, n_tok, epi, aux, part, st));

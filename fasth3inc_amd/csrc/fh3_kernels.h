@@ -73,9 +73,12 @@ hipError_t fh3k_gemv8_epi(const void *W, int64_t row_bytes, int N, int K, const 
 // Up to fh3k_sweep_max_tokens() tokens from prepared fragments and their group
 // sums (fh3k_xprep with xsum), when fh3k_sweep_fits(K, M); persistent, the
 // activations held in registers.
+// K beyond 32 super-blocks is split into slices whose partial sums go to part
+// (fh3k_sweep_part_bytes(N, K, M) bytes; 0 = no split, part may be NULL).
 hipError_t fh3k_sweep_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16, const float *xs_inv,
                           const float *xsum, const float *bias, float *y, int M, int epi, const float *aux,
-                          hipStream_t st);
+                          float *part, hipStream_t st);
+size_t fh3k_sweep_part_bytes(int N, int K, int M);
 int fh3k_sweep_fits(int K, int M);
 int fh3k_sweep_max_tokens(void);
 // Large M.  When the 256 x 128 tiles alone would not fill the chip, K is split

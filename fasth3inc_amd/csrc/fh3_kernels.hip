@@ -15,7 +15,8 @@
 //                       Q4_K, Q5_K or Q6_K blocks read in place
 //   k_sweep<C>          up to 16 tokens: k_skinny's exact weights, persistent
 //                       workgroups with the activations held in registers, the
-//                       offsets from precomputed group sums (f32 MFMA)
+//                       offsets from precomputed group sums (f32 MFMA); long
+//                       rows in K slices added by k_midm_sum
 //   k_gemv8<MT,C>       up to 4 tokens: integer MFMA on the raw nibbles, fp32
 //                       activations quantised in the kernel, persistent
 //   k_gemm              large n_tok: 256x128 output tile, Q4_K dequantised into LDS
@@ -1050,7 +1051,8 @@ template <int C, int LB, int EPI>
 __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int K,
                                               const half8 *__restrict__ X16, const float *__restrict__ xs_inv,
                                               const float *__restrict__ xsum, const float *__restrict__ bias,
-                                              float *__restrict__ Y, int M, const float *__restrict__ aux, int nblk) {
+                                              float *__restrict__ Y, int M, const float *__restrict__ aux, int nblk,
+                                              int S, float *__restrict__ part) {
     extern __shared__ f32x4 red[];  // [2][NW][64]
     const int NW = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -1058,18 +1060,25 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
     const int j = lane & 15, q = lane >> 4;
     const int F = N >> 1;
     constexpr int ROWS = EPI == EPI_SWIGLU ? 8 : 16;  // output columns per block
-    const int nsb = K >> 8, kf_n = K >> 4;
+    // K in S slices of SL super-blocks (S = 1: all of K): workgroup g takes
+    // slice g % S and the row blocks g / S, + gridDim.x / S, ...; window
+    // offsets below are relative to the slice's first super-block sbb
+    const int nsb_all = K >> 8, kf_n = K >> 4;
+    const int SL = (nsb_all + S - 1) / S;
+    const int ks = (int)blockIdx.x % S, gw = (int)blockIdx.x / S, GW = (int)gridDim.x / S;
+    const int sbb = ks * SL;
+    const int nsb = SL < nsb_all - sbb ? SL : nsb_all - sbb;
     const int own = wave * C;
     const int s0 = own < nsb - C ? own : nsb - C;
-    const int nit = (nblk - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int nit = (nblk - gw + GW - 1) / GW;
 
     // weight row of this lane in block it: rows o0..o0+15, or (SwiGLU) value
     // rows o0..o0+7 and gate rows F+o0..F+o0+7
     auto wptr = [&](int it) {
-        const int o0 = ((int)blockIdx.x + it * (int)gridDim.x) * ROWS;
+        const int o0 = (gw + it * GW) * ROWS;
         int orow = EPI == EPI_SWIGLU ? (j < 8 ? o0 + j : F + o0 + j - 8) : o0 + j;
         orow = orow < N ? orow : N - 1;
-        return W + (size_t)orow * row_bytes + (size_t)s0 * 144;
+        return W + (size_t)orow * row_bytes + (size_t)(sbb + s0) * 144;
     };
     u32x4 hv[C], ca[C], cb[C];
     {
@@ -1087,8 +1096,8 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
     float xg[C][2];
     {
         const int t = j < M ? j : M - 1;
-        const half8 *xq[1] = {X16 + ((size_t)(t >> 5) * kf_n + (size_t)s0 * 16 + 4 * q) * 64 + (t & 31)};
-        const float *xs = xsum + (size_t)t * (K >> 5) + (size_t)s0 * 8 + q;
+        const half8 *xq[1] = {X16 + ((size_t)(t >> 5) * kf_n + (size_t)(sbb + s0) * 16 + 4 * q) * 64 + (t & 31)};
+        const float *xs = xsum + (size_t)t * (K >> 5) + (size_t)(sbb + s0) * 8 + q;
 #pragma unroll
         for (int i = 0; i < C; i++) {
             skinny_load_a<1>(xq, i, a[i]);
@@ -1105,10 +1114,11 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
     // the 16x16 result holds column st_l % 16 and tokens 4 (st_l / 16) + v.
     // With fewer than four wavefronts (in <= 1536) the threads of the
     // workgroup take the 256 outputs in turn (st_all).
-    const bool st_all = blockDim.x < 256;
+    const bool st_all = blockDim.x < 256 || part;
     const int st_l = (int)threadIdx.x & 63, st_v = (int)threadIdx.x >> 6;
     const int st_t = 4 * (st_l >> 4) + st_v, st_j = st_l & 15;
     const bool storer = !st_all && (int)threadIdx.x < 256 && st_t < M && (EPI != EPI_SWIGLU || st_j < 8);
+    const size_t mn = (size_t)M * N;
     const float st_xs = storer ? xs_inv[st_t] : 0.f;
     // one output (token t, column o = o0 + jj) from the NW partial sums of
     // result lane l, register v
@@ -1128,7 +1138,7 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
 
     auto block = [&](int it, auto more_tag) {
         constexpr bool MORE = decltype(more_tag)::value;
-        const int o0 = ((int)blockIdx.x + it * (int)gridDim.x) * ROWS;
+        const int o0 = (gw + it * GW) * ROWS;
         const int st_o = o0 + st_j;
         const bool st_ok = storer && st_o < N;
         float e_b = 0.f, e_bg = 0.f, e_aux = 0.f, e_y = 0.f;
@@ -1166,7 +1176,16 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
         rb[wave * 64 + lane] = acc - accm;
         __syncthreads();
         if (st_ok) store(rb, st_l, st_v, st_t, st_o, st_xs, e_b, e_bg, e_aux, e_y);
-        if (st_all) {
+        if (part) {  // K slices: this slice's raw sums of every row of the block
+            for (int idx = (int)threadIdx.x; idx < 256; idx += (int)blockDim.x) {
+                const int l = idx & 63, v = idx >> 6, t = 4 * (l >> 4) + v, jj = l & 15;
+                const int col = EPI == EPI_SWIGLU ? o0 + (jj & 7) : o0 + jj;
+                if (t >= M || col >= (EPI == EPI_SWIGLU ? F : N)) continue;
+                float sv = rb[l][v];
+                for (int w = 1; w < NW; w++) sv += rb[w * 64 + l][v];
+                part[(size_t)ks * mn + (size_t)t * N + (EPI == EPI_SWIGLU && jj >= 8 ? F + col : col)] = sv;
+            }
+        } else if (st_all) {
             for (int idx = (int)threadIdx.x; idx < 256; idx += (int)blockDim.x) {
                 const int l = idx & 63, v = idx >> 6, t = 4 * (l >> 4) + v, o = o0 + (l & 15);
                 if (t >= M || o >= N || (EPI == EPI_SWIGLU && (l & 15) >= 8)) continue;
@@ -2472,46 +2491,72 @@ extern "C" hipError_t fh3k_gemv8(const void *W, int64_t row_bytes, int N, int K,
     return fh3k_gemv8_epi(W, row_bytes, N, K, x, bias, y, M, EPI_NONE, nullptr, st);
 }
 
-// k_sweep: C = 2 super-blocks per wavefront, 2 <= nsb <= 32: NW <= 12
-// wavefronts at <= 168 VGPRs (about 160 used), NW = 13..16 at <= 128 (a few
-// registers spilled); C = 3 would spill.
-static int sweep_c(int nsb) { return nsb >= 2 && nsb <= 32 ? 2 : 0; }
+// k_sweep: C = 2 super-blocks per wavefront over K slices of at most 20
+// super-blocks, so at most 10 wavefronts at <= 168 VGPRs (about 160 used; C =
+// 3 would spill).  Rows longer than 20 super-blocks (to K = 32768) are split
+// into S slices whose raw sums go to part[S][M][N] and are added in slice
+// order by k_midm_sum (slices of at most 20 measured best: at K = 8192 two
+// slices of 16 beat one of 32 by 3-10 %, at K = 25600 five of 20 beat four of
+// 25 and seven of 15; K = 5120 stays whole).
+static void sweep_split(int nsb, int &S, int &SL) {
+    S = (nsb + 19) / 20;
+    SL = (nsb + S - 1) / S;
+}
 
 extern "C" int fh3k_sweep_max_tokens(void) { return 16; }
 
 extern "C" int fh3k_sweep_fits(int K, int M) {
-    return M >= 1 && M <= 16 && K >= 256 && K % 256 == 0 && sweep_c(K / 256) > 0;
+    return M >= 1 && M <= 16 && K >= 512 && K <= 32768 && K % 256 == 0;
 }
+
+extern "C" size_t fh3k_sweep_part_bytes(int N, int K, int M) {
+    int S, SL;
+    if (!fh3k_sweep_fits(K, M) || N < 1) return 0;
+    sweep_split(K / 256, S, SL);
+    return S > 1 ? (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+namespace {
+__global__ __launch_bounds__(256) void k_midm_sum(const float *__restrict__ part, int S, int M, int N,
+                                                  const float *__restrict__ xs_inv, const float *__restrict__ bias,
+                                                  float *__restrict__ Y, int epi, const float *__restrict__ aux);
+}  // namespace
 
 template <int EPI>
 static hipError_t launch_sweep_e(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,
-                                 const float *xsum, const float *bias, float *y, int M, const float *aux,
+                                 const float *xsum, const float *bias, float *y, int M, const float *aux, float *part,
                                  hipStream_t st) {
     constexpr int C = 2;
-    const int nsb = K / 256, NW = (nsb + C - 1) / C;
+    int S, SL;
+    sweep_split(K / 256, S, SL);
+    const int NW = (SL + C - 1) / C;
     const int nblk = (int)row_blocks16(N, EPI);
-    const int cus = device_cus();
-    const int grid = nblk < cus ? nblk : cus;
+    const int per = device_cus() / S;  // workgroups per slice
+    const int grid = (nblk < per ? nblk : per) * S;
     const size_t lds = 2 * (size_t)NW * 64 * sizeof(f32x4);
-    if (NW * 64 > 1024 || nblk < 1) return hipErrorInvalidValue;
-    if (NW <= 12)
-        hipLaunchKernelGGL((k_sweep<C, 768, EPI>), dim3(grid), dim3(NW * 64), lds, st, (const uint8_t *)W, rb, N, K,
-                           (const half8 *)x16, xs_inv, xsum, bias, y, M, aux, nblk);
-    else
-        hipLaunchKernelGGL((k_sweep<C, 1024, EPI>), dim3(grid), dim3(NW * 64), lds, st, (const uint8_t *)W, rb, N,
-                           K, (const half8 *)x16, xs_inv, xsum, bias, y, M, aux, nblk);
+    if (NW * 64 > 640 || nblk < 1 || grid < S || (S > 1 && !part)) return hipErrorInvalidValue;
+    float *pp = S > 1 ? part : nullptr;
+    hipLaunchKernelGGL((k_sweep<C, 768, EPI>), dim3(grid), dim3(NW * 64), lds, st, (const uint8_t *)W, rb, N, K,
+                       (const half8 *)x16, xs_inv, xsum, bias, y, M, aux, nblk, S, pp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || S == 1) return e;
+    const int64_t outs = (int64_t)M * (EPI == EPI_SWIGLU ? N / 2 : N);
+    hipLaunchKernelGGL(k_midm_sum, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, st, part, S, M, N, xs_inv,
+                       bias, y, EPI, aux);
     return hipGetLastError();
 }
 
 extern "C" hipError_t fh3k_sweep_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16,
                                      const float *xs_inv, const float *xsum, const float *bias, float *y, int M,
-                                     int epi, const float *aux, hipStream_t st) {
+                                     int epi, const float *aux, float *part, hipStream_t st) {
     if (!fh3k_sweep_fits(K, M) || N < 1 || !xsum || (epi == EPI_SWIGLU && (N % 16))) return hipErrorInvalidValue;
     switch (epi) {
-        case EPI_NONE: return launch_sweep_e<EPI_NONE>(W, row_bytes, N, K, x16, xs_inv, xsum, bias, y, M, aux, st);
+        case EPI_NONE:
+            return launch_sweep_e<EPI_NONE>(W, row_bytes, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
         case EPI_GATE_RES:
-            return launch_sweep_e<EPI_GATE_RES>(W, row_bytes, N, K, x16, xs_inv, xsum, bias, y, M, aux, st);
-        case EPI_SWIGLU: return launch_sweep_e<EPI_SWIGLU>(W, row_bytes, N, K, x16, xs_inv, xsum, bias, y, M, aux, st);
+            return launch_sweep_e<EPI_GATE_RES>(W, row_bytes, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
+        case EPI_SWIGLU:
+            return launch_sweep_e<EPI_SWIGLU>(W, row_bytes, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
         default: return hipErrorInvalidValue;
     }
 }

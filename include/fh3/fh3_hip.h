@@ -237,10 +237,12 @@ int fh3_hip_matmul_noalloc_dev(const Fh3W *w, const float *d_x, float *d_y, int 
  *     planes, one power-of-two scale per token and wavefront window) inside
  *     the kernel, integer MFMA on the raw 4-bit weights, no preparation launch
  *     and no workspace;
- *   - FH3_HIP_PATH_SWEEP for the other n_tok <= 16 when 512 <= in <= 8192:
+ *   - FH3_HIP_PATH_SWEEP for the other n_tok <= 16 when 512 <= in <= 32768:
  *     fp16 activations with their group sums (prepared), exact fp16 sc*q
  *     weights, persistent workgroups that keep each wavefront's activations in
- *     registers while they sweep the weight rows;
+ *     registers while they sweep the weight rows; rows of more than 5120
+ *     weights are split into K slices whose partial sums (library workspace,
+ *     see fh3_hip_matmul_workspace_bytes) are added in slice order;
  *   - FH3_HIP_PATH_MIDM for 17 <= n_tok <= 64 and in >= 8192: K split into
  *     windows over 128-row workgroups that share staged activations, partial
  *     sums in a library workspace, then an ordered sum (any n_tok <= 64 when

@@ -1,7 +1,8 @@
 """GPU parity of the persistent small-M kernel (FH3_HIP_PATH_SWEEP: up to 16
-tokens, 512 <= K <= 8192; fp16 activations held in registers, exact fp16
-sc*q weights, the offsets dmin*m from the prepared group sums) against the
-CPU oracle, through the C-ABI.
+tokens, 512 <= K <= 32768; fp16 activations held in registers, exact fp16
+sc*q weights, the offsets dmin*m from the prepared group sums; rows of more
+than 20 super-blocks in K slices whose partial sums are added in slice order)
+against the CPU oracle, through the C-ABI.
 
 Bars as for the other product kernels: rel-Frobenius <= 2e-3 against the
 oracle (fh3's CPU fh3_matmul, src/core/fh3_ops.c:317-404), bitwise
@@ -51,8 +52,11 @@ CASES = [
     (8, 2048, 200, "silu_gated", 2.0, True),      # partial last row block
     (9, 5376, 130, "outliers", 0.0, False),       # 21 super-blocks: shared window
     (13, 6144, 640, "normal", 2.0, False),        # 12 wavefronts
-    (16, 6400, 96, "outliers", 1.0, True),        # 13 wavefronts: the 1024-thread instantiation
-    (12, 8192, 300, "silu_gated", 0.0, False),    # 16 wavefronts (the text encoder's o-projection rows)
+    (16, 6400, 96, "outliers", 1.0, True),        # two K slices of 13 and 12 super-blocks
+    (12, 8192, 300, "silu_gated", 0.0, False),    # two slices of 16 (the text encoder's o-projection rows)
+    (3, 13824, 130, "outliers", 0.0, False),      # three slices (18 each); past the int8 kernel's window
+    (1, 25600, 64, "normal", 2.0, True),          # five slices of 20 (the text encoder's down-projection)
+    (16, 25600, 520, "normal", 0.0, False),
     (16, 5120, 5120, "normal", 0.0, False),       # text-encoder attention projection
     (16, 5120, 17408, "outliers", 0.0, True),     # text-encoder MLP, several blocks per workgroup
 ]
@@ -137,12 +141,13 @@ def test_sweep_non_finite_row_stays_in_its_row(gpu, oracle, bad):
     assert H.rel_fro(y[keep], yo) <= TOL
 
 
-def test_sweep_prepared_equals_direct(gpu):
+@pytest.mark.parametrize("K", [5120, 25600])
+def test_sweep_prepared_equals_direct(gpu, K):
     """The two-stage API (prepare, then product) gives the one-call result bit
     for bit; the prepared form carries the group sums."""
     F = gpu
     rng = np.random.default_rng(34)
-    K, N, M = 5120, 1024, 16
+    N, M = 1024, 16
     raw = H.random_q4k(rng, N, K)
     x = rng.standard_normal((M, K)).astype(np.float32)
     direct = _sweep(F, raw, K, N, x)
@@ -157,11 +162,13 @@ def test_sweep_prepared_equals_direct(gpu):
     assert np.array_equal(dy.download(np.float32, (M, N)).view(np.uint32), direct.view(np.uint32))
 
 
-@pytest.mark.parametrize("M", [5, 16])
-def test_sweep_gate_residual_and_swiglu(gpu, oracle, M):
+@pytest.mark.parametrize("M,K", [(5, 2560), (16, 2560), (16, 8192)])
+def test_sweep_gate_residual_and_swiglu(gpu, oracle, M, K):
+    """Both epilogues, in the kernel's store and (K = 8192: two slices) in the
+    ordered sum of the slices."""
     F = gpu
-    rng = np.random.default_rng(410 + M)
-    K, Fd = 2560, 192
+    rng = np.random.default_rng(410 + M + K)
+    Fd = 192
     N = 2 * Fd
     raw = F.synth_q4k_weights(M + 17, 1, N, K, 0.05, 0.0)
     x = (rng.standard_normal((M, K)) * 3).astype(np.float32)
@@ -190,12 +197,14 @@ def test_sweep_gate_residual_and_swiglu(gpu, oracle, M):
     assert H.rel_fro(gr - h, href - h) <= TOL
 
 
-def test_sweep_graph_replay_matches_eager(gpu):
+@pytest.mark.parametrize("K", [4096, 13824])
+def test_sweep_graph_replay_matches_eager(gpu, K):
     """Captured calls replayed three times equal the eager result (the
-    prepared workspace is sized by the eager call first)."""
+    prepared workspace and, for K slices, the partial sums are sized by the
+    eager call first)."""
     F = gpu
     rng = np.random.default_rng(35)
-    K, N, M = 4096, 512, 16
+    N, M = 512, 16
     raw = H.random_q4k(rng, N, K)
     x = rng.standard_normal((M, K)).astype(np.float32)
     dw, dx = F.DeviceBuffer.from_array(raw), _buf(F, x)

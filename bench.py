@@ -247,18 +247,25 @@ def dit_blocks_streamed(ev, st, n_blocks=8, M=16384, passes=2):
 
 
 def te_other_types(ev, st, R=64):
-    """The text encoder's Q5_K / Q6_K tensors (K -> N: Q5_K 5120 -> 1024;
-    Q6_K 5120 -> 1024, 8192 -> 5120, 25600 -> 5120) at M = 1, 16 and 64
-    tokens: fh3_hip_matmul_dev, whose Q5_K / Q6_K product reads the blocks in
-    place (k_skinny).  Weights are random blocks with finite scales, rotated
-    over more than 256 MB of device copies; graph of R calls."""
+    """The text encoder's long-row Q4_K products (o-projection 8192 -> 5120,
+    down-projection 25600 -> 5120) and its Q5_K / Q6_K tensors (Q5_K 5120 ->
+    1024; Q6_K 5120 -> 1024, 8192 -> 5120, 25600 -> 5120) at M = 1, 16 and 64
+    tokens through fh3_hip_matmul_dev (Q4_K: k_gemv8, k_sweep in K slices,
+    k_skinny or k_midm by shape; Q5_K / Q6_K: k_skinny reading the blocks in
+    place).  Q4_K weights are the seeded N(0, 0.02) encoding, the others random
+    blocks with finite scales, all rotated over more than 256 MB of device
+    copies; graph of R calls."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import helpers as H
     rows = []
-    for name, K, N in (("Q5_K", 5120, 1024), ("Q6_K", 5120, 1024), ("Q6_K", 8192, 5120), ("Q6_K", 25600, 5120)):
+    for name, K, N in (("Q4_K", 8192, 5120), ("Q4_K", 25600, 5120), ("Q5_K", 5120, 1024), ("Q6_K", 5120, 1024),
+                       ("Q6_K", 8192, 5120), ("Q6_K", 25600, 5120)):
         t, _, bb, _ = H.QTYPES[name]
         rng = np.random.default_rng(t * 100 + K + N)
-        raw = H.random_blocks(rng, name, N, K, scale_lo=-12, scale_hi=-8)
+        if name == "Q4_K":
+            raw = F.synth_q4k_weights(t, K + N, N, K, 0.02, 0.0)
+        else:
+            raw = H.random_blocks(rng, name, N, K, scale_lo=-12, scale_hi=-8)
         wb = raw.nbytes
         copies = max(2, -(-(MALL_BYTES + (64 << 20)) // wb))
         ws = [F.DeviceBuffer.from_array(raw)]
@@ -280,7 +287,8 @@ def te_other_types(ev, st, R=64):
             g.launch()
             t_c = ev.time_ms(lambda i: g.launch(), 8, st) / R
             g.close()
-            rows.append({"type": name, "M": M, "K": K, "N": N, "call_us": round(t_c * 1e3, 2),
+            rows.append({"type": name, "M": M, "K": K, "N": N, "path": F.matmul_path(M, K) if name == "Q4_K" else 1,
+                         "call_us": round(t_c * 1e3, 2),
                          "weight_GBps": round(wb / (t_c * 1e-3) / 1e9, 1),
                          "hbm_frac": round((wb + 4 * M * (K + N)) / (t_c * 1e-3) / HBM_PEAK, 4)})
             log("[bench] %s M=%d K=%d N=%d call %.2f us (%.0f GB/s of weights)"
@@ -611,10 +619,10 @@ def main():
     extra["gemv"] = per_gemv
 
     try:
-        extra["te_q5k_q6k"] = te_other_types(ev, st)
+        extra["te_long_rows_and_q5k_q6k"] = te_other_types(ev, st)
     except Exception as e:  # keep the headline line when this leg fails
         log("[bench] Q5_K / Q6_K leg failed: %r" % (e,))
-        extra["te_q5k_q6k"] = {"error": repr(e)}
+        extra["te_long_rows_and_q5k_q6k"] = {"error": repr(e)}
 
     # ---------------- DiT attention branch ---------------------------------
     roofline_attn = None

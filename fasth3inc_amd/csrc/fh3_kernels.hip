@@ -2702,11 +2702,23 @@ __global__ __launch_bounds__(256) void k_midm_sum(const float *__restrict__ part
     const int t = (int)(i / width), o = (int)(i - (int64_t)t * width);
     const size_t mn = (size_t)M * N;
     const float *p = part + (size_t)t * N + o;
-    float s = p[0];
-    for (int k = 1; k < S; k++) s += p[k * mn];
+    // the windows' partials are loaded eight at a time before they are added
+    // (in window order), so their latencies overlap
+    auto ordered_sum = [&](const float *q) {
+        float s = 0.f;
+        for (int k0 = 0; k0 < S; k0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = k0 + k < S ? q[(size_t)(k0 + k) * mn] : 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (k0 + k < S) s = k0 + k == 0 ? v[0] : s + v[k];
+        }
+        return s;
+    };
+    const float s = ordered_sum(p);
     if (epi == EPI_SWIGLU) {
-        float sg = p[F];
-        for (int k = 1; k < S; k++) sg += p[k * mn + F];
+        const float sg = ordered_sum(p + F);
         const float bv = bias ? bias[o] : 0.f, bg = bias ? bias[F + o] : 0.f;
         Y[(size_t)t * F + o] = (s * xs_inv[t] + bv) * silu_f32(sg * xs_inv[t] + bg);
         return;

@@ -15,6 +15,10 @@ Workloads (each launch sequence is preceded by one untimed warmup launch):
          2-decade per-super-block scale spread, down K=13824 -> N=5120 on
          SiLU-gated activations): fh3_hip_matmul_prepared_dev -> k_gemm, and
          the activation prep k_xprep_r8
+  te     the text encoder's long Q4_K rows at M = 1 and 16 (o-projection
+         K=8192 -> N=5120, down-projection K=25600 -> N=5120):
+         fh3_hip_matmul_prepared_dev -> k_gemv8 (M = 1, K = 8192) or k_sweep in
+         K slices then k_midm_sum; weights rotated as for gemv
   copy   hipMemcpy device-to-device of 256 MiB: a copy of known size that
          calibrates FETCH_SIZE / WRITE_SIZE against the bytes moved
   attn   the DiT attention branch at n = 16384 tokens, 40 heads of 128
@@ -51,6 +55,24 @@ def gemv(reps):
                 F.matmul_prepared_dev(ws[i % copies], K, N, prep, dy, M)
             F.synchronize()
             print("gemv M=%d N=%d K=%d: %d launches, %d weight copies" % (M, N, K, reps, copies), flush=True)
+            for b in ws + [dx, dy, prep]:
+                b.close()
+
+
+def te(reps):
+    for K, N in ((8192, 5120), (25600, 5120)):
+        for M in (1, 16):
+            raw = F.synth_q4k_weights(0, 100 + N + K, N, K, 0.02, 0.0)
+            copies = max(2, -(-(MALL_BYTES + (64 << 20)) // raw.nbytes))
+            ws = [F.DeviceBuffer.from_array(raw) for _ in range(copies)]
+            dx = F.DeviceBuffer.from_array(F.synth_x("normal", 0, 200 + M, M, K))
+            dy = F.DeviceBuffer(M * N * 4)
+            prep = F.DeviceBuffer(F.prepared_bytes(M, K))
+            F.prepare_x_dev(dx, M, K, prep)
+            for i in range(reps + 1):
+                F.matmul_prepared_dev(ws[i % copies], K, N, prep, dy, M)
+            F.synchronize()
+            print("te M=%d N=%d K=%d path %d: %d launches" % (M, N, K, F.matmul_path(M, K), reps), flush=True)
             for b in ws + [dx, dy, prep]:
                 b.close()
 
@@ -137,7 +159,7 @@ def vsa(reps, heads=56, hd=128, rot=96):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("workload", choices=("gemv", "gemm", "mlp", "copy", "attn", "vsa", "all"))
+    ap.add_argument("workload", choices=("gemv", "te", "gemm", "mlp", "copy", "attn", "vsa", "all"))
     ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args(argv)
     F.init(0)

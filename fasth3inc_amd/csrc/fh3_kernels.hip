@@ -13,7 +13,7 @@
 //                       C super-blocks, exact weights (sc*q in fp16), two
 //                       v_mfma_f32_16x16x32_f16 chains, LDS reduce over the slices;
 //                       Q4_K, Q5_K or Q6_K blocks read in place
-//   k_sweep<C>          up to 16 tokens: k_skinny's exact weights, persistent
+//   k_sweep<C,TB>       up to 32 tokens: k_skinny's exact weights, persistent
 //                       workgroups with the activations held in registers, the
 //                       offsets from precomputed group sums (f32 MFMA); long
 //                       rows in K slices added by k_midm_sum
@@ -994,7 +994,7 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) vo
 }
 
 // ---------------------------------------------------------------------------
-// Small-M sweep (k_sweep): one token block (M <= 16), persistent.  k_skinny
+// Small-M sweep (k_sweep): TB token blocks (M <= 16 TB), persistent.  k_skinny
 // reads a wavefront's activation fragments again for every 16-row block (as
 // many bytes of fp16 activations per super-block as the Q4_K weights it
 // multiplies, 16 tokens x 256 k x 2 B against 144 B x 16 rows); here each
@@ -1023,14 +1023,17 @@ __device__ __forceinline__ half2v magic_fma2(uint32_t a, uint32_t sel, half2v s,
     return __builtin_elementwise_fma(q4k_magic_pair(a, sel), s, ns);
 }
 
-// sum_k (sc*q)_k x_k of one super-block for 16 tokens x 16 weight rows (A:
-// skinny_load_a's fragments; lane (row j, chunk c) holds chunk c of row j)
-__device__ __forceinline__ f32x4 sweep_scq(const u32x4 hv, const u32x4 ca, const u32x4 cb, const Q4kField flo,
-                                           const Q4kField fhi, const half8 (&a)[8][1]) {
+// sum_k (sc*q)_k x_k of one super-block for TB blocks of 16 tokens x 16
+// weight rows (A: skinny_load_a's fragments; lane (row j, chunk c) holds chunk
+// c of row j); each B operand is built once and used by every token block
+template <int TB>
+__device__ __forceinline__ void sweep_scq(const u32x4 hv, const u32x4 ca, const u32x4 cb, const Q4kField flo,
+                                          const Q4kField fhi, const half8 (&a)[8][TB], f32x4 (&aq)[TB]) {
     const uint32_t sclo = q4k_sc(hv, flo), schi = q4k_sc(hv, fhi);
     const half2v s_lo = splat2(sclo), ns_lo = s_lo * (_Float16)-1024.0f;
     const half2v s_hi = splat2(schi) * (_Float16)0.0625f, ns_hi = splat2(schi) * (_Float16)-64.0f;
-    f32x4 aq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++) aq[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < 8; m++) {
         const int part = m & 3;
@@ -1042,18 +1045,18 @@ __device__ __forceinline__ f32x4 sweep_scq(const u32x4 hv, const u32x4 ca, const
         const half2v p0 = magic_fma2(u0, 0x04010400u, s, ns), p1 = magic_fma2(u0, 0x04030402u, s, ns);
         const half2v p2 = magic_fma2(u1, 0x04010400u, s, ns), p3 = magic_fma2(u1, 0x04030402u, s, ns);
         const half8 b = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-        aq = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][0], b, aq, 0, 0, 0);
+#pragma unroll
+        for (int tb = 0; tb < TB; tb++) aq[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][tb], b, aq[tb], 0, 0, 0);
     }
-    return aq;
 }
 
-template <int C, int LB, int EPI>
+template <int C, int TB, int LB, int EPI>
 __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int K,
                                               const half8 *__restrict__ X16, const float *__restrict__ xs_inv,
                                               const float *__restrict__ xsum, const float *__restrict__ bias,
                                               float *__restrict__ Y, int M, const float *__restrict__ aux, int nblk,
                                               int S, float *__restrict__ part) {
-    extern __shared__ f32x4 red[];  // [2][NW][64]
+    extern __shared__ f32x4 red[];  // [2][NW][TB][64]
     const int NW = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1090,19 +1093,27 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
             cb[s] = ld16(wc + s * 144 + 16);
         }
     }
-    // A fragments and group sums of the window for token j (padding tokens
-    // re-read the last real row; their outputs are never stored)
-    half8 a[C][8][1];
-    float xg[C][2];
+    // A fragments and group sums of the window for tokens 16 tb + j (padding
+    // tokens re-read the last real row; their outputs are never stored)
+    half8 a[C][8][TB];
+    float xg[C][TB][2];
     {
-        const int t = j < M ? j : M - 1;
-        const half8 *xq[1] = {X16 + ((size_t)(t >> 5) * kf_n + (size_t)(sbb + s0) * 16 + 4 * q) * 64 + (t & 31)};
-        const float *xs = xsum + (size_t)t * (K >> 5) + (size_t)(sbb + s0) * 8 + q;
+        const half8 *xq[TB];
+        const float *xs[TB];
+#pragma unroll
+        for (int tb = 0; tb < TB; tb++) {
+            const int t = 16 * tb + j < M ? 16 * tb + j : M - 1;
+            xq[tb] = X16 + ((size_t)(t >> 5) * kf_n + (size_t)(sbb + s0) * 16 + 4 * q) * 64 + (t & 31);
+            xs[tb] = xsum + (size_t)t * (K >> 5) + (size_t)(sbb + s0) * 8 + q;
+        }
 #pragma unroll
         for (int i = 0; i < C; i++) {
-            skinny_load_a<1>(xq, i, a[i]);
-            xg[i][0] = xs[i * 8];
-            xg[i][1] = xs[i * 8 + 4];
+            skinny_load_a<TB>(xq, i, a[i]);
+#pragma unroll
+            for (int tb = 0; tb < TB; tb++) {
+                xg[i][tb][0] = xs[tb][i * 8];
+                xg[i][tb][1] = xs[tb][i * 8 + 4];
+            }
         }
     }
     // scale fields of groups 2q (low nibbles) and 2q + 1, min fields of groups
@@ -1112,22 +1123,22 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
 
     // the output this thread stores after each block, if any: lane st_l of
     // the 16x16 result holds column st_l % 16 and tokens 4 (st_l / 16) + v.
-    // With fewer than four wavefronts (in <= 1536) the threads of the
-    // workgroup take the 256 outputs in turn (st_all).
-    const bool st_all = blockDim.x < 256 || part;
+    // With fewer than four wavefronts (in <= 1536), or two token blocks, the
+    // threads of the workgroup take the TB x 256 outputs in turn (st_all).
+    const bool st_all = blockDim.x < 256 || part || TB > 1;
     const int st_l = (int)threadIdx.x & 63, st_v = (int)threadIdx.x >> 6;
     const int st_t = 4 * (st_l >> 4) + st_v, st_j = st_l & 15;
     const bool storer = !st_all && (int)threadIdx.x < 256 && st_t < M && (EPI != EPI_SWIGLU || st_j < 8);
     const size_t mn = (size_t)M * N;
     const float st_xs = storer ? xs_inv[st_t] : 0.f;
     // one output (token t, column o = o0 + jj) from the NW partial sums of
-    // result lane l, register v
+    // result lane l, register v (rb: this token block's [NW][TB][64] slice)
     auto store = [&](const f32x4 *rb, int l, int v, int t, int o, float xs, float b, float bg, float ax, float y0) {
         float s = rb[l][v];
-        for (int w = 1; w < NW; w++) s += rb[w * 64 + l][v];
+        for (int w = 1; w < NW; w++) s += rb[w * TB * 64 + l][v];
         if (EPI == EPI_SWIGLU) {  // the gate of column l % 16 is row l % 16 + 8 of the block
             float sg = rb[l + 8][v];
-            for (int w = 1; w < NW; w++) sg += rb[w * 64 + l + 8][v];
+            for (int w = 1; w < NW; w++) sg += rb[w * TB * 64 + l + 8][v];
             Y[(size_t)t * F + o] = (s * xs + b) * silu_f32(sg * xs + bg);
         } else if (EPI == EPI_GATE_RES) {
             Y[(size_t)t * N + o] = __builtin_fmaf(ax, s * xs + b, y0);
@@ -1152,7 +1163,9 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
                 e_y = Y[(size_t)st_t * N + st_o];
             }
         }
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f}, accm = {0.f, 0.f, 0.f, 0.f};
+        f32x4 acc[TB], accm[TB];
+#pragma unroll
+        for (int tb = 0; tb < TB; tb++) acc[tb] = accm[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
         const uint8_t *nh = wptr(MORE ? it + 1 : it), *nc = nh + 16 + 32 * q;
 #pragma unroll
         for (int i = 0; i < C; i++) {
@@ -1160,39 +1173,47 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
             const bool valid = s0 + i >= own;
             const float d = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xFFFFu)) : 0.f;
             const float dmin = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x >> 16)) : 0.f;
-            const f32x4 aq = sweep_scq(h, ca[i], cb[i], flo, fhi, a[i]);
-#pragma unroll
-            for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf(d, aq[v], acc[v]);
+            f32x4 aq[TB];
+            sweep_scq<TB>(h, ca[i], cb[i], flo, fhi, a[i], aq);
             const float bm0 = dmin * (float)q4k_mn(h, fm0), bm1 = dmin * (float)q4k_mn(h, fm1);
-            accm = __builtin_amdgcn_mfma_f32_16x16x4f32(xg[i][0], bm0, accm, 0, 0, 0);
-            accm = __builtin_amdgcn_mfma_f32_16x16x4f32(xg[i][1], bm1, accm, 0, 0, 0);
+#pragma unroll
+            for (int tb = 0; tb < TB; tb++) {
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[tb][v] = __builtin_fmaf(d, aq[tb][v], acc[tb][v]);
+                accm[tb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xg[i][tb][0], bm0, accm[tb], 0, 0, 0);
+                accm[tb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xg[i][tb][1], bm1, accm[tb], 0, 0, 0);
+            }
             if (MORE) {
                 hv[i] = ld16(nh + i * 144);
                 ca[i] = ld16(nc + i * 144);
                 cb[i] = ld16(nc + i * 144 + 16);
             }
         }
-        f32x4 *rb = red + (it & 1) * NW * 64;  // alternate buffers: one barrier per block
-        rb[wave * 64 + lane] = acc - accm;
+        f32x4 *rb = red + (it & 1) * NW * TB * 64;  // alternate buffers: one barrier per block
+#pragma unroll
+        for (int tb = 0; tb < TB; tb++) rb[(wave * TB + tb) * 64 + lane] = acc[tb] - accm[tb];
         __syncthreads();
         if (st_ok) store(rb, st_l, st_v, st_t, st_o, st_xs, e_b, e_bg, e_aux, e_y);
         if (part) {  // K slices: this slice's raw sums of every row of the block
-            for (int idx = (int)threadIdx.x; idx < 256; idx += (int)blockDim.x) {
-                const int l = idx & 63, v = idx >> 6, t = 4 * (l >> 4) + v, jj = l & 15;
+            for (int idx = (int)threadIdx.x; idx < TB * 256; idx += (int)blockDim.x) {
+                const int tb = idx >> 8, l = idx & 63, v = (idx >> 6) & 3, jj = l & 15;
+                const int t = 16 * tb + 4 * (l >> 4) + v;
                 const int col = EPI == EPI_SWIGLU ? o0 + (jj & 7) : o0 + jj;
                 if (t >= M || col >= (EPI == EPI_SWIGLU ? F : N)) continue;
-                float sv = rb[l][v];
-                for (int w = 1; w < NW; w++) sv += rb[w * 64 + l][v];
+                const f32x4 *rt = rb + tb * 64;
+                float sv = rt[l][v];
+                for (int w = 1; w < NW; w++) sv += rt[w * TB * 64 + l][v];
                 part[(size_t)ks * mn + (size_t)t * N + (EPI == EPI_SWIGLU && jj >= 8 ? F + col : col)] = sv;
             }
         } else if (st_all) {
-            for (int idx = (int)threadIdx.x; idx < 256; idx += (int)blockDim.x) {
-                const int l = idx & 63, v = idx >> 6, t = 4 * (l >> 4) + v, o = o0 + (l & 15);
+            for (int idx = (int)threadIdx.x; idx < TB * 256; idx += (int)blockDim.x) {
+                const int tb = idx >> 8, l = idx & 63, v = (idx >> 6) & 3;
+                const int t = 16 * tb + 4 * (l >> 4) + v, o = o0 + (l & 15);
                 if (t >= M || o >= N || (EPI == EPI_SWIGLU && (l & 15) >= 8)) continue;
                 const float b = bias ? bias[o] : 0.f, bg = (bias && EPI == EPI_SWIGLU) ? bias[F + o] : 0.f;
                 const float ax = EPI == EPI_GATE_RES ? aux[(size_t)t * N + o] : 0.f;
                 const float y0 = EPI == EPI_GATE_RES ? Y[(size_t)t * N + o] : 0.f;
-                store(rb, l, v, t, o, xs_inv[t], b, bg, ax, y0);
+                store(rb + tb * 64, l, v, t, o, xs_inv[t], b, bg, ax, y0);
             }
         }
     };
@@ -2491,28 +2512,33 @@ extern "C" hipError_t fh3k_gemv8(const void *W, int64_t row_bytes, int N, int K,
     return fh3k_gemv8_epi(W, row_bytes, N, K, x, bias, y, M, EPI_NONE, nullptr, st);
 }
 
-// k_sweep: C = 2 super-blocks per wavefront over K slices of at most 20
-// super-blocks, so at most 10 wavefronts at <= 168 VGPRs (about 160 used; C =
-// 3 would spill).  Rows longer than 20 super-blocks (to K = 32768) are split
-// into S slices whose raw sums go to part[S][M][N] and are added in slice
-// order by k_midm_sum (slices of at most 20 measured best: at K = 8192 two
-// slices of 16 beat one of 32 by 3-10 %, at K = 25600 five of 20 beat four of
-// 25 and seven of 15; K = 5120 stays whole).
-static void sweep_split(int nsb, int &S, int &SL) {
-    S = (nsb + 19) / 20;
+// k_sweep: up to 16 tokens (one token block) with C = 2 super-blocks per
+// wavefront, 17..32 tokens (two token blocks) with C = 1; either way the
+// activation fragments of a wavefront's window take 64 VGPRs and at most 10
+// wavefronts run at <= 168 VGPRs (about 160 used; C = 3 would spill), so a
+// K slice holds at most 10 C super-blocks.  Longer rows (to K = 32768) are
+// split into S equal slices whose raw sums go to part[S][M][N] and are added
+// in slice order by k_midm_sum (slices of at most 20 measured best for one
+// token block: at K = 8192 two slices of 16 beat one of 32 by 3-10 %, at
+// K = 25600 five of 20 beat four of 25 and seven of 15; K = 5120 stays whole).
+static int sweep_tb(int M) { return M > 16 ? 2 : 1; }
+
+static void sweep_split(int nsb, int M, int &S, int &SL) {
+    const int cap = 10 * (3 - sweep_tb(M));  // 20 (one token block) or 10 (two)
+    S = (nsb + cap - 1) / cap;
     SL = (nsb + S - 1) / S;
 }
 
-extern "C" int fh3k_sweep_max_tokens(void) { return 16; }
+extern "C" int fh3k_sweep_max_tokens(void) { return 32; }
 
 extern "C" int fh3k_sweep_fits(int K, int M) {
-    return M >= 1 && M <= 16 && K >= 512 && K <= 32768 && K % 256 == 0;
+    return M >= 1 && M <= 32 && K >= 512 && K <= 32768 && K % 256 == 0;
 }
 
 extern "C" size_t fh3k_sweep_part_bytes(int N, int K, int M) {
     int S, SL;
     if (!fh3k_sweep_fits(K, M) || N < 1) return 0;
-    sweep_split(K / 256, S, SL);
+    sweep_split(K / 256, M, S, SL);
     return S > 1 ? (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
@@ -2522,21 +2548,20 @@ __global__ __launch_bounds__(256) void k_midm_sum(const float *__restrict__ part
                                                   float *__restrict__ Y, int epi, const float *__restrict__ aux);
 }  // namespace
 
-template <int EPI>
-static hipError_t launch_sweep_e(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,
+template <int C, int TB, int EPI>
+static hipError_t launch_sweep_c(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,
                                  const float *xsum, const float *bias, float *y, int M, const float *aux, float *part,
                                  hipStream_t st) {
-    constexpr int C = 2;
     int S, SL;
-    sweep_split(K / 256, S, SL);
+    sweep_split(K / 256, M, S, SL);
     const int NW = (SL + C - 1) / C;
     const int nblk = (int)row_blocks16(N, EPI);
     const int per = device_cus() / S;  // workgroups per slice
     const int grid = (nblk < per ? nblk : per) * S;
-    const size_t lds = 2 * (size_t)NW * 64 * sizeof(f32x4);
-    if (NW * 64 > 640 || nblk < 1 || grid < S || (S > 1 && !part)) return hipErrorInvalidValue;
+    const size_t lds = 2 * (size_t)NW * TB * 64 * sizeof(f32x4);
+    if (NW * 64 > 640 || SL < C || nblk < 1 || grid < S || (S > 1 && !part)) return hipErrorInvalidValue;
     float *pp = S > 1 ? part : nullptr;
-    hipLaunchKernelGGL((k_sweep<C, 768, EPI>), dim3(grid), dim3(NW * 64), lds, st, (const uint8_t *)W, rb, N, K,
+    hipLaunchKernelGGL((k_sweep<C, TB, 768, EPI>), dim3(grid), dim3(NW * 64), lds, st, (const uint8_t *)W, rb, N, K,
                        (const half8 *)x16, xs_inv, xsum, bias, y, M, aux, nblk, S, pp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || S == 1) return e;
@@ -2544,6 +2569,15 @@ static hipError_t launch_sweep_e(const void *W, int64_t rb, int N, int K, const 
     hipLaunchKernelGGL(k_midm_sum, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, st, part, S, M, N, xs_inv,
                        bias, y, EPI, aux);
     return hipGetLastError();
+}
+
+template <int EPI>
+static hipError_t launch_sweep_e(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,
+                                 const float *xsum, const float *bias, float *y, int M, const float *aux, float *part,
+                                 hipStream_t st) {
+    if (sweep_tb(M) == 1)
+        return launch_sweep_c<2, 1, EPI>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
+    return launch_sweep_c<1, 2, EPI>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
 }
 
 extern "C" hipError_t fh3k_sweep_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16,

@@ -78,7 +78,7 @@ int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok,
  * same normalised rows) or that time the product kernel alone.
  *   fh3_hip_prepared_bytes: device bytes a prepared buffer for n_tok x in
  *     needs (fragments of round_up(n_tok, 256) rows, fp16, plus one fp32 scale
- *     per row, plus for n_tok <= 16 one fp32 sum per 32-value group);
+ *     per row, plus for n_tok <= 32 one fp32 sum per 32-value group);
  *   fh3_hip_prepare_x_dev: fill d_prep (16-byte aligned) from d_x[n_tok][in];
  *   fh3_hip_matmul_prepared_dev: the product from a prepared buffer; same
  *     results as fh3_hip_matmul_dev.  Its only library workspace is the
@@ -237,7 +237,7 @@ int fh3_hip_matmul_noalloc_dev(const Fh3W *w, const float *d_x, float *d_y, int 
  *     planes, one power-of-two scale per token and wavefront window) inside
  *     the kernel, integer MFMA on the raw 4-bit weights, no preparation launch
  *     and no workspace;
- *   - FH3_HIP_PATH_SWEEP for the other n_tok <= 16 when 512 <= in <= 32768:
+ *   - FH3_HIP_PATH_SWEEP for the other n_tok <= 32 when 512 <= in <= 32768:
  *     fp16 activations with their group sums (prepared), exact fp16 sc*q
  *     weights, persistent workgroups that keep each wavefront's activations in
  *     registers while they sweep the weight rows; rows of more than 5120

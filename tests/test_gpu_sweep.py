@@ -1,5 +1,5 @@
-"""GPU parity of the persistent small-M kernel (FH3_HIP_PATH_SWEEP: up to 16
-tokens, 512 <= K <= 32768; fp16 activations held in registers, exact fp16
+"""GPU parity of the persistent small-M kernel (FH3_HIP_PATH_SWEEP: up to 32
+tokens in one or two token blocks, 512 <= K <= 32768; fp16 activations held in registers, exact fp16
 sc*q weights, the offsets dmin*m from the prepared group sums; rows of more
 than 20 super-blocks in K slices whose partial sums are added in slice order)
 against the CPU oracle, through the C-ABI.
@@ -57,6 +57,10 @@ CASES = [
     (3, 13824, 130, "outliers", 0.0, False),      # three slices (18 each); past the int8 kernel's window
     (1, 25600, 64, "normal", 2.0, True),          # five slices of 20 (the text encoder's down-projection)
     (16, 25600, 520, "normal", 0.0, False),
+    (17, 1024, 48, "normal", 0.0, True),          # two token blocks, one super-block per wavefront
+    (24, 5120, 300, "outliers", 1.0, False),      # two token blocks, two K slices
+    (32, 5120, 17408, "normal", 0.0, True),       # text-encoder MLP shape at 32 tokens (sampled rows)
+    (29, 25600, 200, "silu_gated", 2.0, False),   # two token blocks in ten slices of ten super-blocks
     (16, 5120, 5120, "normal", 0.0, False),       # text-encoder attention projection
     (16, 5120, 17408, "outliers", 0.0, True),     # text-encoder MLP, several blocks per workgroup
 ]
@@ -141,13 +145,13 @@ def test_sweep_non_finite_row_stays_in_its_row(gpu, oracle, bad):
     assert H.rel_fro(y[keep], yo) <= TOL
 
 
-@pytest.mark.parametrize("K", [5120, 25600])
-def test_sweep_prepared_equals_direct(gpu, K):
+@pytest.mark.parametrize("K,M", [(5120, 16), (25600, 16), (5120, 32)])
+def test_sweep_prepared_equals_direct(gpu, K, M):
     """The two-stage API (prepare, then product) gives the one-call result bit
     for bit; the prepared form carries the group sums."""
     F = gpu
     rng = np.random.default_rng(34)
-    N, M = 1024, 16
+    N = 1024
     raw = H.random_q4k(rng, N, K)
     x = rng.standard_normal((M, K)).astype(np.float32)
     direct = _sweep(F, raw, K, N, x)
@@ -162,10 +166,10 @@ def test_sweep_prepared_equals_direct(gpu, K):
     assert np.array_equal(dy.download(np.float32, (M, N)).view(np.uint32), direct.view(np.uint32))
 
 
-@pytest.mark.parametrize("M,K", [(5, 2560), (16, 2560), (16, 8192)])
+@pytest.mark.parametrize("M,K", [(5, 2560), (16, 2560), (16, 8192), (32, 2560), (20, 8192)])
 def test_sweep_gate_residual_and_swiglu(gpu, oracle, M, K):
-    """Both epilogues, in the kernel's store and (K = 8192: two slices) in the
-    ordered sum of the slices."""
+    """Both epilogues, in the kernel's store and (K slices) in the ordered sum
+    of the slices, for one and two token blocks."""
     F = gpu
     rng = np.random.default_rng(410 + M + K)
     Fd = 192
@@ -197,14 +201,14 @@ def test_sweep_gate_residual_and_swiglu(gpu, oracle, M, K):
     assert H.rel_fro(gr - h, href - h) <= TOL
 
 
-@pytest.mark.parametrize("K", [4096, 13824])
-def test_sweep_graph_replay_matches_eager(gpu, K):
+@pytest.mark.parametrize("K,M", [(4096, 16), (13824, 16), (4096, 32)])
+def test_sweep_graph_replay_matches_eager(gpu, K, M):
     """Captured calls replayed three times equal the eager result (the
     prepared workspace and, for K slices, the partial sums are sized by the
     eager call first)."""
     F = gpu
     rng = np.random.default_rng(35)
-    N, M = 512, 16
+    N = 512
     raw = H.random_q4k(rng, N, K)
     x = rng.standard_normal((M, K)).astype(np.float32)
     dw, dx = F.DeviceBuffer.from_array(raw), _buf(F, x)

@@ -133,13 +133,16 @@ int choose_path(int n_tok, int64_t in) {
     if (g.path == FH3_HIP_PATH_MIDM && n_tok <= fh3k_midm_max_tokens()) return FH3_HIP_PATH_MIDM;
     if (g.path == FH3_HIP_PATH_GEMM) return FH3_HIP_PATH_GEMM;
     if (g8) return FH3_HIP_PATH_GEMV8;
-    // up to 32 tokens: the persistent kernel that keeps the activations in
-    // registers, long rows in K slices (measured 10-20 % faster than k_skinny
-    // at M = 16, K = 5120, 1.2-1.5x at K = 25600; at 17..32 tokens 6-25 %
-    // faster than k_skinny and k_midm at K = 5120, 1.2-1.3x over k_midm at
-    // K = 25600)
-    if (sw) return FH3_HIP_PATH_SWEEP;
-    // long rows (K >= 8192) with 33..64 tokens: the split-K kernel reads the
+    // up to 16 tokens, and up to 64 on rows of at least 5120: the persistent
+    // kernel that keeps the activations in registers, long rows in K slices
+    // (measured 10-20 % faster than k_skinny at M = 16, K = 5120, 1.2-1.5x at
+    // K = 25600; at 17..64 tokens 0-25 % faster than k_skinny and k_midm at
+    // K = 5120, 1.1-1.4x over k_midm at K = 25600; at K = 4096 more than 16
+    // tokens need a K split and the ordered sum, and k_skinny is 10-15 %
+    // faster)
+    if (sw && (n_tok <= 16 || in >= 5120)) return FH3_HIP_PATH_SWEEP;
+    // long rows (K >= 8192) with 17..64 tokens (when not taken above): the
+    // split-K kernel reads the
     // activations once per 128 rows instead of once per 16 (measured 25-45 %
     // faster at K = 13824; slower than k_skinny at K <= 5120)
     if (n_tok > 16 && n_tok <= fh3k_midm_max_tokens() && in >= 8192) return FH3_HIP_PATH_MIDM;
@@ -420,7 +423,7 @@ static int check_weights(const Fh3W *w, const char *fn) {
 }
 
 // Prepared-activation layout: fragments of Mpad = round_up(n_tok, 256) rows,
-// then Mpad fp32 inverse scales at a 256-byte aligned offset, then (up to 32
+// then Mpad fp32 inverse scales at a 256-byte aligned offset, then (up to 64
 // tokens) the fp32 sums of each 32-value group, [n_tok][in / 32], at the next
 // 256-byte boundary: the FH3_HIP_PATH_SWEEP kernel's offsets.
 static int64_t prep_rows(int n_tok) { return round_up(n_tok, fh3k_gemm_row_pad()); }

@@ -13,7 +13,7 @@
 //                       C super-blocks, exact weights (sc*q in fp16), two
 //                       v_mfma_f32_16x16x32_f16 chains, LDS reduce over the slices;
 //                       Q4_K, Q5_K or Q6_K blocks read in place
-//   k_sweep<C,TB>       up to 32 tokens: k_skinny's exact weights, persistent
+//   k_sweep<C,TB>       up to 64 tokens: k_skinny's exact weights, persistent
 //                       workgroups with the activations held in registers, the
 //                       offsets from precomputed group sums (f32 MFMA); long
 //                       rows in K slices added by k_midm_sum
@@ -2521,18 +2521,19 @@ extern "C" hipError_t fh3k_gemv8(const void *W, int64_t row_bytes, int N, int K,
 // in slice order by k_midm_sum (slices of at most 20 measured best for one
 // token block: at K = 8192 two slices of 16 beat one of 32 by 3-10 %, at
 // K = 25600 five of 20 beat four of 25 and seven of 15; K = 5120 stays whole).
-static int sweep_tb(int M) { return M > 16 ? 2 : 1; }
+static int sweep_tb(int M) { return (M + 15) / 16; }
 
 static void sweep_split(int nsb, int M, int &S, int &SL) {
-    const int cap = 10 * (3 - sweep_tb(M));  // 20 (one token block) or 10 (two)
+    const int tb = sweep_tb(M);
+    const int cap = tb == 1 ? 20 : (tb == 2 ? 10 : 8);
     S = (nsb + cap - 1) / cap;
     SL = (nsb + S - 1) / S;
 }
 
-extern "C" int fh3k_sweep_max_tokens(void) { return 32; }
+extern "C" int fh3k_sweep_max_tokens(void) { return 64; }
 
 extern "C" int fh3k_sweep_fits(int K, int M) {
-    return M >= 1 && M <= 32 && K >= 512 && K <= 32768 && K % 256 == 0;
+    return M >= 1 && M <= 64 && K >= 512 && K <= 32768 && K % 256 == 0;
 }
 
 extern "C" size_t fh3k_sweep_part_bytes(int N, int K, int M) {
@@ -2548,7 +2549,7 @@ __global__ __launch_bounds__(256) void k_midm_sum(const float *__restrict__ part
                                                   float *__restrict__ Y, int epi, const float *__restrict__ aux);
 }  // namespace
 
-template <int C, int TB, int EPI>
+template <int C, int TB, int LB, int EPI>
 static hipError_t launch_sweep_c(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,
                                  const float *xsum, const float *bias, float *y, int M, const float *aux, float *part,
                                  hipStream_t st) {
@@ -2559,9 +2560,10 @@ static hipError_t launch_sweep_c(const void *W, int64_t rb, int N, int K, const 
     const int per = device_cus() / S;  // workgroups per slice
     const int grid = (nblk < per ? nblk : per) * S;
     const size_t lds = 2 * (size_t)NW * TB * 64 * sizeof(f32x4);
-    if (NW * 64 > 640 || SL < C || nblk < 1 || grid < S || (S > 1 && !part)) return hipErrorInvalidValue;
+    if (NW * 64 > (LB < 640 ? LB : 640) || SL < C || nblk < 1 || grid < S || (S > 1 && !part))
+        return hipErrorInvalidValue;
     float *pp = S > 1 ? part : nullptr;
-    hipLaunchKernelGGL((k_sweep<C, TB, 768, EPI>), dim3(grid), dim3(NW * 64), lds, st, (const uint8_t *)W, rb, N, K,
+    hipLaunchKernelGGL((k_sweep<C, TB, LB, EPI>), dim3(grid), dim3(NW * 64), lds, st, (const uint8_t *)W, rb, N, K,
                        (const half8 *)x16, xs_inv, xsum, bias, y, M, aux, nblk, S, pp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || S == 1) return e;
@@ -2575,9 +2577,14 @@ template <int EPI>
 static hipError_t launch_sweep_e(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,
                                  const float *xsum, const float *bias, float *y, int M, const float *aux, float *part,
                                  hipStream_t st) {
-    if (sweep_tb(M) == 1)
-        return launch_sweep_c<2, 1, EPI>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
-    return launch_sweep_c<1, 2, EPI>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
+    switch (sweep_tb(M)) {
+        case 1: return launch_sweep_c<2, 1, 768, EPI>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
+        case 2: return launch_sweep_c<1, 2, 768, EPI>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
+        // three or four token blocks: 96 / 128 VGPRs of activations, so at most
+        // 8 wavefronts (two per SIMD, 256 VGPRs each)
+        case 3: return launch_sweep_c<1, 3, 512, EPI>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
+        default: return launch_sweep_c<1, 4, 512, EPI>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
+    }
 }
 
 extern "C" hipError_t fh3k_sweep_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16,

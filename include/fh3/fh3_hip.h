@@ -78,7 +78,7 @@ int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok,
  * same normalised rows) or that time the product kernel alone.
  *   fh3_hip_prepared_bytes: device bytes a prepared buffer for n_tok x in
  *     needs (fragments of round_up(n_tok, 256) rows, fp16, plus one fp32 scale
- *     per row, plus for n_tok <= 32 one fp32 sum per 32-value group);
+ *     per row, plus for n_tok <= 64 one fp32 sum per 32-value group);
  *   fh3_hip_prepare_x_dev: fill d_prep (16-byte aligned) from d_x[n_tok][in];
  *   fh3_hip_matmul_prepared_dev: the product from a prepared buffer; same
  *     results as fh3_hip_matmul_dev.  Its only library workspace is the
@@ -237,16 +237,16 @@ int fh3_hip_matmul_noalloc_dev(const Fh3W *w, const float *d_x, float *d_y, int 
  *     planes, one power-of-two scale per token and wavefront window) inside
  *     the kernel, integer MFMA on the raw 4-bit weights, no preparation launch
  *     and no workspace;
- *   - FH3_HIP_PATH_SWEEP for the other n_tok <= 32 when 512 <= in <= 32768:
+ *   - FH3_HIP_PATH_SWEEP for the other n_tok <= 16 when 512 <= in <= 32768,
+ *     and n_tok <= 64 when 5120 <= in <= 32768:
  *     fp16 activations with their group sums (prepared), exact fp16 sc*q
  *     weights, persistent workgroups that keep each wavefront's activations in
  *     registers while they sweep the weight rows; rows of more than 5120
  *     weights are split into K slices whose partial sums (library workspace,
  *     see fh3_hip_matmul_workspace_bytes) are added in slice order;
- *   - FH3_HIP_PATH_MIDM for 17 <= n_tok <= 64 and in >= 8192: K split into
- *     windows over 128-row workgroups that share staged activations, partial
- *     sums in a library workspace, then an ordered sum (any n_tok <= 64 when
- *     forced);
+ *   - FH3_HIP_PATH_MIDM only when forced (n_tok <= 64): K split into windows
+ *     over 128-row workgroups that share staged activations, partial sums in
+ *     a library workspace, then an ordered sum;
  *   - FH3_HIP_PATH_SKINNY (fp16 activations, exact fp16 sc*q weights) for
  *     the other n_tok <= fh3_hip_skinny_max();
  *   - FH3_HIP_PATH_GEMM above.

@@ -109,9 +109,8 @@ def test_matmul_path_selection(fh3):
     """Kernel family per shape (host-side decision, no GPU call): the int8
     kernel takes one to four tokens while its window fits (K <= 20480 for one
     or two tokens, K <= 12288 for three or four), the persistent fp16 sweep up
-    to 32 tokens for 512 <= K <= 32768 (long rows in K slices), the split-K
-    kernel for 33..64 tokens on rows of K >= 8192, the fp16 GEMV up to 64
-    tokens, the
+    to 16 tokens for 512 <= K <= 32768 and up to 64 from K = 5120 (long rows
+    in K slices), the fp16 GEMV up to 64 tokens on shorter rows, the
     GEMM above; a forced path that cannot take a shape falls back to the
     automatic choice."""
     F = fh3
@@ -124,11 +123,12 @@ def test_matmul_path_selection(fh3):
     assert F.matmul_path(5, 5120) == SW and F.matmul_path(16, 5120) == SW and F.matmul_path(16, 6144) == SW
     assert F.matmul_path(16, 6400) == SW and F.matmul_path(16, 8192) == SW and F.matmul_path(16, 32768) == SW
     assert F.matmul_path(5, 256) == SK and F.matmul_path(17, 5120) == SW and F.matmul_path(32, 25600) == SW
-    assert F.matmul_path(33, 5120) == SK and F.matmul_path(64, 5120) == SK
+    assert F.matmul_path(33, 5120) == SW and F.matmul_path(64, 5120) == SW and F.matmul_path(64, 256) == SK
+    assert F.matmul_path(17, 4864) == SK and F.matmul_path(64, 4096) == SK and F.matmul_path(16, 4096) == SW
     assert F.matmul_path(65, 5120) == GM
     MD = F.PATH_MIDM
-    assert F.matmul_path(33, 8192) == MD and F.matmul_path(64, 13824) == MD and F.matmul_path(17, 8192) == SW
-    assert F.matmul_path(16, 13824) == SW and F.matmul_path(33, 7936) == SK and F.matmul_path(65, 13824) == GM
+    assert F.matmul_path(33, 8192) == SW and F.matmul_path(64, 13824) == SW and F.matmul_path(17, 8192) == SW
+    assert F.matmul_path(16, 13824) == SW and F.matmul_path(33, 7936) == SW and F.matmul_path(65, 13824) == GM
     try:
         F.set_path(MD)
         assert F.matmul_path(1, 5120) == MD and F.matmul_path(64, 256) == MD and F.matmul_path(65, 5120) == GM
@@ -138,7 +138,7 @@ def test_matmul_path_selection(fh3):
         assert F.matmul_path(4, 5120) == G8 and F.matmul_path(5, 5120) == SW
         F.set_path(SW)
         assert F.matmul_path(1, 5120) == SW and F.matmul_path(16, 512) == SW
-        assert F.matmul_path(33, 5120) == SK and F.matmul_path(32, 8192) == SW and F.matmul_path(16, 256) == SK
+        assert F.matmul_path(65, 5120) == GM and F.matmul_path(64, 8192) == SW and F.matmul_path(16, 256) == SK
         F.set_path(GM)
         assert F.matmul_path(1, 5120) == GM
     finally:

@@ -1,5 +1,5 @@
-"""GPU parity of the persistent small-M kernel (FH3_HIP_PATH_SWEEP: up to 32
-tokens in one or two token blocks, 512 <= K <= 32768; fp16 activations held in registers, exact fp16
+"""GPU parity of the persistent small-M kernel (FH3_HIP_PATH_SWEEP: up to 64
+tokens in one to four token blocks, 512 <= K <= 32768; fp16 activations held in registers, exact fp16
 sc*q weights, the offsets dmin*m from the prepared group sums; rows of more
 than 20 super-blocks in K slices whose partial sums are added in slice order)
 against the CPU oracle, through the C-ABI.
@@ -61,6 +61,10 @@ CASES = [
     (24, 5120, 300, "outliers", 1.0, False),      # two token blocks, two K slices
     (32, 5120, 17408, "normal", 0.0, True),       # text-encoder MLP shape at 32 tokens (sampled rows)
     (29, 25600, 200, "silu_gated", 2.0, False),   # two token blocks in ten slices of ten super-blocks
+    (33, 2048, 96, "normal", 0.0, True),          # three token blocks, the third with one token
+    (48, 5120, 640, "outliers", 1.0, True),       # three token blocks in three slices (7, 7, 6)
+    (64, 8192, 200, "silu_gated", 0.0, False),    # four token blocks in four slices of eight
+    (64, 5120, 17408, "normal", 0.0, False),      # text-encoder MLP shape at 64 tokens (sampled rows)
     (16, 5120, 5120, "normal", 0.0, False),       # text-encoder attention projection
     (16, 5120, 17408, "outliers", 0.0, True),     # text-encoder MLP, several blocks per workgroup
 ]
@@ -145,7 +149,7 @@ def test_sweep_non_finite_row_stays_in_its_row(gpu, oracle, bad):
     assert H.rel_fro(y[keep], yo) <= TOL
 
 
-@pytest.mark.parametrize("K,M", [(5120, 16), (25600, 16), (5120, 32)])
+@pytest.mark.parametrize("K,M", [(5120, 16), (25600, 16), (5120, 32), (5120, 64)])
 def test_sweep_prepared_equals_direct(gpu, K, M):
     """The two-stage API (prepare, then product) gives the one-call result bit
     for bit; the prepared form carries the group sums."""
@@ -166,7 +170,7 @@ def test_sweep_prepared_equals_direct(gpu, K, M):
     assert np.array_equal(dy.download(np.float32, (M, N)).view(np.uint32), direct.view(np.uint32))
 
 
-@pytest.mark.parametrize("M,K", [(5, 2560), (16, 2560), (16, 8192), (32, 2560), (20, 8192)])
+@pytest.mark.parametrize("M,K", [(5, 2560), (16, 2560), (16, 8192), (32, 2560), (20, 8192), (64, 2560), (40, 1024)])
 def test_sweep_gate_residual_and_swiglu(gpu, oracle, M, K):
     """Both epilogues, in the kernel's store and (K slices) in the ordered sum
     of the slices, for one and two token blocks."""
@@ -180,17 +184,21 @@ def test_sweep_gate_residual_and_swiglu(gpu, oracle, M, K):
     gate = rng.standard_normal((M, N)).astype(np.float32)
     h = rng.standard_normal((M, N)).astype(np.float32)
     y = H.oracle_matmul(oracle, raw, K, N, x, bias)
-    assert F.matmul_path(M, K) == F.PATH_SWEEP
-    dwt, dx, db = F.DeviceBuffer.from_array(raw), _buf(F, x), _buf(F, bias)
-    # SwiGLU on the [val | gate] rows
-    dout = F.DeviceBuffer(M * Fd * 4)
-    F.matmul_epi_dev(dwt, K, N, dx, M, F.EPI_SWIGLU, dout, None, db)
-    # gate residual, through the two-stage API
-    dg, dh = _buf(F, gate), _buf(F, h)
-    prep = F.DeviceBuffer(F.prepared_bytes(M, K))
-    F.prepare_x_dev(dx, M, K, prep)
-    F.matmul_prepared_epi_dev(dwt, K, N, prep, M, F.EPI_GATE_RESIDUAL, dh, dg, db)
-    F.synchronize()
+    F.set_path(F.PATH_SWEEP)  # the automatic choice takes k_skinny above 16 tokens on rows below 5120
+    try:
+        assert F.matmul_path(M, K) == F.PATH_SWEEP
+        dwt, dx, db = F.DeviceBuffer.from_array(raw), _buf(F, x), _buf(F, bias)
+        # SwiGLU on the [val | gate] rows
+        dout = F.DeviceBuffer(M * Fd * 4)
+        F.matmul_epi_dev(dwt, K, N, dx, M, F.EPI_SWIGLU, dout, None, db)
+        # gate residual, through the two-stage API
+        dg, dh = _buf(F, gate), _buf(F, h)
+        prep = F.DeviceBuffer(F.prepared_bytes(M, K))
+        F.prepare_x_dev(dx, M, K, prep)
+        F.matmul_prepared_epi_dev(dwt, K, N, prep, M, F.EPI_GATE_RESIDUAL, dh, dg, db)
+        F.synchronize()
+    finally:
+        F.set_path(F.PATH_AUTO)
     sw = dout.download(np.float32, (M, Fd))
     gr = dh.download(np.float32, (M, N))
     ref = np.zeros((M, Fd), np.float32)
@@ -201,7 +209,7 @@ def test_sweep_gate_residual_and_swiglu(gpu, oracle, M, K):
     assert H.rel_fro(gr - h, href - h) <= TOL
 
 
-@pytest.mark.parametrize("K,M", [(4096, 16), (13824, 16), (4096, 32)])
+@pytest.mark.parametrize("K,M", [(4096, 16), (13824, 16), (5120, 32), (5120, 64)])
 def test_sweep_graph_replay_matches_eager(gpu, K, M):
     """Captured calls replayed three times equal the eager result (the
     prepared workspace and, for K slices, the partial sums are sized by the

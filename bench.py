@@ -577,6 +577,32 @@ def main():
                                                        "the kernel time (k_skinny, four token blocks)"}}
     g1.free()
 
+    # ---------------- 17..64-token products (k_sweep with 2-4 token blocks) -
+    # text-encoder prompt lengths between the headline's 16 and the GEMM's 65
+    # tokens, at K = 5120 (graph of 32 calls, weights rotated past the MALL)
+    prompt = []
+    for N in (5120, 17408):
+        for M in (17, 32, 48, 64):
+            c = Gemv(M, 5120, N, seed=0)
+            c.call(0)
+            c.kernel(0)
+            F.synchronize()
+            gk = F.capture(lambda c=c: [c.kernel(i) for i in range(32)])
+            gc = F.capture(lambda c=c: [c.call(i) for i in range(32)])
+            gk.launch()
+            gc.launch()
+            t_k = ev.time_ms(lambda i: gk.launch(), 4, st) / 32
+            t_c = ev.time_ms(lambda i: gc.launch(), 4, st) / 32
+            gk.close()
+            gc.close()
+            prompt.append({"M": M, "K": 5120, "N": N, "path": F.matmul_path(M, 5120),
+                           "kernel_us": round(t_k * 1e3, 2), "call_us": round(t_c * 1e3, 2),
+                           "call_weight_GBps": round(c.wbytes / (t_c * 1e-3) / 1e9, 1)})
+            for b in c.w + [c.dx, c.dy, c.prep]:
+                b.close()
+    extra["prompt_17_64_tokens"] = prompt
+    log("[bench] 17..64 tokens: %s" % ", ".join("M=%d N=%d %.1f us" % (r["M"], r["N"], r["call_us"]) for r in prompt))
+
     # ---------------- few-hundred-token products (split-K GEMM path) -------
     # text-encoder prompt lengths: 65..512 tokens at K = N = 5120, where the
     # 256 x 128 GEMM tiles alone would leave most CUs idle

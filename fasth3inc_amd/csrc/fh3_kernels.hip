@@ -2068,7 +2068,7 @@ __global__ __launch_bounds__(512) void k_skinny16(const _Float16 *__restrict__ W
 #pragma unroll
             for (int m = 0; m < 8; m++) {
                 b[cur ^ 1][m] = wr[(i + 1) * 32 + 4 * m];
-                if (AB == 2) {
+                if constexpr (AB == 2) {
 #pragma unroll
                     for (int tb = 0; tb < TB; tb++) a[ac ^ 1][m][tb] = xq[tb][((i + 1) * 16 + 2 * m) * 64];
                 }

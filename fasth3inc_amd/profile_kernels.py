@@ -19,6 +19,9 @@ Workloads (each launch sequence is preceded by one untimed warmup launch):
          K=8192 -> N=5120, down-projection K=25600 -> N=5120):
          fh3_hip_matmul_prepared_dev -> k_gemv8 (M = 1, K = 8192) or k_sweep in
          K slices then k_midm_sum; weights rotated as for gemv
+  prompt 17 to 64 tokens at K = 5120 (M in {17, 32, 48, 64}, N in {5120,
+         17408}): fh3_hip_matmul_prepared_dev -> k_sweep with two to four
+         token blocks; weights rotated as for gemv
   copy   hipMemcpy device-to-device of 256 MiB: a copy of known size that
          calibrates FETCH_SIZE / WRITE_SIZE against the bytes moved
   attn   the DiT attention branch at n = 16384 tokens, 40 heads of 128
@@ -75,6 +78,28 @@ def te(reps):
             print("te M=%d N=%d K=%d path %d: %d launches" % (M, N, K, F.matmul_path(M, K), reps), flush=True)
             for b in ws + [dx, dy, prep]:
                 b.close()
+
+
+def _rotated_products(tag, shapes, reps):
+    for M, K, N in shapes:
+        raw = F.synth_q4k_weights(0, 100 + N + K, N, K, 0.02, 0.0)
+        copies = max(2, -(-(MALL_BYTES + (64 << 20)) // raw.nbytes))
+        ws = [F.DeviceBuffer.from_array(raw) for _ in range(copies)]
+        dx = F.DeviceBuffer.from_array(F.synth_x("normal", 0, 200 + M, M, K))
+        dy = F.DeviceBuffer(M * N * 4)
+        prep = F.DeviceBuffer(F.prepared_bytes(M, K))
+        F.prepare_x_dev(dx, M, K, prep)
+        for i in range(reps + 1):
+            F.matmul_prepared_dev(ws[i % copies], K, N, prep, dy, M)
+        F.synchronize()
+        print("%s M=%d N=%d K=%d path %d: %d launches, %d weight copies" % (tag, M, N, K, F.matmul_path(M, K), reps,
+                                                                          copies), flush=True)
+        for b in ws + [dx, dy, prep]:
+            b.close()
+
+
+def prompt(reps):
+    _rotated_products("prompt", [(M, 5120, N) for N in (5120, 17408) for M in (17, 32, 48, 64)], reps)
 
 
 def gemm(reps):
@@ -159,7 +184,7 @@ def vsa(reps, heads=56, hd=128, rot=96):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("workload", choices=("gemv", "te", "gemm", "mlp", "copy", "attn", "vsa", "all"))
+    ap.add_argument("workload", choices=("gemv", "te", "prompt", "gemm", "mlp", "copy", "attn", "vsa", "all"))
     ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args(argv)
     F.init(0)

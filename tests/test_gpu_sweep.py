@@ -170,10 +170,12 @@ def test_sweep_prepared_equals_direct(gpu, K, M):
     assert np.array_equal(dy.download(np.float32, (M, N)).view(np.uint32), direct.view(np.uint32))
 
 
-@pytest.mark.parametrize("M,K", [(5, 2560), (16, 2560), (16, 8192), (32, 2560), (20, 8192), (64, 2560), (40, 1024)])
+@pytest.mark.parametrize("M,K", [(5, 2560), (16, 2560), (16, 8192), (32, 2560), (20, 8192), (64, 2560), (40, 1024),
+                                 (24, 5120), (48, 5120), (64, 5120)])
 def test_sweep_gate_residual_and_swiglu(gpu, oracle, M, K):
     """Both epilogues, in the kernel's store and (K slices) in the ordered sum
-    of the slices, for one and two token blocks."""
+    of the slices, for one to four token blocks (K = 5120: the automatic
+    choice at 17-64 tokens, in two or three slices)."""
     F = gpu
     rng = np.random.default_rng(410 + M + K)
     Fd = 192

@@ -25,10 +25,11 @@ def _pair(F, K, N, M, seed):
     return F.DeviceBuffer.from_array(raw), F.DeviceBuffer.from_array(x), F.DeviceBuffer.from_array(bias)
 
 
-# (K, N, first n_tok, second n_tok): k_gemv8, k_skinny, k_midm, split-K
-# k_gemm, k_gemm with K whole
-CASES = [(5120, 5120, 2, 1), (5120, 17408, 16, 4), (13824, 5120, 64, 24), (5120, 5120, 512, 65),
-         (4096, 4096, 4096, 300)]
+# (K, N, first n_tok, second n_tok): k_gemv8; k_sweep then k_gemv8; k_sweep in
+# K slices (partial sums in the scratch array); k_skinny; split-K k_gemm;
+# k_gemm with K whole
+CASES = [(5120, 5120, 2, 1), (5120, 17408, 16, 4), (13824, 5120, 64, 24), (2048, 1024, 40, 20),
+         (5120, 5120, 512, 65), (4096, 4096, 4096, 300)]
 
 
 @pytest.mark.parametrize("K,N,M1,M2", CASES)

@@ -18,8 +18,13 @@ LIB_PATH = os.path.join(_PKG, "lib", "libfh3hip.so")
 # GGML type ids (reference include/fh3/fh3.h:63-79)
 FH3_QUANT_F32 = 0
 FH3_QUANT_F16 = 1
+FH3_QUANT_Q8_0 = 8
+FH3_QUANT_Q2_K = 10
+FH3_QUANT_Q3_K = 11
 FH3_QUANT_Q4_K = 12
+FH3_QUANT_Q5_K = 13
 FH3_QUANT_Q6_K = 14
+FH3_QUANT_BF16 = 30
 
 FH3_OK = 0
 FH3_ERR = -1

@@ -22,6 +22,13 @@ Workloads (each launch sequence is preceded by one untimed warmup launch):
   prompt 17 to 64 tokens at K = 5120 (M in {17, 32, 48, 64}, N in {5120,
          17408}): fh3_hip_matmul_prepared_dev -> k_sweep with two to four
          token blocks; weights rotated as for gemv
+  single the 64 x 4096 x 4096 product of the reference's bench_matmul.c, one
+         weight copy (warm in the Infinity Cache after the first launch, as the
+         benchmark runs it): fh3_hip_matmul_prepared_dev -> k_skinny
+  q56    Q5_K and Q6_K weights read in place at the text encoder's shapes
+         (Q5_K 5120 -> 1024, Q6_K 5120 -> 1024, 8192 -> 5120, 25600 -> 5120)
+         at M = 1 and 16: fh3_hip_matmul_prepared_dev -> k_skinny<Q5_K / Q6_K>;
+         weights rotated as for gemv
   copy   hipMemcpy device-to-device of 256 MiB: a copy of known size that
          calibrates FETCH_SIZE / WRITE_SIZE against the bytes moved
   attn   the DiT attention branch at n = 16384 tokens, 40 heads of 128
@@ -95,6 +102,59 @@ def _rotated_products(tag, shapes, reps):
         print("%s M=%d N=%d K=%d path %d: %d launches, %d weight copies" % (tag, M, N, K, F.matmul_path(M, K), reps,
                                                                           copies), flush=True)
         for b in ws + [dx, dy, prep]:
+            b.close()
+
+
+def _random_q56(qt, rows, K, seed):
+    """Random Q5_K (176 B) or Q6_K (210 B) super-blocks: random quant and
+    scale bytes, fp16 block scales (d, and dmin for Q5_K) set to 2^-10."""
+    bb = 176 if qt == F.FH3_QUANT_Q5_K else 210
+    rng = np.random.default_rng(seed)
+    raw = rng.integers(0, 256, size=(rows, K // 256, bb), dtype=np.uint8)
+    d = np.frombuffer(np.float16(2.0 ** -10).tobytes(), np.uint8)
+    if qt == F.FH3_QUANT_Q5_K:
+        raw[:, :, 0:2] = d
+        raw[:, :, 2:4] = d
+    else:
+        raw[:, :, 208:210] = d
+    return raw.reshape(-1)
+
+
+def single(reps):
+    M, K, N = 64, 4096, 4096
+    raw = F.synth_q4k_weights(0, 100 + N + K, N, K, 0.02, 0.0)
+    dw = F.DeviceBuffer.from_array(raw)
+    dx = F.DeviceBuffer.from_array(F.synth_x("normal", 0, 200 + M, M, K))
+    dy = F.DeviceBuffer(M * N * 4)
+    prep = F.DeviceBuffer(F.prepared_bytes(M, K))
+    F.prepare_x_dev(dx, M, K, prep)
+    for i in range(reps + 1):
+        F.matmul_prepared_dev(dw, K, N, prep, dy, M)
+    F.synchronize()
+    print("single M=%d N=%d K=%d path %d: %d launches, one weight copy" % (M, N, K, F.matmul_path(M, K), reps),
+          flush=True)
+    for b in (dw, dx, dy, prep):
+        b.close()
+
+
+def q56(reps):
+    for qt, K, N in ((F.FH3_QUANT_Q5_K, 5120, 1024), (F.FH3_QUANT_Q6_K, 5120, 1024), (F.FH3_QUANT_Q6_K, 8192, 5120),
+                     (F.FH3_QUANT_Q6_K, 25600, 5120)):
+        raw = _random_q56(qt, N, K, seed=5)
+        copies = max(2, -(-(MALL_BYTES + (64 << 20)) // raw.nbytes))
+        ws = [F.DeviceBuffer.from_array(raw) for _ in range(copies)]
+        for M in (1, 16):
+            dx = F.DeviceBuffer.from_array(F.synth_x("normal", 0, 200 + M, M, K))
+            dy = F.DeviceBuffer(M * N * 4)
+            prep = F.DeviceBuffer(F.prepared_bytes(M, K))
+            F.prepare_x_dev(dx, M, K, prep)
+            for i in range(reps + 1):
+                F.matmul_prepared_dev(ws[i % copies], K, N, prep, dy, M, qtype=qt)
+            F.synchronize()
+            print("q56 type %d M=%d N=%d K=%d: %d launches, %d weight copies" % (qt, M, N, K, reps, copies), flush=True)
+            for b in (dx, dy, prep):
+                b.close()
+        for b in ws:
             b.close()
 
 
@@ -184,7 +244,8 @@ def vsa(reps, heads=56, hd=128, rot=96):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("workload", choices=("gemv", "te", "prompt", "gemm", "mlp", "copy", "attn", "vsa", "all"))
+    ap.add_argument("workload", choices=("gemv", "te", "prompt", "single", "q56", "gemm", "mlp", "copy", "attn", "vsa",
+                                         "all"))
     ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args(argv)
     F.init(0)

@@ -1,7 +1,7 @@
 """The drop-in at link level, on the CPU (no compute calls).
 
-The recipe of INTEGRATION.md, section 1, is built by `make -C oracle
-integration` from the reference's own sources where they lie: fh3_core with
+The integration recipe is built by `make -C oracle integration` from the
+reference's own sources where they lie: fh3_core with
 the CPU matmul, dequant, attention and pack reader renamed and the trunk
 streamer left out, then the reference's CLI main and its bench_matmul linked
 against that archive and libfh3hip.so.  Checked here:

@@ -74,7 +74,7 @@ def test_attention_vs_oracle(gpu, oracle, n, heads, hd, sigma):
 
 
 def test_attention_large_n_rows(gpu, oracle):
-    """n = 8192 keys (config-5-sized sequence per head): 96 seeded query rows
+    """n = 8192 keys (a DiT-length sequence per head): 96 seeded query rows
     against the oracle; every row is a convex combination of v (row sums of
     the weights are 1), so |o| <= max |v| on every channel."""
     F = gpu

@@ -1,12 +1,13 @@
-"""Parity at the benchmark configurations' full sizes.
+"""Parity at the benchmark workloads' full sizes.
 
-Each configuration runs whole on the GPU with the benchmark's seeded inputs:
-  1. M=64, K=4096, N=4096, N(0,1) activations
-  2. M in {1,4,16}, K=5120, N in {5120,17408}
-  3. M=8192, K=5120, N in {15360, 5120}, N(0,1) with 1% outliers at +-8
-  4. M=32768, K=5120 -> N=13824 with a 2-decade per-super-block scale spread,
-     and K=13824 -> N=5120 on SiLU-gated activations
-Configurations 1 and 2 are compared with the oracle in full.  For 3 and 4 the
+Each workload runs whole on the GPU with the benchmark's seeded inputs:
+  - single product: M=64, K=4096, N=4096, N(0,1) activations
+  - text-encoder GEMV: M in {1,4,16}, K=5120, N in {5120,17408}
+  - DiT attention linears: M=8192, K=5120, N in {15360, 5120}, N(0,1) with 1%
+    outliers at +-8
+  - DiT MLP linears: M=32768, K=5120 -> N=13824 with a 2-decade per-super-block
+    scale spread, and K=13824 -> N=5120 on SiLU-gated activations
+The first two are compared with the oracle in full.  For the DiT shapes the
 oracle computes a seeded subset of tokens (output rows depend only on their own
 activation row, as in the reference's fh3_matmul loop over tokens), which
 includes the first and last token of the tile edges.  At full size a property
@@ -41,10 +42,10 @@ def _subset(M, n, seed):
     return np.array(sorted(pick))
 
 
-def test_config1_single_matmul_m64(gpu, oracle):
+def test_single_matmul_m64_k4096_n4096(gpu, oracle):
     F = gpu
     M, K, N = 64, 4096, 4096
-    print("case: config 1 M=64 K=4096 N=4096", flush=True)
+    print("case: single matmul M=64 K=4096 N=4096", flush=True)
     raw = F.synth_q4k_weights(0, 300 + N + K, N, K, 0.02, 0.0)
     x = F.synth_x("normal", 0, 400 + K, M, K)
     y = _run(F, raw, K, N, x)
@@ -52,12 +53,12 @@ def test_config1_single_matmul_m64(gpu, oracle):
 
 
 @pytest.mark.parametrize("N", [5120, 17408])
-def test_config2_gemv_shapes(gpu, oracle, N):
+def test_text_encoder_gemv_k5120(gpu, oracle, N):
     F = gpu
     K = 5120
     raw = F.synth_q4k_weights(0, 100 + N, N, K, 0.02, 0.0)
     for M in (1, 4, 16):
-        print("case: config 2 M=%d K=%d N=%d" % (M, K, N), flush=True)
+        print("case: text-encoder GEMV M=%d K=%d N=%d" % (M, K, N), flush=True)
         x = F.synth_x("normal", 0, 200 + M, M, K)
         y = _run(F, raw, K, N, x)
         yo = H.oracle_matmul(oracle, raw, K, N, x)
@@ -71,10 +72,10 @@ def test_config2_gemv_shapes(gpu, oracle, N):
 
 
 @pytest.mark.parametrize("N", [15360, 5120])
-def test_config3_dit_attention(gpu, oracle, N):
+def test_dit_attention_linears_m8192_k5120(gpu, oracle, N):
     F = gpu
     M, K = 8192, 5120
-    print("case: config 3 M=%d K=%d N=%d" % (M, K, N), flush=True)
+    print("case: DiT attention linear M=%d K=%d N=%d" % (M, K, N), flush=True)
     raw = F.synth_q4k_weights(1, 300 + N + K, N, K, 0.02, 0.0)
     x = F.synth_x("outliers", 1, 400 + K, M, K)
     y = _run(F, raw, K, N, x)
@@ -88,10 +89,10 @@ def test_config3_dit_attention(gpu, oracle, N):
 
 
 @pytest.mark.parametrize("K,N,xkind", [(5120, 13824, "normal"), (13824, 5120, "silu_gated")])
-def test_config4_dit_mlp(gpu, oracle, K, N, xkind):
+def test_dit_mlp_linears_m32768(gpu, oracle, K, N, xkind):
     F = gpu
     M = 32768
-    print("case: config 4 M=%d K=%d N=%d x=%s" % (M, K, N, xkind), flush=True)
+    print("case: DiT MLP linear M=%d K=%d N=%d x=%s" % (M, K, N, xkind), flush=True)
     raw = F.synth_q4k_weights(1, 300 + N + K, N, K, 0.02, 2.0)
     x = F.synth_x(xkind, 1, 400 + K, M, K)
     y = _run(F, raw, K, N, x)

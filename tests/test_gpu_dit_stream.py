@@ -114,7 +114,7 @@ PRODUCTS = (("qkv", HIDDEN, QKV, "xa"), ("out", HIDDEN, HIDDEN, "xa"), ("fc1", H
             ("fc2", MLP, HIDDEN, "xm"))
 
 
-def test_config5_streamed_products(gpu, oracle, blocks, acts):
+def test_streamed_dit_blocks_m16384_products(gpu, oracle, blocks, acts):
     F = gpu
     path, specs = blocks
     dx = {k: F.DeviceBuffer.from_array(acts[k]) for k in ("xa", "xm")}
@@ -134,12 +134,12 @@ def test_config5_streamed_products(gpu, oracle, blocks, acts):
         F.synchronize()
         return outs
 
-    print("case: config 5 resident, %d blocks M=%d" % (N_BLOCKS, M), flush=True)
+    print("case: DiT blocks resident, %d blocks M=%d" % (N_BLOCKS, M), flush=True)
     views, wbufs = _resident_views(F, path, specs)
     want = run(lambda L: views[L])
     for host_budget, label in ((0, "disk -> host ring -> 2 device slots"),
                                (1 << 40, "page-locked host blocks -> 2 device slots")):
-        print("case: config 5 streamed (%s)" % label, flush=True)
+        print("case: DiT blocks streamed (%s)" % label, flush=True)
         with F.Trunk(path, host_budget) as tr:
             tr.attach_device(0)
             assert tr.info().dpin == 0
@@ -169,7 +169,7 @@ def test_config5_streamed_products(gpu, oracle, blocks, acts):
         b.close()
 
 
-def test_config5_streamed_fused_block(gpu, oracle, blocks, acts):
+def test_streamed_dit_blocks_m16384_fused_block(gpu, oracle, blocks, acts):
     F = gpu
     path, specs = blocks
     d = {k: F.DeviceBuffer.from_array(acts[k]) for k in ("xa", "shift", "scale", "gate")}
@@ -192,10 +192,10 @@ def test_config5_streamed_fused_block(gpu, oracle, blocks, acts):
         F.synchronize()
         return h, qkvs
 
-    print("case: config 5 fused block sequence, resident", flush=True)
+    print("case: DiT fused block sequence, resident", flush=True)
     views, wbufs = _resident_views(F, path, specs)
     h_want, q_want = run(lambda L: views[L])
-    print("case: config 5 fused block sequence, streamed through 2 device slots", flush=True)
+    print("case: DiT fused block sequence, streamed through 2 device slots", flush=True)
     with F.Trunk(path, 1 << 40) as tr:
         tr.attach_device(0)
         h_got, q_got = run(lambda L: _streamed(F, tr, L))

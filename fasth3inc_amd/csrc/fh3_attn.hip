@@ -125,15 +125,20 @@ __global__ __launch_bounds__(256) void k_attn_prep(const float *__restrict__ q, 
 #pragma unroll
             for (int i = 0; i < DPT; i++) sx[r][d0 + i] = x[i];
             __syncthreads();
-            const int half = rot >> 1;
-            if (tok >= 0 && (rot & 7) == 0) {
+            // rot through an empty asm: otherwise the per-element region
+            // tests below are hoisted out of the q/k loop and their 64-bit
+            // lane masks, two per element, overflow the scalar registers
+            int rv = rot;
+            asm volatile("" : "+s"(rv));
+            const int half = rv >> 1;
+            if (tok >= 0 && (rv & 7) == 0) {
                 // 4-element chunks never straddle half or rot: one region
                 // test, and 16-byte reads of the tables and the partner chunk
-                const float *cr = cosb + (size_t)tok * rot, *sr = sinb + (size_t)tok * rot;
+                const float *cr = cosb + (size_t)tok * rv, *sr = sinb + (size_t)tok * rv;
 #pragma unroll
                 for (int i = 0; i < DPT / 4; i++) {
                     const int d = d0 + 4 * i;
-                    if (d < rot) {
+                    if (d < rv) {
                         const bool lo = d < half;
                         const f32x4 cv = *(const f32x4 *)(cr + d), sv = *(const f32x4 *)(sr + d);
                         const f32x4 pv = *(const f32x4 *)&sx[r][lo ? d + half : d - half];
@@ -145,14 +150,14 @@ __global__ __launch_bounds__(256) void k_attn_prep(const float *__restrict__ q, 
                     }
                 }
             } else if (tok >= 0) {
-                const float *cr = cosb + (size_t)tok * rot, *sr = sinb + (size_t)tok * rot;
+                const float *cr = cosb + (size_t)tok * rv, *sr = sinb + (size_t)tok * rv;
 #pragma unroll
                 for (int i = 0; i < DPT; i++) {
                     const int d = d0 + i;
                     if (d < half) {
                         const float a = x[i] * cr[d], b = sx[r][d + half] * sr[d];
                         x[i] = a - b;
-                    } else if (d < rot) {
+                    } else if (d < rv) {
                         const float a = x[i] * cr[d], b = sx[r][d - half] * sr[d];
                         x[i] = a + b;
                     }

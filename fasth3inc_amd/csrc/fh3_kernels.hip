@@ -323,13 +323,18 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 //   x = fma(x, 1 + scale[t], shift[t])   (src/core/fh3_ops.c:529-557),
 // shift / scale being [M][K] rows.
 // Sum over each aligned group of 8 lanes (every lane of the group gets it).
+// DPP read of v from another lane of its row of 16 (every lane is written:
+// full row and bank masks), with no old operand, so the move folds into the
+// VALU op that consumes it
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
 __device__ __forceinline__ float sum8_f32(float v) {
-    int iv = __builtin_bit_cast(int, v);
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(iv, iv, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
-    iv = __builtin_bit_cast(int, v);
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(iv, iv, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
-    iv = __builtin_bit_cast(int, v);
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(iv, iv, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f32<0x141>(v);  // row_half_mirror
     return v;
 }
 
@@ -1275,13 +1280,14 @@ constexpr int G8_REC = 288;        // x_q bytes of one (super-block, token, plan
 constexpr int G8_XS = 32;          // eight int32 group sums per (super-block, token)
 constexpr int G8_MAX_TOKENS = 4;
 
-// Maximum over the wavefront (DPP within rows of 16, then row broadcasts),
-// read from lane 63.
-__device__ __forceinline__ float wave_max_f32(float v) {
-    int iv = __builtin_bit_cast(int, v);
-#define FH3_DPP_MAX(ctrl, rows)                                                                 \
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(iv, iv, ctrl, rows, 0xF, false))); \
-    iv = __builtin_bit_cast(int, v);
+// Maximum over the wavefront of v >= 0 or NaN (DPP within rows of 16, then
+// row broadcasts), read from lane 63.  On such floats the bit patterns
+// order as the values do, NaN above Inf, so this is an unsigned integer
+// maximum; 0, its identity, stands in the lanes a row broadcast leaves
+// unwritten, and every move folds into the v_max_u32 that consumes it.
+__device__ __forceinline__ float wave_max_abs_f32(float v) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+#define FH3_DPP_MAX(ctrl, rows) u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, ctrl, rows, 0xF, false));
     FH3_DPP_MAX(0xB1, 0xF)   // quad_perm [1,0,3,2]
     FH3_DPP_MAX(0x4E, 0xF)   // quad_perm [2,3,0,1]
     FH3_DPP_MAX(0x141, 0xF)  // row_half_mirror
@@ -1289,7 +1295,7 @@ __device__ __forceinline__ float wave_max_f32(float v) {
     FH3_DPP_MAX(0x142, 0xA)  // row_bcast:15 into rows 1, 3
     FH3_DPP_MAX(0x143, 0xC)  // row_bcast:31 into rows 2, 3
 #undef FH3_DPP_MAX
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 63));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)u, 63));
 }
 
 template <int MT, int C, int LB, int EPI>
@@ -1350,19 +1356,25 @@ __global__ __launch_bounds__(LB) void k_gemv8(const uint8_t *__restrict__ W, int
         inv[t] = 0.f;
         inv2[t] = 1.f;
         if (t < M) {
-            float mx = 0.f, chk = 0.f;
+            // window maximum of |x| with NaN propagated (v_maximum3_f32), so
+            // that one value also flags a non-finite window; the wavefront
+            // maximum then runs on the bit patterns, which order as the
+            // values do on |x| (Inf and NaN above every finite value)
+            float mx = 0.f;
 #pragma unroll
             for (int i = 0; i < C; i++) {
                 const f32x4 v = xv[t][i];
-                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-                chk = __builtin_fmaf((v.x + v.y) + (v.z + v.w), 0x1p-64f, chk);  // Inf/NaN survive
+                mx = __builtin_elementwise_maximum(
+                    mx, __builtin_elementwise_maximum(
+                            __builtin_elementwise_maximum(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
+                            __builtin_elementwise_maximum(__builtin_fabsf(v.z), __builtin_fabsf(v.w))));
             }
-            mx = wave_max_f32(mx);
-            const bool bad = __builtin_amdgcn_ballot_w64(!__builtin_isfinite(chk)) != 0;
+            mx = wave_max_abs_f32(mx);
+            const bool bad = !(mx <= 3.4028234663852886e38f);
             // 2^e = 2^e1 * 2^e2, both factors normal: e <= 162 for subnormal
             // windows, e >= -114 (largest finite max)
             int e = 0;
-            if (mx > 0.f) {
+            if (mx > 0.f && !bad) {
                 int E;
                 (void)frexpf(mx, &E);
                 e = 14 - E;
@@ -1371,25 +1383,43 @@ __global__ __launch_bounds__(LB) void k_gemv8(const uint8_t *__restrict__ W, int
             const float sc = ldexpf(1.0f, e1), sc2 = ldexpf(1.0f, e2);
             inv[t] = bad ? __builtin_nanf("") : ldexpf(1.0f, -e1);
             inv2[t] = ldexpf(1.0f, -e2);
+            // x_q + (1.5*2^23 + 128) = rne(x * 2^e1 * 2^e2 + 1.5*2^23 + 128); x * 2^e1
+            // is exact (or below 2^-100, where both forms give the constant), so
+            // with e2 = 0, the usual case, one fma with 2^e1 gives the same value
+            auto quantise = [&](auto two_factors) {
 #pragma unroll
-            for (int i = 0; i < C; i++) {
-                const f32x4 v = xv[t][i] * sc;  // exact
-                const float f0 = __builtin_fmaf(v.x, sc2, 12583040.0f), f1 = __builtin_fmaf(v.y, sc2, 12583040.0f);
-                const float f2 = __builtin_fmaf(v.z, sc2, 12583040.0f), f3 = __builtin_fmaf(v.w, sc2, 12583040.0f);
-                const uint32_t v0 = __builtin_bit_cast(uint32_t, f0), v1 = __builtin_bit_cast(uint32_t, f1);
-                const uint32_t v2 = __builtin_bit_cast(uint32_t, f2), v3 = __builtin_bit_cast(uint32_t, f3);
-                const uint32_t p01 = __builtin_amdgcn_perm(v1, v0, 0x05040100u);  // v0.b0 v0.b1 v1.b0 v1.b1
-                const uint32_t p23 = __builtin_amdgcn_perm(v3, v2, 0x05040100u);
-                uint8_t *rec = my + (i * MT + t) * 2 * G8_REC + 4 * lane;
-                *reinterpret_cast<uint32_t *>(rec) = __builtin_amdgcn_perm(p23, p01, 0x07050301u);
-                *reinterpret_cast<uint32_t *>(rec + G8_REC) =
-                    __builtin_amdgcn_perm(p23, p01, 0x06040200u) ^ 0x80808080u;
-                // f - (1.5*2^23 + 128) = x_q exactly; a group's 32 of them sum to
-                // less than 2^19 in magnitude, exact in fp32
-                const float gs = sum8_f32(((f0 - 12583040.0f) + (f1 - 12583040.0f)) +
-                                          ((f2 - 12583040.0f) + (f3 - 12583040.0f)));
-                if ((lane & 7) == 0) reinterpret_cast<int *>(xsb)[(i * MT + t) * 8 + (lane >> 3)] = (int)gs;
-            }
+                for (int i = 0; i < C; i++) {
+                    // scalars, not vector elements: __builtin_bit_cast of an
+                    // element expression reads element 0 with this compiler
+                    float f0, f1, f2, f3;
+                    if constexpr (decltype(two_factors)::value) {
+                        const f32x4 v = xv[t][i] * sc;  // exact
+                        f0 = __builtin_fmaf(v.x, sc2, 12583040.0f), f1 = __builtin_fmaf(v.y, sc2, 12583040.0f);
+                        f2 = __builtin_fmaf(v.z, sc2, 12583040.0f), f3 = __builtin_fmaf(v.w, sc2, 12583040.0f);
+                    } else {
+                        const f32x4 v = xv[t][i];
+                        f0 = __builtin_fmaf(v.x, sc, 12583040.0f), f1 = __builtin_fmaf(v.y, sc, 12583040.0f);
+                        f2 = __builtin_fmaf(v.z, sc, 12583040.0f), f3 = __builtin_fmaf(v.w, sc, 12583040.0f);
+                    }
+                    const uint32_t v0 = __builtin_bit_cast(uint32_t, f0), v1 = __builtin_bit_cast(uint32_t, f1);
+                    const uint32_t v2 = __builtin_bit_cast(uint32_t, f2), v3 = __builtin_bit_cast(uint32_t, f3);
+                    const uint32_t p01 = __builtin_amdgcn_perm(v1, v0, 0x05040100u);  // v0.b0 v0.b1 v1.b0 v1.b1
+                    const uint32_t p23 = __builtin_amdgcn_perm(v3, v2, 0x05040100u);
+                    uint8_t *rec = my + (i * MT + t) * 2 * G8_REC + 4 * lane;
+                    *reinterpret_cast<uint32_t *>(rec) = __builtin_amdgcn_perm(p23, p01, 0x07050301u);
+                    *reinterpret_cast<uint32_t *>(rec + G8_REC) =
+                        __builtin_amdgcn_perm(p23, p01, 0x06040200u) ^ 0x80808080u;
+                    // f - (1.5*2^23 + 128) = x_q exactly; a group's 32 of them sum
+                    // to less than 2^19 in magnitude, exact in fp32
+                    const float gs = sum8_f32(((f0 - 12583040.0f) + (f1 - 12583040.0f)) +
+                                              ((f2 - 12583040.0f) + (f3 - 12583040.0f)));
+                    if ((lane & 7) == 0) reinterpret_cast<int *>(xsb)[(i * MT + t) * 8 + (lane >> 3)] = (int)gs;
+                }
+            };
+            if (e2 == 0)
+                quantise(std::false_type{});
+            else
+                quantise(std::true_type{});
         } else {  // padding token of the tile: zero records (its outputs are not stored)
 #pragma unroll
             for (int i = 0; i < C; i++) {

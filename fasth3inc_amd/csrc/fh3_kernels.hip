@@ -1384,8 +1384,9 @@ __global__ __launch_bounds__(LB) void k_gemv8(const uint8_t *__restrict__ W, int
             inv[t] = bad ? __builtin_nanf("") : ldexpf(1.0f, -e1);
             inv2[t] = ldexpf(1.0f, -e2);
             // x_q + (1.5*2^23 + 128) = rne(x * 2^e1 * 2^e2 + 1.5*2^23 + 128); x * 2^e1
-            // is exact (or below 2^-100, where both forms give the constant), so
-            // with e2 = 0, the usual case, one fma with 2^e1 gives the same value
+            // is exact unless it is below 2^-126 in magnitude, where both forms
+            // round to the constant itself, so with e2 = 0, the usual case, one
+            // fma with 2^e1 gives the same value
             auto quantise = [&](auto two_factors) {
 #pragma unroll
                 for (int i = 0; i < C; i++) {

@@ -1031,12 +1031,54 @@ __device__ __forceinline__ half2v magic_fma2(uint32_t a, uint32_t sel, half2v s,
 // sum_k (sc*q)_k x_k of one super-block for TB blocks of 16 tokens x 16
 // weight rows (A: skinny_load_a's fragments; lane (row j, chunk c) holds chunk
 // c of row j); each B operand is built once and used by every token block
+// The 6-bit scales of groups 2q and 2q + 1 (the lane's chunk q) as exact fp16
+// (sc_lo, sc_hi).  Byte g of {sc_b : scales[0..3]} is group g's scale once
+// masked to 6 bits (groups 0-3 are the low bits of scales[0..3], sc_b holds
+// groups 4-7; reference src/core/fh3_quant.c:168-177), so one v_perm with the
+// lane's selector ssel = (2q, zero, 2q + 1, zero) takes both, and 0x6400 in
+// each half makes it the fp16 value 1024 + sc.
+__device__ __forceinline__ half2v q4k_sc_pair(const u32x4 h, uint32_t ssel) {
+    const uint32_t sc_b = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+    const uint32_t x = (__builtin_amdgcn_perm(sc_b, h.y, ssel) & 0x003F003Fu) | 0x64006400u;
+    return __builtin_bit_cast(half2v, x) - half2v{(_Float16)1024.0f, (_Float16)1024.0f};
+}
+
+// The 6-bit mins of groups q and q + 4 in bytes 0 and 2: byte g of
+// {m_b : scales[4..7]} is group g's min once masked (m_b holds groups 4-7),
+// msel = (q, zero, 4 + q, zero).
+__device__ __forceinline__ uint32_t q4k_mn_pair(const u32x4 h, uint32_t msel) {
+    const uint32_t m_b = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+    return __builtin_amdgcn_perm(m_b, h.z, msel) & 0x003F003Fu;
+}
+
+// The lane's scale operands, (1024 + q) * s - 1024 * s for the low nibbles and
+// (1024 + 16q) * (s/16) - 64 * s for the high ones, all products exact in fp16
+// (63 * 1024 < 65504).  One token block: both scales from one v_perm
+// (q4k_sc_pair).  More token blocks: the two field decodes, which measured
+// faster there (17-24 tokens at N = 17408: 21.8 against 24.5 us).
 template <int TB>
-__device__ __forceinline__ void sweep_scq(const u32x4 hv, const u32x4 ca, const u32x4 cb, const Q4kField flo,
-                                          const Q4kField fhi, const half8 (&a)[8][TB], f32x4 (&aq)[TB]) {
-    const uint32_t sclo = q4k_sc(hv, flo), schi = q4k_sc(hv, fhi);
-    const half2v s_lo = splat2(sclo), ns_lo = s_lo * (_Float16)-1024.0f;
-    const half2v s_hi = splat2(schi) * (_Float16)0.0625f, ns_hi = splat2(schi) * (_Float16)-64.0f;
+__device__ __forceinline__ void sweep_scale_ops(const u32x4 hv, uint32_t ssel, const Q4kField flo,
+                                                const Q4kField fhi, half2v &s_lo, half2v &ns_lo, half2v &s_hi,
+                                                half2v &ns_hi) {
+    if constexpr (TB == 1) {
+        const half2v sc = q4k_sc_pair(hv, ssel);
+        const half2v m = sc * half2v{(_Float16)1.0f, (_Float16)0.0625f};
+        const half2v n = sc * half2v{(_Float16)-1024.0f, (_Float16)-64.0f};
+        s_lo = __builtin_shufflevector(m, m, 0, 0), s_hi = __builtin_shufflevector(m, m, 1, 1);
+        ns_lo = __builtin_shufflevector(n, n, 0, 0), ns_hi = __builtin_shufflevector(n, n, 1, 1);
+    } else {
+        const uint32_t sclo = q4k_sc(hv, flo), schi = q4k_sc(hv, fhi);
+        s_lo = splat2(sclo), ns_lo = s_lo * (_Float16)-1024.0f;
+        s_hi = splat2(schi) * (_Float16)0.0625f, ns_hi = splat2(schi) * (_Float16)-64.0f;
+    }
+}
+
+template <int TB>
+__device__ __forceinline__ void sweep_scq(const u32x4 hv, const u32x4 ca, const u32x4 cb, uint32_t ssel,
+                                          const Q4kField flo, const Q4kField fhi, const half8 (&a)[8][TB],
+                                          f32x4 (&aq)[TB]) {
+    half2v s_lo, ns_lo, s_hi, ns_hi;
+    sweep_scale_ops<TB>(hv, ssel, flo, fhi, s_lo, ns_lo, s_hi, ns_hi);
 #pragma unroll
     for (int tb = 0; tb < TB; tb++) aq[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1121,8 +1163,11 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
             }
         }
     }
-    // scale fields of groups 2q (low nibbles) and 2q + 1, min fields of groups
-    // q and q + 4 (the offset MFMA's k)
+    // the scales of groups 2q (low nibbles) and 2q + 1 and the mins of groups
+    // q and q + 4 (the offset MFMA's k): byte selectors (one token block) or
+    // field positions
+    const uint32_t ssel = (uint32_t)(2 * q) | 0x0C00u | ((uint32_t)(2 * q + 1) << 16) | 0x0C000000u;
+    const uint32_t msel = (uint32_t)q | 0x0C00u | ((uint32_t)(4 + q) << 16) | 0x0C000000u;
     const Q4kField flo = q4k_field(2 * q), fhi = q4k_field(2 * q + 1);
     const Q4kField fm0 = q4k_field(q), fm1 = q4k_field(q + 4);
 
@@ -1179,8 +1224,14 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
             const float d = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xFFFFu)) : 0.f;
             const float dmin = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x >> 16)) : 0.f;
             f32x4 aq[TB];
-            sweep_scq<TB>(h, ca[i], cb[i], flo, fhi, a[i], aq);
-            const float bm0 = dmin * (float)q4k_mn(h, fm0), bm1 = dmin * (float)q4k_mn(h, fm1);
+            sweep_scq<TB>(h, ca[i], cb[i], ssel, flo, fhi, a[i], aq);
+            float bm0, bm1;
+            if constexpr (TB == 1) {
+                const uint32_t mp = q4k_mn_pair(h, msel);
+                bm0 = dmin * (float)(mp & 0xFFu), bm1 = dmin * (float)(mp >> 16);
+            } else {
+                bm0 = dmin * (float)q4k_mn(h, fm0), bm1 = dmin * (float)q4k_mn(h, fm1);
+            }
 #pragma unroll
             for (int tb = 0; tb < TB; tb++) {
 #pragma unroll

@@ -48,14 +48,19 @@ struct State {
     DevBuf st_w, st_x, st_y, st_b;  // staging for the host-pointer wrappers
     int path = FH3_HIP_PATH_AUTO;
     // Workspace buffers replaced while captured graphs exist stay allocated
-    // (graphs hold their addresses) until the last graph is destroyed.
+    // (graphs hold their addresses) until the last graph is destroyed; after
+    // a capture begun outside fh3_hip_graph_begin (a caller's own graph, whose
+    // lifetime the library cannot see) they stay until fh3_hip_shutdown.
     int live_graphs = 0;
+    bool foreign_capture = false;
     std::vector<void *> retired;
     std::recursive_mutex mu;
 };
 
 State g;
 thread_local char g_err[512] = "";
+// Set on a thread between fh3_hip_graph_begin and fh3_hip_graph_end.
+thread_local bool t_own_capture = false;
 // Device address of the fixed scratch array of fh3_kernels.hip, per device
 // (bound once per device by fh3_hip_init).
 void *g_scratch[64];
@@ -94,7 +99,7 @@ bool capturing(hipStream_t st) {
 // graph when captured graphs exist (their kernels hold its address).
 int release(DevBuf &b) {
     if (b.p) {
-        if (g.live_graphs > 0) {
+        if (g.live_graphs > 0 || g.foreign_capture) {
             g.retired.push_back(b.p);
         } else {
             FH3_HIPCALL(hipDeviceSynchronize());
@@ -109,8 +114,11 @@ int release(DevBuf &b) {
 // Grow-only device buffer.  A grow allocates, so it is refused while `st` is
 // being captured into a graph: the call must have run once eagerly first.
 int grow(DevBuf &b, size_t need, hipStream_t st) {
+    const bool cap = capturing(st);
+    // a graph the library does not own may now hold this buffer's address
+    if (cap && !t_own_capture) g.foreign_capture = true;
     if (b.cap >= need) return FH3_OK;
-    if (capturing(st))
+    if (cap)
         return set_err(FH3_E_INVALID,
                        "the library workspace must grow to %zu bytes while the stream is captured into a graph; "
                        "run the call once eagerly before capturing it", need);
@@ -123,8 +131,26 @@ int grow(DevBuf &b, size_t need, hipStream_t st) {
 
 int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
+// Longest row (in) any product takes: rows of up to fh3k_max_in() values that
+// are whole super-blocks run the kernels that read Q4_K in place; other rows
+// ("general rows": in % 256 != 0, or in > fh3k_max_in()) are decoded to fp16
+// rows zero-padded to kpad(in) columns.
+constexpr int64_t kMaxInGeneral = (int64_t)1 << 24;
+bool general_rows(int64_t in) { return in % 256 != 0 || in > fh3k_max_in(); }
+int64_t kpad(int64_t in) { return round_up(in, 256); }
+
+// Kernel family of the fp16-row products (weights of another type than Q4_K,
+// and general rows of any type): k_skinny16 up to 64 tokens on padded rows of
+// at most fh3k_max_in() values, else k_gemm16.
+int path16(int n_tok, int64_t in) {
+    if (g.path == FH3_HIP_PATH_GEMM) return FH3_HIP_PATH_GEMM;
+    return n_tok <= fh3k_skinny_max_tokens() && kpad(in) <= fh3k_max_in() ? FH3_HIP_PATH_SKINNY
+                                                                            : FH3_HIP_PATH_GEMM;
+}
+
 // A forced path that cannot take the shape falls back to the automatic choice.
 int choose_path(int n_tok, int64_t in) {
+    if (general_rows(in)) return path16(n_tok, in);
     const bool g8 = in <= fh3k_max_in() && fh3k_gemv8_fits((int)in, n_tok);
     const bool sw = in <= fh3k_max_in() && fh3k_sweep_fits((int)in, n_tok);
     if (g.path == FH3_HIP_PATH_GEMV8 && g8) return FH3_HIP_PATH_GEMV8;
@@ -273,6 +299,8 @@ extern "C" void fh3_hip_shutdown(void) {
     g.regs.clear();
     for (void *p : g.retired) (void)hipFree(p);
     g.retired.clear();
+    g.foreign_capture = false;
+    g.live_graphs = 0;
     for (int &k : g.vsa_key) k = -1;  // the VSA geometry was freed with vsa_geo
     g.vsa_T = g.vsa_P = 0;
     (void)hipStreamDestroy(g.stream);
@@ -339,12 +367,14 @@ extern "C" int fh3_hip_graph_begin(void *stream) {
     int rc = ensure_init();
     if (rc != FH3_OK) return rc;
     FH3_HIPCALL(hipStreamBeginCapture(stream ? (hipStream_t)stream : g.stream, hipStreamCaptureModeThreadLocal));
+    t_own_capture = true;
     return FH3_OK;
 }
 
 extern "C" int fh3_hip_graph_end(void *stream, void **graph_exec) {
     if (!graph_exec) return set_err(FH3_E_INVALID, "fh3_hip_graph_end: NULL out pointer");
     hipGraph_t graph = nullptr;
+    t_own_capture = false;
     FH3_HIPCALL(hipStreamEndCapture(stream ? (hipStream_t)stream : g.stream, &graph));
     hipGraphExec_t exec = nullptr;
     hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
@@ -366,7 +396,7 @@ extern "C" int fh3_hip_graph_destroy(void *graph_exec) {
     if (!graph_exec) return FH3_OK;
     FH3_HIPCALL(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
     std::lock_guard<std::recursive_mutex> lk(g.mu);
-    if (g.live_graphs > 0 && --g.live_graphs == 0 && !g.retired.empty()) {
+    if (g.live_graphs > 0 && --g.live_graphs == 0 && !g.foreign_capture && !g.retired.empty()) {
         // no graph holds the replaced workspace buffers any more
         hipError_t e = hipDeviceSynchronize();
         for (void *p : g.retired) {
@@ -411,13 +441,16 @@ extern "C" int fh3_hip_dequant_dev(int type, const void *d_src, float *d_dst, in
 static int check_weights(const Fh3W *w, const char *fn) {
     if (!w || !w->data || w->in <= 0 || w->out <= 0)
         return set_err(FH3_E_INVALID, "%s: NULL weights or non-positive size", fn);
-    if (fh3k_dequant_block_len(w->type) == 0)
-        return set_err(FH3_E_INVALID, "%s: unsupported weight type %d", fn, w->type);
-    if (w->in % 256)
-        return set_err(FH3_E_INVALID, "%s: in=%lld is not a multiple of 256", fn, (long long)w->in);
-    if (w->in > fh3k_max_in() || w->out > 0x7FFFFFFF)
-        return set_err(FH3_E_INVALID, "%s: in=%lld out=%lld out of range (in <= %d)", fn, (long long)w->in,
-                       (long long)w->out, fh3k_max_in());
+    const int bl = fh3k_dequant_block_len(w->type);
+    if (bl == 0) return set_err(FH3_E_INVALID, "%s: unsupported weight type %d", fn, w->type);
+    // a row must be whole blocks of its type: the reference decodes whole
+    // blocks only and leaves the rest of such a row undefined
+    if (w->in % bl)
+        return set_err(FH3_E_INVALID, "%s: in=%lld is not a multiple of the type's block length %d", fn,
+                       (long long)w->in, bl);
+    if (w->in > kMaxInGeneral || w->out > 0x7FFFFFFF)
+        return set_err(FH3_E_INVALID, "%s: in=%lld out=%lld out of range (in <= %lld)", fn, (long long)w->in,
+                       (long long)w->out, (long long)kMaxInGeneral);
     if ((uintptr_t)w->data & 15u) return set_err(FH3_E_INVALID, "%s: weights must be 16-byte aligned", fn);
     return FH3_OK;
 }
@@ -428,7 +461,7 @@ static int check_weights(const Fh3W *w, const char *fn) {
 // 256-byte boundary: the FH3_HIP_PATH_SWEEP kernel's offsets.
 static int64_t prep_rows(int n_tok) { return round_up(n_tok, fh3k_gemm_row_pad()); }
 static size_t prep_scale_offset(int n_tok, int64_t in) {
-    return (size_t)round_up(prep_rows(n_tok) * in * 2, 256);
+    return (size_t)round_up(prep_rows(n_tok) * kpad(in) * 2, 256);
 }
 static size_t prep_sum_offset(int n_tok, int64_t in) {
     return (size_t)round_up((int64_t)(prep_scale_offset(n_tok, in) + (size_t)prep_rows(n_tok) * sizeof(float)), 256);
@@ -436,7 +469,9 @@ static size_t prep_sum_offset(int n_tok, int64_t in) {
 
 extern "C" size_t fh3_hip_prepared_bytes(int n_tok, int64_t in) {
     if (n_tok <= 0 || in <= 0) return 0;
-    const size_t sums = n_tok <= fh3k_sweep_max_tokens() ? (size_t)n_tok * (size_t)(in / 32) * sizeof(float) : 0;
+    const size_t sums = n_tok <= fh3k_sweep_max_tokens() && !general_rows(in)
+                            ? (size_t)n_tok * (size_t)(in / 32) * sizeof(float)
+                            : 0;
     return prep_sum_offset(n_tok, in) + sums;
 }
 
@@ -448,7 +483,19 @@ static const float *prep_sums(const void *prep, int n_tok, int64_t in) {
     return (const float *)((const char *)prep + prep_sum_offset(n_tok, in));
 }
 
+// Where the preparation writes the group sums: for every fragment form of up
+// to fh3k_sweep_max_tokens() tokens, whichever kernel the current path
+// setting picks, so that a prepared buffer stays valid for k_sweep when the
+// setting changes between preparation and product.
+static float *prep_sums_out(void *prep, int n_tok, int64_t in) {
+    return n_tok <= fh3k_sweep_max_tokens() && !general_rows(in) ? (float *)prep_sums(prep, n_tok, in) : nullptr;
+}
+
 static int prepare(const float *d_x, int n_tok, int64_t in, void *d_prep, int64_t rows, hipStream_t st) {
+    if (general_rows(in)) {
+        FH3_HIPCALL(fh3k_xprep_any(d_x, n_tok, (int)in, (int)rows, d_prep, (float *)prep_scales(d_prep, n_tok, in), st));
+        return FH3_OK;
+    }
     const int path = choose_path(n_tok, in);
     if (path == FH3_HIP_PATH_GEMV8) {
         // that kernel quantises fp32 activations itself: the prepared form is x
@@ -457,8 +504,7 @@ static int prepare(const float *d_x, int n_tok, int64_t in, void *d_prep, int64_
         return FH3_OK;
     }
     float *xs_inv = (float *)prep_scales(d_prep, n_tok, in);
-    float *xsum = path == FH3_HIP_PATH_SWEEP ? (float *)prep_sums(d_prep, n_tok, in) : nullptr;
-    FH3_HIPCALL(fh3k_xprep(d_x, n_tok, (int)in, (int)rows, d_prep, xs_inv, xsum, st));
+    FH3_HIPCALL(fh3k_xprep(d_x, n_tok, (int)in, (int)rows, d_prep, xs_inv, prep_sums_out(d_prep, n_tok, in), st));
     return FH3_OK;
 }
 
@@ -470,7 +516,7 @@ static int64_t kernel_rows(int path, int n_tok) {
 }
 
 extern "C" int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, void *d_prep, void *stream) {
-    if (!d_x || !d_prep || n_tok <= 0 || in <= 0 || in % 256 || in > fh3k_max_in())
+    if (!d_x || !d_prep || n_tok <= 0 || in <= 0 || in > kMaxInGeneral)
         return set_err(FH3_E_INVALID, "fh3_hip_prepare_x_dev: bad arguments");
     if (((uintptr_t)d_x & 15u) || ((uintptr_t)d_prep & 15u))
         return set_err(FH3_E_INVALID, "fh3_hip_prepare_x_dev: pointers must be 16-byte aligned");
@@ -479,33 +525,40 @@ extern "C" int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, vo
     return prepare(d_x, n_tok, in, d_prep, prep_rows(n_tok), stream ? (hipStream_t)stream : g.stream);
 }
 
-// Weights of another type than Q4_K: Q5_K and Q6_K up to 64 tokens are read
-// in place by k_skinny; otherwise fp16 rows (the weight itself for F16, else
-// decoded into the library's w16 buffer), then k_skinny16 / k_gemm16.
-static int path16(int n_tok) {
-    if (g.path == FH3_HIP_PATH_GEMM) return FH3_HIP_PATH_GEMM;
-    return n_tok <= fh3k_skinny_max_tokens() ? FH3_HIP_PATH_SKINNY : FH3_HIP_PATH_GEMM;
+// Weights of another type than Q4_K, and general rows of any type: Q5_K and
+// Q6_K rows of whole super-blocks up to 64 tokens are read in place by
+// k_skinny; otherwise fp16 rows of kpad(in) columns (the weight itself for
+// F16 rows of whole super-blocks, else decoded, zero-padded, into the
+// library's w16 buffer), then k_skinny16 / k_gemm16.
+static bool reads_in_place_q(const Fh3W *w, int n_tok) {
+    return !general_rows(w->in) && path16(n_tok, w->in) == FH3_HIP_PATH_SKINNY && fh3k_skinny_q_takes(w->type);
+}
+
+static size_t w16_bytes(const Fh3W *w, int n_tok) {
+    if (reads_in_place_q(w, n_tok) || (w->type == FH3_QUANT_F16 && !general_rows(w->in))) return 0;
+    return (size_t)w->out * (size_t)kpad(w->in) * 2;
 }
 
 static int product16(const Fh3W *w, const void *x16, const float *xs_inv, int n_tok, const float *bias, float *d_y,
                      hipStream_t st) {
-    const int K = (int)w->in, N = (int)w->out;
-    if (path16(n_tok) == FH3_HIP_PATH_SKINNY && fh3k_skinny_q_takes(w->type)) {
+    const int K = (int)w->in, Kp = (int)kpad(w->in), N = (int)w->out;
+    if (reads_in_place_q(w, n_tok)) {
         FH3_HIPCALL(fh3k_skinny_q(w->type, w->data, (int64_t)fh3_row_bytes(w->type, w->in), N, K, x16, xs_inv, bias,
                                   d_y, n_tok, st));
         return FH3_OK;
     }
     const void *w16 = w->data;
-    if (w->type != FH3_QUANT_F16) {
-        int rc = grow(g.w16, (size_t)w->out * (size_t)w->in * 2, st);
+    if (const size_t wb = w16_bytes(w, n_tok)) {
+        int rc = grow(g.w16, wb, st);
         if (rc != FH3_OK) return rc;
-        FH3_HIPCALL(fh3k_weights_f16(w->type, w->data, (int64_t)fh3_row_bytes(w->type, w->in), K, N, g.w16.p, st));
+        FH3_HIPCALL(fh3k_weights_f16(w->type, w->data, (int64_t)fh3_row_bytes(w->type, w->in), K, Kp, N, g.w16.p,
+                                     st));
         w16 = g.w16.p;
     }
-    if (path16(n_tok) == FH3_HIP_PATH_SKINNY)
-        FH3_HIPCALL(fh3k_skinny16(w16, N, K, x16, xs_inv, bias, d_y, n_tok, st));
+    if (path16(n_tok, w->in) == FH3_HIP_PATH_SKINNY)
+        FH3_HIPCALL(fh3k_skinny16(w16, N, Kp, x16, xs_inv, bias, d_y, n_tok, st));
     else
-        FH3_HIPCALL(fh3k_gemm16(w16, N, K, x16, xs_inv, bias, d_y, n_tok, st));
+        FH3_HIPCALL(fh3k_gemm16(w16, N, Kp, x16, xs_inv, bias, d_y, n_tok, st));
     return FH3_OK;
 }
 
@@ -524,7 +577,7 @@ static size_t part_bytes(const Fh3W *w, int n_tok, int epi) {
 // part_bytes()), else in the library's grow-only buffer.
 static int product(const Fh3W *w, const void *prep, int n_tok, const float *bias, float *d_y, hipStream_t st,
                    int epi = FH3_EPI_NONE, const float *aux = nullptr, float *part_ext = nullptr) {
-    if (w->type != FH3_QUANT_Q4_K) {
+    if (w->type != FH3_QUANT_Q4_K || general_rows(w->in)) {
         std::lock_guard<std::recursive_mutex> lk(g.mu);
         if (choose_path(n_tok, w->in) == FH3_HIP_PATH_GEMV8) {
             // the prepared form is then a copy of x: make the fragments here
@@ -586,7 +639,9 @@ extern "C" int fh3_hip_matmul_prepared_dev(const Fh3W *w, const void *d_prep, fl
 static int check_epi(const Fh3W *w, int epi, const float *aux, const char *fn) {
     if (epi == FH3_EPI_NONE) return FH3_OK;
     if (epi != FH3_EPI_GATE_RESIDUAL && epi != FH3_EPI_SWIGLU) return set_err(FH3_E_INVALID, "%s: bad epilogue %d", fn, epi);
-    if (w->type != FH3_QUANT_Q4_K) return set_err(FH3_E_INVALID, "%s: fused epilogues take Q4_K weights", fn);
+    if (w->type != FH3_QUANT_Q4_K || general_rows(w->in))
+        return set_err(FH3_E_INVALID, "%s: fused epilogues take Q4_K weights with in %% 256 == 0 and in <= %d", fn,
+                       fh3k_max_in());
     if (epi == FH3_EPI_SWIGLU && w->out % 128)
         return set_err(FH3_E_INVALID, "%s: SwiGLU needs out %% 128 == 0 (out=%lld)", fn, (long long)w->out);
     if (epi == FH3_EPI_GATE_RESIDUAL && !aux) return set_err(FH3_E_INVALID, "%s: gate-residual needs the gate", fn);
@@ -604,13 +659,16 @@ static int matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok, co
     rc = ensure_init();
     if (rc != FH3_OK) return rc;
     hipStream_t st = stream ? (hipStream_t)stream : g.stream;
-    if (w->type != FH3_QUANT_Q4_K) {
+    if (w->type != FH3_QUANT_Q4_K || general_rows(w->in)) {
         std::lock_guard<std::recursive_mutex> lk(g.mu);
-        const int64_t rows = path16(n_tok) == FH3_HIP_PATH_SKINNY ? round_up(n_tok, 32) : prep_rows(n_tok);
+        const int64_t rows = path16(n_tok, w->in) == FH3_HIP_PATH_SKINNY ? round_up(n_tok, 32) : prep_rows(n_tok);
         rc = grow(g.ws, fh3_hip_prepared_bytes(n_tok, w->in), st);
         if (rc != FH3_OK) return rc;
         float *xs = (float *)prep_scales(g.ws.p, n_tok, w->in);
-        FH3_HIPCALL(fh3k_xprep(d_x, n_tok, (int)w->in, (int)rows, g.ws.p, xs, nullptr, st));
+        if (general_rows(w->in))
+            FH3_HIPCALL(fh3k_xprep_any(d_x, n_tok, (int)w->in, (int)rows, g.ws.p, xs, st));
+        else
+            FH3_HIPCALL(fh3k_xprep(d_x, n_tok, (int)w->in, (int)rows, g.ws.p, xs, nullptr, st));
         return product16(w, g.ws.p, xs, n_tok, d_bias_or_null, d_y, st);
     }
     const int path = choose_path(n_tok, w->in);
@@ -654,14 +712,13 @@ extern "C" int fh3_hip_matmul_prepared_epi_dev(const Fh3W *w, const void *d_prep
 }
 
 extern "C" size_t fh3_hip_matmul_workspace_bytes(const Fh3W *w, int n_tok, int epi, int prepared) {
-    if (!w || w->in <= 0 || w->out <= 0 || n_tok <= 0 || w->in % 256 || w->in > fh3k_max_in() ||
-        fh3k_dequant_block_len(w->type) == 0)
+    const int bl = w ? fh3k_dequant_block_len(w->type) : 0;
+    if (!w || w->in <= 0 || w->out <= 0 || n_tok <= 0 || bl == 0 || w->in % bl || w->in > kMaxInGeneral)
         return 0;
     const size_t prep = fh3_hip_prepared_bytes(n_tok, w->in);
-    if (w->type != FH3_QUANT_Q4_K) {
-        const size_t w16 = w->type == FH3_QUANT_F16 ? 0 : (size_t)w->out * (size_t)w->in * 2;
+    if (w->type != FH3_QUANT_Q4_K || general_rows(w->in)) {
         const bool own_prep = !prepared || choose_path(n_tok, w->in) == FH3_HIP_PATH_GEMV8;
-        return w16 + (own_prep ? prep : 0);
+        return w16_bytes(w, n_tok) + (own_prep ? prep : 0);
     }
     const bool gemv8 = choose_path(n_tok, w->in) == FH3_HIP_PATH_GEMV8;
     return (prepared || gemv8 ? 0 : prep) + part_bytes(w, n_tok, epi);
@@ -676,6 +733,9 @@ extern "C" int fh3_hip_matmul_noalloc_dev(const Fh3W *w, const float *d_x, float
     int rc = check_weights(w, fn);
     if (rc != FH3_OK) return rc;
     if (w->type != FH3_QUANT_Q4_K) return set_err(FH3_E_INVALID, "%s: Q4_K weights only (type %d)", fn, w->type);
+    if (general_rows(w->in))
+        return set_err(FH3_E_INVALID, "%s: in=%lld; rows of more than %d values take fh3_hip_matmul_dev", fn,
+                       (long long)w->in, fh3k_max_in());
     if (!d_x || !d_y || n_tok <= 0) return set_err(FH3_E_INVALID, "%s: NULL pointer or n_tok <= 0", fn);
     if ((uintptr_t)d_x & 15u) return set_err(FH3_E_INVALID, "%s: x must be 16-byte aligned", fn);
     if (!g.init || !g_scratch[g.device])
@@ -717,7 +777,7 @@ extern "C" int fh3_hip_prepare_x_norm_dev(const float *d_x, int n_tok, int64_t i
         return FH3_OK;
     }
     float *xs_inv = (float *)prep_scales(d_prep, n_tok, in);
-    float *xsum = choose_path(n_tok, in) == FH3_HIP_PATH_SWEEP ? (float *)prep_sums(d_prep, n_tok, in) : nullptr;
+    float *xsum = prep_sums_out(d_prep, n_tok, in);
     FH3_HIPCALL(fh3k_xprep_norm(d_x, n_tok, (int)in, (int)prep_rows(n_tok), d_prep, xs_inv, d_norm_w, eps, d_shift,
                                 d_scale, xsum, st));
     return FH3_OK;
@@ -907,7 +967,7 @@ static int vsa_plan(const Fh3Seq *sq, int tile, hipStream_t st, const char *fn) 
     }
     // captured graphs keep reading the geometry they were captured with: give
     // the new one its own buffer
-    int rc = g.live_graphs > 0 ? release(g.vsa_geo) : FH3_OK;
+    int rc = g.live_graphs > 0 || g.foreign_capture ? release(g.vsa_geo) : FH3_OK;
     if (rc == FH3_OK) rc = grow(g.vsa_geo, host.size() * sizeof(int), st);
     if (rc != FH3_OK) return rc;
     FH3_HIPCALL(hipDeviceSynchronize());  // earlier calls may still read the old geometry

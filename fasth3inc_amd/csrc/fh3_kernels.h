@@ -48,10 +48,17 @@ hipError_t fh3k_gemv8(const void *W, int64_t row_bytes, int N, int K, const floa
 int fh3k_gemv8_max_tokens(void);
 int fh3k_gemv8_fits(int K, int M);
 
-// Weights of any decodable type as fp16 rows dst[N][K] (the exact fp32 value
-// rounded once; F16 copied), K % 256 == 0; then the fp16-row products, same
-// activation fragments and launch rules as fh3k_skinny / fh3k_gemm.
-hipError_t fh3k_weights_f16(int type, const void *src, int64_t row_bytes, int K, int N, void *dst, hipStream_t st);
+// Weights of any decodable type as fp16 rows dst[N][Kp] (the exact fp32 value
+// rounded once; F16 copied), K a multiple of the type's block length, Kp >= K
+// a multiple of 256, columns K..Kp-1 zero; then the fp16-row products, same
+// activation fragments and launch rules as fh3k_skinny / fh3k_gemm (with Kp
+// as their K).
+hipError_t fh3k_weights_f16(int type, const void *src, int64_t row_bytes, int K, int Kp, int N, void *dst,
+                            hipStream_t st);
+// x[M][K] fp32 with any K and 4-byte alignment -> x16 fragments of
+// Kp = round_up(K, 256) columns (zeros at k >= K) and xs_inv[Mpad], with
+// fh3k_xprep's scale rule and rounding (the same bits where both apply).
+hipError_t fh3k_xprep_any(const float *x, int M, int K, int Mpad, void *x16, float *xs_inv, hipStream_t st);
 hipError_t fh3k_skinny16(const void *W16, int N, int K, const void *x16, const float *xs_inv, const float *bias,
                          float *y, int M, hipStream_t st);
 hipError_t fh3k_gemm16(const void *W16, int N, int K, const void *x16, const float *xs_inv, const float *bias,

@@ -445,6 +445,48 @@ __global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ X, int 
     }
 }
 
+// Activations of any row length K and alignment (rows of the run-once
+// projections: 32, 96, 64 or 128 values, or more than 32768) -> X16 fragments
+// of Kp = round_up(K, 256) columns, zeros at k >= K.  The scale rule and the
+// rounding are k_xprep's, so for a K that k_xprep takes the output is the
+// same bit for bit.  The row is read twice (its maximum, then the
+// fragments), so K is not bounded by one workgroup's registers.  Rows
+// M..gridDim.x-1 are written as zeros with scale 1.
+__global__ __launch_bounds__(256) void k_xprep_any(const float *__restrict__ X, int M, int K, int Kp,
+                                                   half8 *__restrict__ X16, float *__restrict__ xs_inv) {
+    __shared__ float s_red[4];
+    const int t = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float *xr = X + (size_t)t * K;
+    const int kv = t < M ? K : 0;
+    float mx = 0.f;
+    for (int k = tid; k < kv; k += 256) mx = fmaxf(mx, fabsf(xr[k]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (lane == 0) s_red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    int e = 0;
+    if (mx > 0.f && mx <= 3.4028234663852886e38f) {
+        int E;
+        (void)frexpf(mx, &E);
+        e = 15 - E;
+        e = e > 126 ? 126 : (e < -126 ? -126 : e);
+    }
+    const float s = ldexpf(1.0f, e);
+    if (tid == 0) xs_inv[t] = ldexpf(1.0f, -e);
+    const int kf_n = Kp / 16;
+    half4 *dst = reinterpret_cast<half4 *>(X16 + (size_t)(t >> 5) * kf_n * 64 + (t & 31));
+    for (int k4 = tid; k4 < Kp / 4; k4 += 256) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = 4 * k4 + i < kv ? xr[4 * k4 + i] : 0.f;
+        const half4 h = {(_Float16)(v[0] * s), (_Float16)(v[1] * s), (_Float16)(v[2] * s), (_Float16)(v[3] * s)};
+        // fragment k4/4, lane half (k4/2)&1, 8-byte half k4&1 (as k_xprep)
+        dst[(size_t)(k4 >> 2) * 128 + ((k4 >> 1) & 1) * 64 + (k4 & 1)] = h;
+    }
+}
+
 // Large-M preparation: RW = 8 (or 4) consecutive rows per 1024-thread
 // workgroup.  Thread (r = lane % RW, cc = tid / RW) owns row t0 + r and its
 // 8-float chunks c = cc + (1024/RW) i (V per thread, K <= 8 V (1024/RW)).  The
@@ -2056,11 +2098,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
 // fp16, as k_gemm rounds Q4_K -- and multiplied by k_skinny16 / k_gemm16, which
 // read those rows directly.  F16 weights are used as they are.
 // ---------------------------------------------------------------------------
+// Output rows hold nblk_out >= nblk blocks; blocks nblk.. of a row (the
+// padding up to a whole number of 256-column steps) are written as zeros.
 template <int T>
 __global__ __launch_bounds__(256) void k_weights_f16_blocks(const uint8_t *__restrict__ src, int64_t row_bytes,
-                                                            int64_t nblk, int64_t rows, _Float16 *__restrict__ dst) {
+                                                            int64_t nblk, int64_t nblk_out, int64_t rows,
+                                                            _Float16 *__restrict__ dst) {
     constexpr int BL = Fmt<T>::BL, BB = Fmt<T>::BB, P = Fmt<T>::P;
-    const int64_t per_row = nblk * P;
+    const int64_t per_row = nblk_out * P;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= rows * per_row) return;
     const int64_t row = gid / per_row;
@@ -2068,8 +2113,13 @@ __global__ __launch_bounds__(256) void k_weights_f16_blocks(const uint8_t *__res
     const int64_t b = rem / P;
     const int G = (int)(rem - b * P);
     float o[16];
-    deq_piece<T>(src + row * row_bytes + b * BB, G, o);
-    half8 *out = reinterpret_cast<half8 *>(dst + row * nblk * BL + b * BL + 16 * G);
+    if (b < nblk) {
+        deq_piece<T>(src + row * row_bytes + b * BB, G, o);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 16; e++) o[e] = 0.f;
+    }
+    half8 *out = reinterpret_cast<half8 *>(dst + row * nblk_out * BL + b * BL + 16 * G);
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         half8 h;
@@ -2077,6 +2127,41 @@ __global__ __launch_bounds__(256) void k_weights_f16_blocks(const uint8_t *__res
         for (int e = 0; e < 8; e++) h[e] = (_Float16)o[8 * j + e];
         out[j] = h;
     }
+}
+
+// F32 / F16 / BF16 rows of any length K (rows row_bytes apart, element
+// aligned) -> fp16 rows of Kp >= K columns (Kp % 8 == 0), zeros at k >= K;
+// 8 outputs per thread.  F16 values are copied bit for bit, the others rounded
+// once to fp16 as k_weights_f16_elem rounds them.
+template <int T>
+__global__ __launch_bounds__(256) void k_weights_f16_any(const uint8_t *__restrict__ src, int64_t row_bytes, int K,
+                                                         int Kp, int64_t rows, _Float16 *__restrict__ dst) {
+    const int64_t per_row = Kp / 8;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= rows * per_row) return;
+    const int64_t row = gid / per_row;
+    const int k0 = (int)(gid - row * per_row) * 8;
+    const uint8_t *s = src + row * row_bytes;
+    uint32_t bits[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const int k = k0 + e;
+        uint32_t b = 0;
+        if (k < K) {
+            if constexpr (T == FH3K_F16) {
+                b = reinterpret_cast<const uint16_t *>(s)[k];
+            } else if constexpr (T == FH3K_BF16) {
+                const float f = __builtin_bit_cast(float, (uint32_t)reinterpret_cast<const uint16_t *>(s)[k] << 16);
+                b = __builtin_bit_cast(uint16_t, (_Float16)f);
+            } else {
+                b = __builtin_bit_cast(uint16_t, (_Float16)reinterpret_cast<const float *>(s)[k]);
+            }
+        }
+        bits[e] = b;
+    }
+    const u32x4 v = {bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16), bits[4] | (bits[5] << 16),
+                     bits[6] | (bits[7] << 16)};
+    *reinterpret_cast<u32x4 *>(dst + row * Kp + k0) = v;
 }
 
 // F32 / BF16 rows -> fp16, 8 elements per thread (n % 8 == 0).
@@ -2363,6 +2448,15 @@ extern "C" hipError_t fh3k_xprep_norm(const float *x, int M, int K, int Mpad, vo
 extern "C" hipError_t fh3k_xprep(const float *x, int M, int K, int Mpad, void *x16, float *xs_inv,
                                  float *xsum, hipStream_t st) {
     return fh3k_xprep_norm(x, M, K, Mpad, x16, xs_inv, nullptr, 0.f, nullptr, nullptr, xsum, st);
+}
+
+extern "C" hipError_t fh3k_xprep_any(const float *x, int M, int K, int Mpad, void *x16, float *xs_inv,
+                                     hipStream_t st) {
+    if (M <= 0 || K <= 0 || Mpad < M || Mpad % 32) return hipErrorInvalidValue;
+    const int64_t Kp = (int64_t)(K + 255) / 256 * 256;
+    if (Kp > 0x7FFFFFFF) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_xprep_any, dim3((unsigned)Mpad), dim3(256), 0, st, x, M, K, (int)Kp, (half8 *)x16, xs_inv);
+    return hipGetLastError();
 }
 
 extern "C" hipError_t fh3k_rownorm_f32(const float *x, int M, int K, float *y, const float *norm_w, float eps,
@@ -2951,23 +3045,33 @@ extern "C" hipError_t fh3k_gemm_epi(const void *W, int64_t row_bytes, int N, int
 // Other weight types: decode to fp16 rows, then k_skinny16 / k_gemm16
 // ---------------------------------------------------------------------------
 template <int T>
-static hipError_t launch_weights_f16_blocks(const void *src, int64_t row_bytes, int64_t n, int64_t rows,
-                                            void *dst, hipStream_t st) {
-    const int64_t nblk = n / Fmt<T>::BL;
-    const int64_t blocks = (rows * nblk * Fmt<T>::P + 255) / 256;
+static hipError_t launch_weights_f16_blocks(const void *src, int64_t row_bytes, int64_t n, int64_t n_out,
+                                            int64_t rows, void *dst, hipStream_t st) {
+    const int64_t nblk = n / Fmt<T>::BL, nblk_out = n_out / Fmt<T>::BL;
+    const int64_t blocks = (rows * nblk_out * Fmt<T>::P + 255) / 256;
     if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_weights_f16_blocks<T>, dim3((unsigned)blocks), dim3(256), 0, st, (const uint8_t *)src,
-                       row_bytes, nblk, rows, (_Float16 *)dst);
+                       row_bytes, nblk, nblk_out, rows, (_Float16 *)dst);
     return hipGetLastError();
 }
 
-extern "C" hipError_t fh3k_weights_f16(int type, const void *src, int64_t row_bytes, int K, int N, void *dst,
-                                       hipStream_t st) {
+template <int T>
+static hipError_t launch_weights_f16_any(const void *src, int64_t row_bytes, int K, int Kp, int64_t rows,
+                                         void *dst, hipStream_t st) {
+    const int64_t blocks = (rows * (Kp / 8) + 255) / 256;
+    if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_weights_f16_any<T>, dim3((unsigned)blocks), dim3(256), 0, st, (const uint8_t *)src,
+                       row_bytes, K, Kp, rows, (_Float16 *)dst);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t fh3k_weights_f16(int type, const void *src, int64_t row_bytes, int K, int Kp, int N,
+                                       void *dst, hipStream_t st) {
     const int bl = fh3k_dequant_block_len(type);
-    if (bl == 0 || K <= 0 || N <= 0 || K % 256) return hipErrorInvalidValue;
-    if (type == FH3K_F16)
+    if (bl == 0 || K <= 0 || N <= 0 || K % bl || Kp < K || Kp % 256) return hipErrorInvalidValue;
+    if (type == FH3K_F16 && Kp == K)
         return hipMemcpyAsync(dst, src, (size_t)N * K * 2, hipMemcpyDeviceToDevice, st);
-    if (type == FH3K_F32 || type == FH3K_BF16) {
+    if ((type == FH3K_F32 || type == FH3K_BF16) && Kp == K) {
         const int64_t n8 = (int64_t)N * K / 8, blocks = (n8 + 255) / 256;
         if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
         if (type == FH3K_BF16)
@@ -2979,12 +3083,15 @@ extern "C" hipError_t fh3k_weights_f16(int type, const void *src, int64_t row_by
         return hipGetLastError();
     }
     switch (type) {
-        case FH3K_Q8_0: return launch_weights_f16_blocks<FH3K_Q8_0>(src, row_bytes, K, N, dst, st);
-        case FH3K_Q2_K: return launch_weights_f16_blocks<FH3K_Q2_K>(src, row_bytes, K, N, dst, st);
-        case FH3K_Q3_K: return launch_weights_f16_blocks<FH3K_Q3_K>(src, row_bytes, K, N, dst, st);
-        case FH3K_Q4_K: return launch_weights_f16_blocks<FH3K_Q4_K>(src, row_bytes, K, N, dst, st);
-        case FH3K_Q5_K: return launch_weights_f16_blocks<FH3K_Q5_K>(src, row_bytes, K, N, dst, st);
-        default: return launch_weights_f16_blocks<FH3K_Q6_K>(src, row_bytes, K, N, dst, st);
+        case FH3K_F32: return launch_weights_f16_any<FH3K_F32>(src, row_bytes, K, Kp, N, dst, st);
+        case FH3K_F16: return launch_weights_f16_any<FH3K_F16>(src, row_bytes, K, Kp, N, dst, st);
+        case FH3K_BF16: return launch_weights_f16_any<FH3K_BF16>(src, row_bytes, K, Kp, N, dst, st);
+        case FH3K_Q8_0: return launch_weights_f16_blocks<FH3K_Q8_0>(src, row_bytes, K, Kp, N, dst, st);
+        case FH3K_Q2_K: return launch_weights_f16_blocks<FH3K_Q2_K>(src, row_bytes, K, Kp, N, dst, st);
+        case FH3K_Q3_K: return launch_weights_f16_blocks<FH3K_Q3_K>(src, row_bytes, K, Kp, N, dst, st);
+        case FH3K_Q4_K: return launch_weights_f16_blocks<FH3K_Q4_K>(src, row_bytes, K, Kp, N, dst, st);
+        case FH3K_Q5_K: return launch_weights_f16_blocks<FH3K_Q5_K>(src, row_bytes, K, Kp, N, dst, st);
+        default: return launch_weights_f16_blocks<FH3K_Q6_K>(src, row_bytes, K, Kp, N, dst, st);
     }
 }
 

@@ -115,8 +115,11 @@ void fh3_dequant(int type, const void *src, float *dst, int64_t n);
  * on the GPU (inputs are copied in and y out on every call).  NULL pointers or
  * non-positive sizes are a silent no-op, as in the reference.  Weight types:
  * every type fh3_dequant decodes (Q4_K on its own kernels; F32, F16, BF16,
- * Q8_0, Q2_K, Q3_K, Q5_K, Q6_K decoded per call to fp16 rows), in % 256 == 0;
- * other types print "unsupported" and leave y unwritten.  Results are
+ * Q8_0, Q2_K, Q3_K, Q5_K, Q6_K decoded per call to fp16 rows).  in is any
+ * length for F32, F16 and BF16 (e.g. the DiT's 32- and 96-value patch rows),
+ * a multiple of 32 for Q8_0 and of 256 for the K types (whole blocks, the
+ * rows the reference defines), up to 2^24; other types or in print an error
+ * and leave y unwritten.  Results are
  * deterministic run to run; they match the CPU path within rel-Frobenius 2e-3
  * (fp16 or int16 operands, fp32 accumulation).  Replaces
  * src/core/fh3_ops.c:317-404. */

@@ -52,11 +52,16 @@ int fh3_hip_dequant_dev(int type, const void *d_src, float *d_dst, int64_t rows,
  * (+ d_bias).  w->data is a device pointer to the packed rows (16-byte
  * aligned; d_x 16-byte aligned, d_y and d_bias any float pointer: a 16-byte
  * aligned d_y with out % 4 == 0 takes the faster full-block stores of the
- * large-M kernel), w->in % 256 == 0.  Q4_K runs the kernels described here; the
- * other types fh3_dequant decodes are first decoded to fp16 rows (the exact
- * value rounded once; F16 used as it is) into a library buffer of
- * out * in * 2 bytes, then multiplied with the same activation handling and
- * fp32 accumulation.  Work is enqueued on `stream` and the call
+ * large-M kernel).  w->in: any length up to 2^24 for F32, F16 and BF16, a
+ * multiple of 32 for Q8_0, of 256 for the K types (FH3_E_INVALID otherwise).
+ * Q4_K rows of whole super-blocks up to 32768 values run the kernels described
+ * here; the other types fh3_dequant decodes, and rows of any type with
+ * in % 256 != 0 or in > 32768, are first decoded to fp16 rows of
+ * round_up(in, 256) columns, zero-padded (the exact value rounded once; F16
+ * used as it is where in % 256 == 0), into a library buffer of
+ * out * round_up(in, 256) * 2 bytes (none for Q5_K / Q6_K up to 64 tokens,
+ * which are read in place), then multiplied with the same activation handling
+ * (zeros past in) and fp32 accumulation.  Work is enqueued on `stream` and the call
  * returns without synchronising.  For one to four tokens (FH3_HIP_PATH_GEMV8
  * below) activations are quantised to int16 inside the product kernel and
  * weights enter an integer MFMA exactly; otherwise activations are converted to
@@ -77,8 +82,9 @@ int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok,
  * matrix to several weight matrices (the DiT's qkv and gate_compress read the
  * same normalised rows) or that time the product kernel alone.
  *   fh3_hip_prepared_bytes: device bytes a prepared buffer for n_tok x in
- *     needs (fragments of round_up(n_tok, 256) rows, fp16, plus one fp32 scale
- *     per row, plus for n_tok <= 64 one fp32 sum per 32-value group);
+ *     needs (fragments of round_up(n_tok, 256) rows by round_up(in, 256)
+ *     columns, fp16, plus one fp32 scale per row, plus for n_tok <= 64 and
+ *     rows of whole super-blocks one fp32 sum per 32-value group);
  *   fh3_hip_prepare_x_dev: fill d_prep (16-byte aligned) from d_x[n_tok][in];
  *   fh3_hip_matmul_prepared_dev: the product from a prepared buffer; same
  *     results as fh3_hip_matmul_dev.  Its only library workspace is the
@@ -87,7 +93,9 @@ int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok,
  *     about 512 (roughly 65..2048 tokens; fh3_hip_matmul_workspace_bytes
  *     gives the exact size).  Weights of a type other than Q4_K also use the
  *     fp16-row buffer.  (For the FH3_HIP_PATH_GEMV8 shapes the prepared form
- *     is a copy of x.) */
+ *     is a copy of x; it is valid only while fh3_hip_set_path keeps the
+ *     setting it was prepared under.  The fragment form, with its group sums,
+ *     is valid under any setting.) */
 size_t fh3_hip_prepared_bytes(int n_tok, int64_t in);
 int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, void *d_prep, void *stream);
 int fh3_hip_matmul_prepared_dev(const Fh3W *w, const void *d_prep, float *d_y, int n_tok,
@@ -198,8 +206,12 @@ const void *fh3_hip_registered_ptr(const void *host, size_t bytes);
  * that a later eager call grows gets a new buffer; the old one stays
  * allocated while any graph made by fh3_hip_graph_end exists (graphs keep
  * their buffer addresses), and is freed when fh3_hip_graph_destroy destroys
- * the last of them.  Graphs therefore stay valid across workspace growth;
- * replays of graphs that share a workspace buffer must not overlap. */
+ * the last of them.  A capture begun by the caller's own
+ * hipStreamBeginCapture is seen when a call under it reaches its workspace;
+ * from then on replaced buffers stay allocated until fh3_hip_shutdown, since
+ * the library cannot see when such a graph is destroyed.  Graphs therefore
+ * stay valid across workspace growth; replays of graphs that share a
+ * workspace buffer must not overlap. */
 int fh3_hip_graph_begin(void *stream);
 int fh3_hip_graph_end(void *stream, void **graph_exec);
 int fh3_hip_graph_launch(void *graph_exec, void *stream);

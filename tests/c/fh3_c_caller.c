@@ -16,6 +16,14 @@
  *       the same weights, so y[t][o] - bias[o] must be one value per token:
  *       checked, and that value against a double-precision sum over the
  *       dequantised block (rel-L2 <= 2e-3).
+ *   fh3_c_caller patch [text] [audio] [video]
+ *       The run-once patch embedding of the reference's DiT forward
+ *       (src/model/fh3_dit.c:350-353): text rows copied into h, then
+ *       fh3_matmul of 32-value audio rows and 96-value video rows (F16
+ *       weights 5376 x 32 and 5376 x 96, F32 biases, as the GGUF holds them)
+ *       written straight into h behind them.  Checks: the text rows are
+ *       untouched, every other row of h is written, and each region against
+ *       a double-precision product (rel-L2 <= 2e-3).
  *   fh3_c_caller trunk <pack.bin>
  *       fh3_trunk_open on an Fh3Trunk held by value on the stack, as the
  *       reference CLI holds it (src/cli/fh3_cli.c:750,963): the host scan,
@@ -174,6 +182,93 @@ static int run_bench(int n_tok, int iters) {
     return 0;
 }
 
+/* IEEE half -> double (finite values only: the weights below are finite). */
+static double half_to_double(uint16_t h) {
+    const int e = (h >> 10) & 31, m = h & 1023;
+    const double v = e ? ldexp(1.0 + m / 1024.0, e - 15) : ldexp(m / 1024.0, -14);
+    return (h & 0x8000) ? -v : v;
+}
+
+/* double -> IEEE half, round to nearest, for |v| well inside the normal range. */
+static uint16_t double_to_half(double v) {
+    const uint16_t s = v < 0 ? 0x8000 : 0;
+    v = fabs(v);
+    if (v < ldexp(1.0, -14)) return s | (uint16_t)lrint(v * ldexp(1.0, 24));
+    int e;
+    const double f = frexp(v, &e); /* v = f * 2^e, f in [0.5, 1) */
+    long mant = lrint((f * 2.0 - 1.0) * 1024.0);
+    if (mant == 1024) mant = 0, e++;
+    return s | (uint16_t)((e - 1 + 15) << 10) | (uint16_t)mant;
+}
+
+static uint32_t lcg_state = 12345u;
+static double lcg_normal(void) { /* sum of 12 uniforms - 6 */
+    double s = 0.0;
+    for (int i = 0; i < 12; i++) {
+        lcg_state = lcg_state * 1664525u + 1013904223u;
+        s += (double)(lcg_state >> 8) / 16777216.0;
+    }
+    return s - 6.0;
+}
+
+static int run_patch(int T, int A, int V) {
+    const int64_t hidden = 5376;
+    const size_t rows = (size_t)(T + A + V);
+    float *h = (float *)malloc(rows * (size_t)hidden * sizeof(float));
+    CHECK(h != NULL);
+    for (size_t i = 0; i < rows * (size_t)hidden; i++) h[i] = NAN;
+    for (size_t i = 0; i < (size_t)T * (size_t)hidden; i++) h[i] = (float)lcg_normal();
+    const int ins[2] = {32, 96}, toks[2] = {A, V}, r0s[2] = {T, T + A};
+    uint16_t *wb[2];
+    float *xs[2], *bs[2];
+    for (int p = 0; p < 2; p++) {
+        const int in = ins[p], n = toks[p];
+        wb[p] = (uint16_t *)malloc((size_t)hidden * (size_t)in * sizeof(uint16_t));
+        xs[p] = (float *)malloc((size_t)n * (size_t)in * sizeof(float));
+        bs[p] = (float *)malloc((size_t)hidden * sizeof(float));
+        CHECK(wb[p] && xs[p] && bs[p]);
+        for (size_t i = 0; i < (size_t)hidden * (size_t)in; i++) wb[p][i] = double_to_half(0.05 * lcg_normal());
+        for (size_t i = 0; i < (size_t)n * (size_t)in; i++) xs[p][i] = (float)lcg_normal();
+        for (int64_t i = 0; i < hidden; i++) bs[p][i] = (float)(0.1 * lcg_normal());
+    }
+    float *text = (float *)malloc((size_t)T * (size_t)hidden * sizeof(float));
+    CHECK(text != NULL);
+    memcpy(text, h, (size_t)T * (size_t)hidden * sizeof(float));
+    /* src/model/fh3_dit.c:352-353 */
+    for (int p = 0; p < 2; p++) {
+        Fh3W w;
+        w.type = FH3_QUANT_F16;
+        w.in = ins[p];
+        w.out = hidden;
+        w.data = (const uint8_t *)wb[p];
+        fh3_matmul(&w, xs[p], h + (size_t)r0s[p] * (size_t)hidden, toks[p], bs[p]);
+    }
+    CHECK(memcmp(text, h, (size_t)T * (size_t)hidden * sizeof(float)) == 0);
+    for (int p = 0; p < 2; p++) {
+        const int in = ins[p], n = toks[p];
+        const size_t cnt = (size_t)n * (size_t)hidden;
+        double *ref = (double *)malloc(cnt * sizeof(double));
+        CHECK(ref != NULL);
+        for (int t = 0; t < n; t++)
+            for (int64_t o = 0; o < hidden; o++) {
+                double s = 0.0;
+                for (int k = 0; k < in; k++)
+                    s += (double)xs[p][(size_t)t * in + k] * half_to_double(wb[p][(size_t)o * in + k]);
+                ref[(size_t)t * hidden + o] = s + (double)bs[p][o];
+            }
+        const float *got = h + (size_t)r0s[p] * (size_t)hidden;
+        for (size_t i = 0; i < cnt; i++) CHECK(isfinite(got[i]));
+        const double err = rel_l2(got, ref, cnt);
+        CHECK(err <= 2e-3);
+        printf("PASS patch projection in=%d tokens=%d out=%lld: rel_l2 %.3e against the fp64 product\n", in, n,
+               (long long)hidden, err);
+        free(ref);
+    }
+    for (int p = 0; p < 2; p++) free(wb[p]), free(xs[p]), free(bs[p]);
+    free(h), free(text);
+    return 0;
+}
+
 static int run_trunk(const char *path) {
     Fh3Trunk tr; /* by value, as the reference CLI holds it */
     CHECK(fh3_trunk_open(path, 0, &tr) == FH3_OK);
@@ -214,7 +309,8 @@ static int run_trunk(const char *path) {
 
 int main(int argc, char **argv) {
     if (argc < 2) {
-        fprintf(stderr, "usage: %s matmul_ref <file> | bench [n_tok] [iters] | trunk <pack>\n", argv[0]);
+        fprintf(stderr, "usage: %s matmul_ref <file> | bench [n_tok] [iters] | patch [T] [A] [V] | trunk <pack>\n",
+                argv[0]);
         return 2;
     }
     CHECK(fh3_hip_init(0) == FH3_OK);
@@ -223,6 +319,9 @@ int main(int argc, char **argv) {
         rc = run_matmul_ref(argv[2]);
     else if (!strcmp(argv[1], "bench"))
         rc = run_bench(argc >= 3 ? atoi(argv[2]) : 1024, argc >= 4 ? atoi(argv[3]) : 3);
+    else if (!strcmp(argv[1], "patch"))
+        rc = run_patch(argc >= 3 ? atoi(argv[2]) : 6, argc >= 4 ? atoi(argv[3]) : 130,
+                       argc >= 5 ? atoi(argv[4]) : 2880);
     else if (!strcmp(argv[1], "trunk") && argc >= 3)
         rc = run_trunk(argv[2]);
     fh3_hip_shutdown();

@@ -1,8 +1,8 @@
 """A C99 program calls the library (tests/c/fh3_c_caller.c, built by
 fasth3inc_amd/build.py against include/fh3/*.h and linked to libfh3hip.so):
 the reference's test_matmul.c checks on its own fixture, the calls of its
-bench_matmul.c with an output check, and the trunk held by value on the
-stack as the reference CLI holds it."""
+bench_matmul.c with an output check, the DiT's run-once patch projections,
+and the trunk held by value on the stack as the reference CLI holds it."""
 import os
 import subprocess
 
@@ -33,6 +33,13 @@ def test_c_caller_matmul_ref():
 def test_c_caller_bench_matmul(n_tok):
     out = _run("bench", n_tok, "3")
     assert "PASS bench_matmul output" in out
+
+
+def test_c_caller_dit_patch_projections():
+    """src/model/fh3_dit.c:352-353 replayed by a C99 caller: 32- and 96-value
+    F16 rows with bias written into h behind the text rows."""
+    out = _run("patch", "6", "130", "2880")
+    assert out.count("PASS patch projection") == 2
 
 
 def test_c_caller_trunk_by_value():

@@ -243,6 +243,47 @@ def test_matmul_other_types_bitwise_vs_reference_build(oracle, ref, name):
         assert np.array_equal(yo.view(np.uint32), yr.view(np.uint32))
 
 
+def _general_rows(rng, name, N, K):
+    if name == "F32":
+        return (rng.standard_normal((N, K)) * 0.02).astype(np.float32).view(np.uint8).reshape(-1)
+    return H.random_blocks(rng, name, N, K, scale_lo=-12, scale_hi=-8)
+
+
+@pytest.mark.parametrize("name,K", [("F32", 7), ("F32", 33), ("F16", 32), ("F16", 96), ("BF16", 200),
+                                    ("F16", 1000), ("Q8_0", 32), ("Q8_0", 96), ("Q8_0", 224)])
+def test_matmul_short_rows_bitwise_vs_reference_build(oracle, ref, name, K):
+    """Rows that are not whole 256-value super-blocks (the DiT's 32- and
+    96-value patch projections, src/model/fh3_dit.c:352-353; any length for
+    the element types, whole 32-blocks for Q8_0): the 8-lane part and the
+    fmaf tail of src/core/fh3_ops.c:19-207, bitwise against the build."""
+    t = 0 if name == "F32" else H.QTYPES[name][0]
+    rng = np.random.default_rng(zlib.crc32(("%s%d" % (name, K)).encode()))
+    N, M = 37, 5
+    raw = _general_rows(rng, name, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    for b in (None, bias):
+        yo = H.matmul_with(oracle, "fh3_oracle_matmul", raw, K, N, x, b, qtype=t)
+        for fn in ("fh3_matmul", "fh3_matmul_scalar"):
+            yr = H.matmul_with(ref, fn, raw, K, N, x, b, qtype=t)
+            assert np.isfinite(yo).all()
+            assert np.array_equal(yo.view(np.uint32), yr.view(np.uint32)), fn
+
+
+@pytest.mark.parametrize("K", [1, 7, 13, 96])
+def test_matmul_short_rows_exact_integers(oracle, K):
+    """Small integers in fp32 weights and activations: every product and
+    partial sum is exact, so the oracle must return the integer product for
+    any row length, tail included (a dropped or doubled tail element fails)."""
+    rng = np.random.default_rng(K)
+    N, M = 11, 3
+    w = rng.integers(-8, 9, size=(N, K)).astype(np.float32)
+    x = rng.integers(-8, 9, size=(M, K)).astype(np.float32)
+    bias = rng.integers(-100, 101, size=N).astype(np.float32)
+    y = H.matmul_with(oracle, "fh3_oracle_matmul", w.view(np.uint8).reshape(-1), K, N, x, bias, qtype=0)
+    assert np.array_equal(y, (x.astype(np.int64) @ w.astype(np.int64).T + bias.astype(np.int64)).astype(np.float32))
+
+
 # --------------------------------------------------------------------------
 # The DiT block's elementwise ops (src/core/fh3_ops.c:410-585) vs the build
 # --------------------------------------------------------------------------

@@ -149,6 +149,61 @@ class Gemm:
             b.close()
 
 
+def _stream_legs(ev, st, path, n_blocks, products, legs, passes, block_wbytes, block_flop, fused_block=None):
+    """Time passes over n_blocks blocks of the pack at `path` through the
+    trunk: per block acquire_dev(L), prefetch_dev(L+1), then the block's
+    products (`products(view)` enqueues them) or `fused_block(view)`.
+    legs: (label, host_budget, dev_budget, compute, fused)."""
+    res = {}
+
+    def run_pass(tr, compute, fused):
+        for L in range(n_blocks):
+            d = tr.acquire_dev(L)
+            if d is None:
+                raise F.Fh3Error(F.FH3_E_IO, F.lib().fh3_hip_last_error().decode())
+            tr.prefetch_dev((L + 1) % n_blocks)
+            if compute:
+                (fused_block if fused else products)(tr.layer(L, d))
+
+    for label, host_budget, dev_budget, compute, fused in legs:
+        with F.Trunk(path, host_budget) as tr:
+            a0 = time.perf_counter()
+            tr.attach_device(dev_budget)
+            attach_s = time.perf_counter() - a0
+            # one untimed pass, then the timed passes right behind it with no
+            # synchronisation between: the pipeline (reads, uploads, products)
+            # is in its steady state when the GPU reaches the start event
+            run_pass(tr, compute, fused)
+            u0, h0 = tr.dev_stats().uploads, tr.stats()
+            w0 = time.perf_counter()
+            ms = ev.time_ms(lambda i: run_pass(tr, compute, fused), passes, st)
+            F.synchronize()
+            wall = (time.perf_counter() - w0) / passes
+            ups = tr.dev_stats().uploads - u0
+            h1 = tr.stats()
+        per_block = ms / n_blocks
+        # wall clock from the start of the timed passes, which also covers the
+        # tail of the untimed pass still on the GPU
+        entry = {"ms_per_block": round(per_block, 3), "wall_ms_per_block": round(wall * 1e3 / n_blocks, 3),
+                 "uploads_per_pass": ups // passes}
+        if host_budget == 0:
+            nb = passes * n_blocks
+            entry["host_reads_per_pass"] = (h1.misses - h0.misses) // passes
+            entry["read_ms_per_block"] = round((h1.read_s - h0.read_s) * 1e3 / nb, 3)
+            entry["wait_ms_per_block"] = round((h1.wait_s - h0.wait_s) * 1e3 / nb, 3)
+            entry["read_GBps"] = round(block_wbytes / max(1e-9, (h1.read_s - h0.read_s) / nb) / 1e9, 1)
+        if dev_budget:
+            entry["attach_s"] = round(attach_s, 3)
+            entry["attach_GBps"] = round(n_blocks * block_wbytes / attach_s / 1e9, 1)
+        if compute:
+            entry["TFLOPs"] = round(block_flop / (per_block * 1e-3) / 1e12, 1)
+        else:
+            entry["upload_GBps"] = round(block_wbytes / (per_block * 1e-3) / 1e9, 1)
+        res[label] = entry
+        log("[bench] DiT blocks %s: %.3f ms/block %s" % (label, per_block, entry))
+    return res
+
+
 def dit_blocks_streamed(ev, st, n_blocks=8, M=16384, passes=2):
     """Eight synthetic DiT blocks (QKV 15360x5120, out 5120x5120, fc1 = up|gate
     27648x5120, fc2 = down 5120x13824; 178.4 MB of Q4_K each) written to an
@@ -156,10 +211,12 @@ def dit_blocks_streamed(ev, st, n_blocks=8, M=16384, passes=2):
     through two device slots (hipMemcpyAsync on the upload stream), M = 16384
     tokens.  Per block: acquire_dev(L), prefetch_dev(L+1), the four
     fh3_hip_matmul_dev calls.  Timed beside the same blocks resident in HBM,
-    beside the uploads alone, and streamed as the block's fused sequence
+    beside the uploads alone, streamed as the block's fused sequence
     (norm1+modulate prep -> qkv; out-proj with the gate residual into h;
-    norm2+modulate prep -> fc1 with SwiGLU -> fc2 with the gate residual),
-    the attention output standing in for its input."""
+    norm2+modulate prep -> fc1 with SwiGLU -> fc2 with the gate residual, the
+    attention output standing in for its input), and read from the pack file
+    by the trunk's worker into the host ring (host budget 0: disk -> host ring
+    -> device slots), with and without the products."""
     import tempfile
     from fasth3inc_amd import pack as P
     hidden, qkv, mlp = 5120, 15360, 13824
@@ -193,55 +250,73 @@ def dit_blocks_streamed(ev, st, n_blocks=8, M=16384, passes=2):
             F.matmul_prepared_epi_dev(v.fc1.data, hidden, 2 * mlp, prep, M, F.EPI_SWIGLU, act)
             F.matmul_epi_dev(v.fc2.data, mlp, hidden, act, M, F.EPI_GATE_RESIDUAL, h, gate)
 
-        def run_pass(tr, compute=True, fused=False):
-            for L in range(n_blocks):
-                d = tr.acquire_dev(L)
-                if d is None:
-                    raise F.Fh3Error(F.FH3_E_IO, F.lib().fh3_hip_last_error().decode())
-                tr.prefetch_dev((L + 1) % n_blocks)
-                if not compute:
-                    continue
-                v = tr.layer(L, d)
-                if fused:
-                    fused_block(v)
-                    continue
-                for w, x, y in ((v.qkv, xa, ys[0]), (v.out, xa, ys[1]), (v.fc1, xa, ys[2]), (v.fc2, xm, ys[3])):
-                    F.matmul_dev(w.data, w.in_, w.out, x, y, M)
+        def products(v):
+            for w, x, y in ((v.qkv, xa, ys[0]), (v.out, xa, ys[1]), (v.fc1, xa, ys[2]), (v.fc2, xm, ys[3])):
+                F.matmul_dev(w.data, w.in_, w.out, x, y, M)
 
-        for label, dev_budget, compute, fused in (("streamed", 0, True, False), ("resident", 1 << 40, True, False),
-                                                  ("uploads_only", 0, False, False),
-                                                  ("streamed_fused_block", 0, True, True)):
-            with F.Trunk(path, 1 << 40) as tr:
-                a0 = time.perf_counter()
-                tr.attach_device(dev_budget)
-                attach_s = time.perf_counter() - a0
-                run_pass(tr, compute, fused)
-                F.synchronize()
-                u0 = tr.dev_stats().uploads
-                w0 = time.perf_counter()
-                ms = ev.time_ms(lambda i: run_pass(tr, compute, fused), passes, st)
-                F.synchronize()
-                wall = (time.perf_counter() - w0) / passes
-                ups = tr.dev_stats().uploads - u0
-            per_block = ms / n_blocks
-            entry = {"ms_per_block": round(per_block, 3), "wall_ms_per_block": round(wall * 1e3 / n_blocks, 3),
-                     "uploads_per_pass": ups // passes}
-            if dev_budget:
-                entry["attach_s"] = round(attach_s, 3)
-                entry["attach_GBps"] = round(n_blocks * block_wbytes / attach_s / 1e9, 1)
-            if compute:
-                entry["TFLOPs"] = round(block_flop / (per_block * 1e-3) / 1e12, 1)
-            else:
-                entry["upload_GBps"] = round(block_wbytes / (per_block * 1e-3) / 1e9, 1)
-            res[label] = entry
-            log("[bench] DiT blocks %s: %.3f ms/block %s" % (label, per_block, entry))
+        legs = (("streamed", 1 << 40, 0, True, False), ("resident", 1 << 40, 1 << 40, True, False),
+                ("uploads_only", 1 << 40, 0, False, False), ("streamed_fused_block", 1 << 40, 0, True, True),
+                ("disk_ring", 0, 0, True, False), ("disk_ring_uploads_only", 0, 0, False, False))
+        res.update(_stream_legs(ev, st, path, n_blocks, products, legs, passes, block_wbytes, block_flop,
+                                fused_block))
         res["unhidden_upload_ms_per_block"] = round(res["streamed"]["ms_per_block"] -
                                                     res["resident"]["ms_per_block"], 3)
         res["fused_ops_ms_per_block"] = round(res["streamed_fused_block"]["ms_per_block"] -
                                               res["streamed"]["ms_per_block"], 3)
+        # the disk ring's block time beyond the larger of its two inputs: the
+        # products alone (resident) and reading plus uploading alone
+        res["disk_ring_unhidden_ms_per_block"] = round(
+            res["disk_ring"]["ms_per_block"] - max(res["resident"]["ms_per_block"],
+                                                   res["disk_ring_uploads_only"]["ms_per_block"]), 3)
         for b in [xa, xm, h, prep, act] + ys + mods:
             b.close()
         return res
+    finally:
+        os.unlink(path)
+
+
+def real_dit_blocks_streamed(ev, st, n_blocks=4, Ms=(3016, 16384), passes=2):
+    """The real model's block (src/cli/fh3_cli.c:935-941: qkv 5376 -> 21504,
+    gate_compress 5376 -> 7168, out 7168 -> 5376, fc1 5376 -> 28672, fc2
+    14336 -> 5376; 238.4 MB of Q4_K per block, 238.5 MB with the norm weights,
+    docs/data/census.json:17),
+    streamed from page-locked host memory through the two device slots beside
+    the same blocks resident in HBM, at the CLI's default sequence (3016
+    tokens) and at 16384 tokens."""
+    import tempfile
+    from fasth3inc_amd import pack as P
+    specs = P.real_dit_block_specs()
+    q4 = [s for s in specs if s.qtype == F.FH3_QUANT_Q4_K]
+    block_wbytes = sum(s.nbytes for s in q4)
+    path = os.path.join(tempfile.gettempdir(), "fh3_bench_dit_real_%d.fh3p" % os.getpid())
+    t0 = time.perf_counter()
+    P.write_pack(path, n_blocks, specs, lambda L: P.synth_dit_block(specs, 6, L))
+    log("[bench] real DiT pack: %d blocks x %.1f MB written in %.1fs" % (n_blocks, block_wbytes / 1e6,
+                                                                          time.perf_counter() - t0))
+    out = {"blocks": n_blocks, "block_weight_bytes": block_wbytes,
+           "shapes": "qkv 5376->21504, gate_compress 5376->7168, out 7168->5376, fc1 5376->28672, "
+                     "fc2 14336->5376"}
+    try:
+        for M in Ms:
+            block_flop = sum(2.0 * M * s.ne1 * s.ne0 for s in q4)
+            xs = {K: F.DeviceBuffer.from_array(F.synth_x("normal", 6, K, M, K)) for K in sorted({s.ne0 for s in q4})}
+            ys = {s.suffix: F.DeviceBuffer(M * s.ne1 * 4) for s in q4}
+            names = ("qkv", "gate_compress", "out", "fc1", "fc2")
+
+            def products(v, M=M, xs=xs, ys=ys):
+                for name, s in zip(names, q4):
+                    w = getattr(v, name)
+                    F.matmul_dev(w.data, w.in_, w.out, xs[w.in_], ys[s.suffix], M)
+
+            legs = (("streamed", 1 << 40, 0, True, False), ("resident", 1 << 40, 1 << 40, True, False))
+            r = _stream_legs(ev, st, path, n_blocks, products, legs, passes, block_wbytes, block_flop)
+            r["block_flop"] = block_flop
+            r["unhidden_upload_ms_per_block"] = round(r["streamed"]["ms_per_block"] -
+                                                      r["resident"]["ms_per_block"], 3)
+            out["M%d" % M] = r
+            for b in list(xs.values()) + list(ys.values()):
+                b.close()
+        return out
     finally:
         os.unlink(path)
 
@@ -691,6 +766,11 @@ def main():
         except Exception as e:  # keep the headline line when this leg fails
             log("[bench] DiT streamed blocks failed: %r" % (e,))
             extra["dit_blocks_streamed"] = {"error": repr(e)}
+        try:
+            extra["real_dit_blocks_streamed"] = real_dit_blocks_streamed(ev, st)
+        except Exception as e:
+            log("[bench] real DiT streamed blocks failed: %r" % (e,))
+            extra["real_dit_blocks_streamed"] = {"error": repr(e)}
 
     out = {
         "metric": METRIC,

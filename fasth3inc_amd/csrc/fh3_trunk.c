@@ -66,6 +66,8 @@ typedef struct TrunkExt {
     void *ev_uploaded[2];         /* hipEvent_t */
     void *ev_slot_free[2];
     void *ev_host_read[2];
+    bool slot_free_pending[2];    /* ev_slot_free[s] recorded by the prefetch that recycled slot s */
+    int inject_fail;              /* test hook: 1 the next upload's copy fails, 2 its event record */
     Fh3TrunkDevStats dev_stats;
 } TrunkExt;
 
@@ -300,6 +302,7 @@ static void detach_device(TrunkExt *x) {
         x->dev_slot[s] = NULL;
         x->ev_uploaded[s] = x->ev_slot_free[s] = x->ev_host_read[s] = NULL;
         x->dev_layer[s] = -1;
+        x->slot_free_pending[s] = false;
     }
     fh3_hip_free(x->dev_resident);
     x->dev_resident = NULL;
@@ -515,14 +518,31 @@ int fh3_trunk_attach_device(Fh3Trunk *t, uint64_t dev_budget_bytes, void *comput
     return FH3_OK;
 }
 
-/* Enqueue "device slot s <- src" behind the compute work already enqueued
- * (which may still read slot s).  host_slot >= 0 names the host ring slot
- * src lies in, so the worker will not overwrite it before the copy ends. */
+/* Order slot s's next upload behind the compute work enqueued so far, the
+ * last that may read it: the call that recycles a slot marks this point. */
+static int mark_slot_free(TrunkExt *x, int s) {
+    if (x->inject_fail == 2) {
+        x->inject_fail = 0;
+        return fh3i_set_error(FH3_ERR, "hipEventRecord: injected failure (fh3_trunk_inject_upload_failure)");
+    }
+    return fh3i_event_record(x->ev_slot_free[s], x->compute_stream);
+}
+
+/* Enqueue "device slot s <- src" behind the work that last read slot s: the
+ * compute enqueued before the prefetch that recycled the slot when one did
+ * (a disk layer's prefetch_dev), else the compute enqueued so far.
+ * host_slot >= 0 names the host ring slot src lies in, so the worker will not
+ * overwrite it before the copy ends. */
 static int upload(const Fh3Trunk *t, TrunkExt *x, int s, int L, const uint8_t *src, int host_slot) {
     const size_t n = run_bytes(t, L);
     x->dev_layer[s] = -1;
-    int rc = fh3i_event_record(x->ev_slot_free[s], x->compute_stream);
+    int rc = x->slot_free_pending[s] ? FH3_OK : mark_slot_free(x, s);
+    x->slot_free_pending[s] = false;
     if (rc == FH3_OK) rc = fh3i_stream_wait(x->upload_stream, x->ev_slot_free[s]);
+    if (rc == FH3_OK && x->inject_fail == 1) {
+        x->inject_fail = 0;
+        rc = fh3i_set_error(FH3_ERR, "hipMemcpyAsync: injected failure (fh3_trunk_inject_upload_failure)");
+    }
     if (rc == FH3_OK) rc = fh3i_copy_async(x->dev_slot[s], src, n, x->upload_stream);
     if (rc == FH3_OK) rc = fh3i_event_record(x->ev_uploaded[s], x->upload_stream);
     if (rc == FH3_OK && host_slot >= 0) rc = fh3i_event_record(x->ev_host_read[host_slot], x->upload_stream);
@@ -540,10 +560,27 @@ void fh3_trunk_prefetch_dev(Fh3Trunk *t, int L) {
     if (x->dev_active >= 0 && x->dev_layer[x->dev_active] == L) return;
     const int idle = x->dev_active == 0 ? 1 : 0;
     if (x->dev_layer[idle] == L) return;
-    if (L < t->npin)
+    if (L < t->npin) {
         (void)upload(t, x, idle, L, t->pinned_layers[L], -1);
-    else
-        fh3_trunk_prefetch(t, L); /* read ahead; the acquire uploads it */
+        return;
+    }
+    /* A disk layer: read ahead; the acquire uploads it.  This call recycles
+     * the idle slot, so its upload needs only the compute enqueued so far
+     * (the block that last read it), not the block the caller enqueues next:
+     * the copy then overlaps that block. */
+    if (!x->slot_free_pending[idle] && mark_slot_free(x, idle) == FH3_OK) {
+        x->slot_free_pending[idle] = true;
+        x->dev_layer[idle] = -1;
+    }
+    fh3_trunk_prefetch(t, L);
+}
+
+int fh3_trunk_inject_upload_failure(Fh3Trunk *t, int what) {
+    TrunkExt *x = t ? ext_of(t) : NULL;
+    if (!x || !x->device || what < 0 || what > 2)
+        return fh3i_set_error(FH3_E_INVALID, "fh3_trunk_inject_upload_failure: trunk not attached or bad kind");
+    x->inject_fail = what;
+    return FH3_OK;
 }
 
 const uint8_t *fh3_trunk_acquire_dev(Fh3Trunk *t, int L) {

@@ -222,6 +222,7 @@ SIGNATURES = {
     "fh3_trunk_prefetch_dev": (None, [_c_void_p, _c_int]),
     "fh3_trunk_acquire_dev": (_c_void_p, [_c_void_p, _c_int]),
     "fh3_trunk_dev_stats": (Fh3TrunkDevStats, [_c_void_p]),
+    "fh3_trunk_inject_upload_failure": (_c_int, [_c_void_p, _c_int]),
     "fh3_trunk_struct_bytes": (_c_size, []),
     "fh3_trunk_info": (_c_int, [_c_void_p, ctypes.POINTER(Fh3TrunkInfo)]),
     "fh3_plan_bytes": (_c_u64, [ctypes.POINTER(Fh3Plan)]),
@@ -695,6 +696,11 @@ class Trunk:
 
     def acquire_dev(self, L):
         return lib().fh3_trunk_acquire_dev(self._t, L)
+
+    def inject_upload_failure(self, what):
+        """Test hook: the next slot upload fails at its copy (1) or at its
+        ordering event (2); 0 clears."""
+        _check(lib().fh3_trunk_inject_upload_failure(self._t, what), "fh3_trunk_inject_upload_failure")
 
     def close(self):
         if self._open:

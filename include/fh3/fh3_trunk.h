@@ -194,12 +194,21 @@ const Fh3Pack *fh3_trunk_pack(const Fh3Trunk *t);
 int fh3_trunk_attach_device(Fh3Trunk *t, uint64_t dev_budget_bytes, void *compute_stream);
 /* Start bringing layer L into the idle device slot: a host-resident layer is
  * uploaded at once (asynchronously); a disk layer is read ahead by the worker
- * and uploaded by the acquire. */
+ * and uploaded by the acquire.  Either way this call recycles the idle slot:
+ * the upload waits only for the compute enqueued before it, so with the loop
+ * acquire_dev(L), prefetch_dev(L+1), block L's work, layer L+1's copy runs
+ * while block L computes. */
 void fh3_trunk_prefetch_dev(Fh3Trunk *t, int L);
 /* Device pointer of layer L's run; work enqueued on the compute stream after
- * this call sees its bytes.  NULL on a short read or a HIP error. */
+ * this call sees its bytes.  NULL on a short read or a HIP error (the message
+ * in fh3_hip_last_error); a later acquire of the same layer tries again. */
 const uint8_t *fh3_trunk_acquire_dev(Fh3Trunk *t, int L);
 Fh3TrunkDevStats fh3_trunk_dev_stats(const Fh3Trunk *t);
+/* Test hook, no counterpart in the reference: make the next slot upload fail
+ * as a HIP error would, at its copy (what = 1) or at the event that orders it
+ * behind the compute (what = 2); 0 clears.  For tests of the error path of
+ * fh3_trunk_acquire_dev / fh3_trunk_prefetch_dev. */
+int fh3_trunk_inject_upload_failure(Fh3Trunk *t, int what);
 
 /* For bindings that cannot mirror the struct (it holds pthread objects):
  * its size, so they can allocate one, and the split chosen at open/attach.

@@ -235,3 +235,97 @@ def test_streamed_dit_blocks_m16384_fused_block(gpu, oracle, blocks, acts):
     assert err <= TOL
     for b in [h_got, h_want, prep, act] + q_got + q_want + list(d.values()) + [b for bl in wbufs for b in bl]:
         b.close()
+
+
+# ---------------------------------------------------------------------------
+# The real model's block (src/cli/fh3_cli.c:935-941): hidden 5376, inner 7168,
+# qkv 21504, gate_compress 7168 (Q4_K), fc1 28672, fc2 14336 -> 5376:
+# 238,480,384 bytes of Q4_K per block (docs/data/census.json:17), at the CLI's
+# default sequence of 3016 tokens (6 text, 130 audio, 2880 video).
+# ---------------------------------------------------------------------------
+RM = 3016
+
+
+@pytest.fixture(scope="module")
+def real_blocks(tmp_path_factory):
+    from fasth3inc_amd import pack as P
+    specs = P.real_dit_block_specs()
+    path = str(tmp_path_factory.mktemp("dit_real") / "dit_real.fh3p")
+    P.write_pack(path, N_BLOCKS, specs, lambda L: P.synth_dit_block(specs, 23, L))
+    return path, specs
+
+
+def test_streamed_real_dit_blocks_m3016(gpu, oracle, real_blocks):
+    """Three real-size blocks (the five Q4_K products, gate_compress
+    included) streamed from disk through the host ring and from page-locked
+    host memory through the two device slots: every output bit for bit
+    equal to the resident run, and sampled token rows against the oracle."""
+    F = gpu
+    from fasth3inc_amd import pack as P
+    path, specs = real_blocks
+    q4 = [s for s in specs if s.qtype == F.FH3_QUANT_Q4_K]
+    # the census's per-block bytes: 238,436,352 of Q4_K plus 44,032 of fp32 norm weights
+    assert sum(s.nbytes for s in specs) == 238480384 and sum(s.nbytes for s in q4) == 238436352
+    ins = sorted({s.ne0 for s in q4})
+    host_x = {K: F.synth_x("outliers" if K == 5376 else "silu_gated" if K == 14336 else "normal", 23, K, RM, K)
+              for K in ins}
+    dx = {K: F.DeviceBuffer.from_array(v) for K, v in host_x.items()}
+    names = ["qkv", "gate_compress", "out", "fc1", "fc2"]
+
+    def run(get_view):
+        outs = []
+        for L in range(N_BLOCKS):
+            v = get_view(L)
+            ys = []
+            for name in names:
+                w = getattr(v, name)
+                y = F.DeviceBuffer(RM * w.out * 4)
+                F.matmul_dev(w.data, w.in_, w.out, dx[w.in_], y, RM)
+                ys.append((y, w.out))
+            outs.append(ys)
+        F.synchronize()
+        return outs
+
+    print("case: real DiT blocks resident, %d blocks M=%d" % (N_BLOCKS, RM), flush=True)
+    bufs = [[F.DeviceBuffer.from_array(a) for a in P.synth_dit_block(specs, 23, L)] for L in range(N_BLOCKS)]
+    with F.Pack(path) as p:
+        pviews = [p.layer(L, None) for L in range(N_BLOCKS)]
+    views = []
+    for L in range(N_BLOCKS):
+        v = F.Fh3LayerView()
+        for t, n in enumerate(F.LAYER_TENSORS):
+            w = getattr(pviews[L], n)
+            setattr(v, n, F.Fh3W(w.type, w.in_, w.out, bufs[L][t].ptr))
+        views.append(v)
+    want = run(lambda L: views[L])
+    for host_budget, label in ((0, "disk -> host ring -> 2 device slots"),
+                               (1 << 40, "page-locked host blocks -> 2 device slots")):
+        print("case: real DiT blocks streamed (%s)" % label, flush=True)
+        with F.Trunk(path, host_budget) as tr:
+            tr.attach_device(0)
+            assert tr.info().dpin == 0 and tr.info().dev_slot_size >= 238480384
+            got = run(lambda L: _streamed(F, tr, L))
+            ds = tr.dev_stats()
+            assert ds.uploads == N_BLOCKS and ds.misses == N_BLOCKS
+        for L in range(N_BLOCKS):
+            for name, (g, N), (w, _) in zip(names, got[L], want[L]):
+                assert _equal_on_device(F, g.ptr, w.ptr, RM * N * 4), (label, L, name)
+        for ys in got:
+            for b, _ in ys:
+                b.close()
+    rng = np.random.default_rng(3016)
+    sub = np.unique(np.concatenate([[0, 5, 6, 135, 136, RM - 1], rng.choice(RM, 26, replace=False)]))
+    for L in range(N_BLOCKS):
+        raws = dict(zip(F.LAYER_TENSORS, P.synth_dit_block(specs, 23, L)))
+        for name, (y, N) in zip(names, want[L]):
+            w = getattr(views[L], name)
+            yo = H.oracle_matmul(oracle, raws[name], w.in_, N, host_x[w.in_][sub])
+            err = H.rel_fro(_rows(F, y, N, sub), yo)
+            print("  block %d %s (%d -> %d): rel_fro %.3e over %d rows" % (L, name, w.in_, N, err, len(sub)),
+                  flush=True)
+            assert err <= TOL, (L, name, err)
+    for ys in want:
+        for b, _ in ys:
+            b.close()
+    for b in list(dx.values()) + [b for bl in bufs for b in bl]:
+        b.close()

@@ -90,6 +90,36 @@ def test_dev_short_read_returns_null(gpu, tmp_path):
         assert np.all(read_back(fh3, d, MB) == 0xA0 + 8)
 
 
+@pytest.mark.parametrize("what", [1, 2])
+def test_dev_upload_failure_returns_null_then_recovers(gpu, tmp_path, what):
+    """A HIP error in a slot upload (its copy, or the event that orders it
+    behind the compute; injected from the host) makes fh3_trunk_acquire_dev
+    return NULL with the error text, as a failed read does in the reference
+    (src/io/fh3_trunk.c:453-456,487-490 -> FH3_ERR in src/model/fh3_dit.c:361-368);
+    the next acquire of the same layer uploads again and returns its bytes.
+    Layers from disk through the host ring and from page-locked host memory."""
+    fh3 = gpu
+    path = helpers.write_pattern_pack(str(tmp_path / "p.bin"), [MB] * 10)
+    with fh3.Trunk(path, 8 * MB) as tr:        # layers 0..5 in host memory, 6..9 from disk
+        tr.attach_device(2 * MB)               # every layer streams through the two slots
+        for L in (3, 7):
+            print("case: injected failure %d at layer %d" % (what, L), flush=True)
+            tr.inject_upload_failure(what)
+            assert tr.acquire_dev(L) is None
+            assert "injected failure" in fh3.lib().fh3_hip_last_error().decode()
+            d = acquired(fh3, tr, L)
+            assert np.all(read_back(fh3, d, MB) == 0xA0 + L)
+        # a failure inside prefetch_dev leaves nothing half done: the acquire uploads again
+        tr.inject_upload_failure(1)
+        tr.prefetch_dev(4)
+        d = acquired(fh3, tr, 4)
+        assert np.all(read_back(fh3, d, MB) == 0xA0 + 4)
+        for L in range(10):
+            d = acquired(fh3, tr, L)
+            tr.prefetch_dev((L + 1) % 10)
+            assert np.all(read_back(fh3, d, MB) == 0xA0 + L)
+
+
 # ---------------------------------------------------------------------------
 # streamed matmuls
 # ---------------------------------------------------------------------------

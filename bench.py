@@ -466,13 +466,15 @@ def _time_cpu(H, lib, fn, raw, K, N, x, iters):
     return min(ts), sum(ts) / len(ts)
 
 
-def cpu_baseline(cases, iters=5, big_iters=2, sample_rows=256):
+def cpu_baseline(cases, iters=5, big_iters=2, sample_tokens=(128, 512)):
     """fh3's CPU matmul on this host's cores, as benchmarks/bench_matmul.c
     times it (1 warmup, then best and mean of N runs): the six GEMV shapes and
     the 64 x 4096 x 4096 product with N = 5; the DiT GEMMs (M = 8192 and
-    32768) on the first `sample_rows` token rows of the same seeded
-    activations with N = 2, reported as GFLOP/s and the full-M time that rate
-    implies."""
+    32768) with N = 2 on a sample: one 64-row output tile per thread (the
+    reference schedules its tiles statically over the threads and dequantises
+    each tile once per call) at two token counts, the time per tile round
+    extended linearly to the full M (dequant fixed, products in M) and
+    multiplied by the full shape's rounds of tiles."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import helpers as H
     ref = H.load_ref()
@@ -480,6 +482,7 @@ def cpu_baseline(cases, iters=5, big_iters=2, sample_rows=256):
         lib, fn, kind = ref, "fh3_matmul", "reference"
     else:
         lib, fn, kind = H.load_oracle(), "fh3_oracle_matmul", "port"
+    threads = H.load_oracle().fh3_oracle_threads()
     total_w, total_t, per = 0, 0.0, []
     for c in cases:
         best, mean = _time_cpu(H, lib, fn, c.raw, c.K, c.N, c.x, iters)
@@ -496,21 +499,24 @@ def cpu_baseline(cases, iters=5, big_iters=2, sample_rows=256):
     configs["single_64x4096x4096"] = {"ms": round(best * 1e3, 3), "mean_ms": round(mean * 1e3, 3),
                                       "GFLOPs": round(flop / best / 1e9, 1),
                                       "weight_GBps": round(q4k_bytes(4096, 4096) / best / 1e9, 2)}
-    # DiT GEMMs on sampled token rows (same weights and activation seeds as the GPU leg)
+    # DiT GEMMs on a sample (same weights and activation seeds as the GPU leg)
     big = [("attn_qkv", 8192, 5120, 15360, "outliers", 0.0), ("attn_out", 8192, 5120, 5120, "outliers", 0.0),
            ("mlp_up_gate", 32768, 5120, 13824, "normal", 2.0), ("mlp_down", 32768, 13824, 5120, "silu_gated", 2.0)]
     rows = []
+    m1, m2 = sample_tokens
     for name, M, K, N, xk, spread in big:
-        raw = F.synth_q4k_weights(1, 300 + N + K, N, K, 0.02, spread)
-        x = F.synth_x(xk, 1, 400 + K, sample_rows, K)
-        best, mean = _time_cpu(H, lib, fn, raw, K, N, x, big_iters)
-        flop = 2.0 * sample_rows * N * K
-        rows.append({"name": name, "M": M, "K": K, "N": N, "sample_rows": sample_rows,
-                     "sample_ms": round(best * 1e3, 2), "sample_mean_ms": round(mean * 1e3, 2),
-                     "GFLOPs": round(flop / best / 1e9, 1), "full_M_ms": round(best * M / sample_rows * 1e3, 1)})
+        ns = min(N, 64 * threads)                     # one tile per thread
+        rounds = -(-(-(-N // 64)) // threads)          # rounds of tiles over the threads at full N
+        raw = F.synth_q4k_weights(1, 300 + N + K, N, K, 0.02, spread)[:ns * q4k_bytes(1, K)]
+        x = F.synth_x(xk, 1, 400 + K, m2, K)
+        t1, _ = _time_cpu(H, lib, fn, raw, K, ns, x[:m1], big_iters)
+        t2, mean2 = _time_cpu(H, lib, fn, raw, K, ns, x, big_iters)
+        full = (t1 + (t2 - t1) * (M - m1) / (m2 - m1)) * rounds
+        rows.append({"name": name, "M": M, "K": K, "N": N, "sample_rows": ns, "sample_tokens": [m1, m2],
+                     "sample_ms": [round(t1 * 1e3, 2), round(t2 * 1e3, 2)],
+                     "GFLOPs": round(2.0 * M * N * K / full / 1e9, 1), "full_M_ms": round(full * 1e3, 1)})
         del raw, x
     configs["dit_gemms_sampled"] = rows
-    threads = H.load_oracle().fh3_oracle_threads()
     cpu = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -524,8 +530,9 @@ def cpu_baseline(cases, iters=5, big_iters=2, sample_rows=256):
                       "of best times), one weight copy; fh3_matmul from the reference's own fh3_quant.c and "
                       "fh3_ops.c with OMP_NUM_THREADS=%d; nproc=%d; %s; built -O3 -mavx2 -mfma -mf16c "
                       "-ffp-contract=off -fopenmp (no -march=native). configs: the 64x4096x4096 product "
-                      "(best of %d) and the DiT GEMMs on %d sampled token rows (best of %d)"
-                      % (iters, threads, os.cpu_count(), cpu, iters, sample_rows, big_iters),
+                      "(best of %d) and the DiT GEMMs from one 64-row tile per thread at %d and %d tokens "
+                      "(best of %d), extended linearly in M and by the rounds of tiles at full N"
+                      % (iters, threads, os.cpu_count(), cpu, iters, m1, m2, big_iters),
             "per_case": per, "configs": configs}
 
 
@@ -783,9 +790,10 @@ def main():
         "ms_per_step_eager": round(ms_eager, 5),
         "ms_per_step_graph_per_step": round(ms_graph_step, 5),
         "higher_is_better": True,
-        "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16 x f16 -> f32 (Q4_K weights, fp32 activations)",
+        "dtype": "i8 x i8 -> i32 (1-4 tokens: Q4_K nibbles x int16 activations as two int8 planes) and "
+                 "f16 x f16 -> f32 (16 tokens: exact sc*q x fp16 activations); Q4_K weights, fp32 activations "
+                 "and outputs",
         "data": "synthetic: Philox-seeded N(0,0.02) weights Q4_K-encoded, N(0,1) activations",
         "config": {"workload": "small-M GEMV, text-encoder shapes: M in {1,4,16}, K=5120, N in {5120,17408}; "
                                "one step = one fh3_hip_matmul_dev per shape, weights rotated over >256 MB of "

@@ -13,7 +13,8 @@ Text encoder (src/model/fh3_te.c:455-487; hidden 5120, 64 query heads and
 8 key/value heads of 128, intermediate 25600 at src/model/fh3_te.h:12-22):
   q 5120 -> 8192, k and v 5120 -> 1024, o 8192 -> 5120, gate and up
   5120 -> 25600, down 25600 -> 5120,
-at prompt lengths 1, 2, 4, 16 and 64 tokens, every row against the oracle.
+at prompt lengths 1, 2, 4, 16 and 64 tokens, every row against the oracle, and
+65, 128, 300 and 600 tokens on sampled rows.
 K = 25600 with one or two tokens is past the integer-MFMA kernel's LDS and
 runs the small-M fp16 kernel.
 """
@@ -36,8 +37,10 @@ TE = [("q", 5120, 8192), ("k", 5120, 1024), ("v", 5120, 1024), ("o", 8192, 5120)
 
 
 def _sub(M, seed, n=64):
+    """n token rows of M (M >= n): the first and last, the two either side of
+    a 256-token tile edge when M has one, and seeded others."""
     rng = np.random.default_rng(seed)
-    edges = {0, 255, 256, M - 1}
+    edges = {t for t in (0, 255, 256, M - 1) if t < M}
     pick = set(int(t) for t in rng.choice(M, n - len(edges), replace=False)) | edges
     return np.array(sorted(pick))
 
@@ -120,5 +123,29 @@ def test_te_real_products(gpu, oracle, name, K, N):
         yo = H.oracle_matmul(oracle, raw, K, N, x)
         err = H.rel_fro(y, yo)
         worst = max(H.rel_fro(y[t], yo[t]) for t in range(M))
+        print("  rel_fro %.3e, worst row %.3e" % (err, worst), flush=True)
+        assert err <= TOL and worst <= TOL, (M, err, worst)
+
+
+@pytest.mark.parametrize("name,K,N", TE, ids=[t[0] for t in TE])
+def test_te_prompt_lengths(gpu, oracle, name, K, N):
+    """The text encoder's prompt lengths past 64 tokens (prompts run about
+    6-600 tokens through src/model/fh3_te.c:455-487): 65, 128, 300 and 600
+    tokens, including the 25600-long down rows, on 48 sampled token rows
+    against the oracle, the worst row within the gate too."""
+    F = gpu
+    raw = F.synth_q4k_weights(34, K + N, N, K, 0.02, 0.0)
+    dw = F.DeviceBuffer.from_array(raw)
+    for M in (65, 128, 300, 600):
+        print("case: TE %s M=%d K=%d N=%d path=%d" % (name, M, K, N, F.matmul_path(M, K)), flush=True)
+        x = F.synth_x("silu_gated" if name == "down" else "normal", 34, 100 * M + K, M, K)
+        dx, dy = F.DeviceBuffer.from_array(x), F.DeviceBuffer(M * N * 4)
+        F.matmul_dev(dw, K, N, dx, dy, M)
+        F.synchronize()
+        sub = _sub(M, M + K, n=48)
+        y = _rows(F, dy, N, sub)
+        yo = H.oracle_matmul(oracle, raw, K, N, x[sub])
+        err = H.rel_fro(y, yo)
+        worst = max(H.rel_fro(y[i], yo[i]) for i in range(len(sub)))
         print("  rel_fro %.3e, worst row %.3e" % (err, worst), flush=True)
         assert err <= TOL and worst <= TOL, (M, err, worst)

@@ -508,11 +508,12 @@ static int prepare(const float *d_x, int n_tok, int64_t in, void *d_prep, int64_
     return FH3_OK;
 }
 
-// prepared rows the kernels of `path` read
+// prepared rows the kernels of `path` read (the preparation zeroes the rows
+// from n_tok up to this count; rows past it are never read)
 static int64_t kernel_rows(int path, int n_tok) {
     return path == FH3_HIP_PATH_SKINNY || path == FH3_HIP_PATH_MIDM || path == FH3_HIP_PATH_SWEEP
                ? round_up(n_tok, 32)
-               : prep_rows(n_tok);
+               : fh3k_gemm_rows(n_tok);
 }
 
 extern "C" int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, void *d_prep, void *stream) {

@@ -96,6 +96,9 @@ hipError_t fh3k_gemm_epi(const void *W, int64_t row_bytes, int N, int K, const v
                          const float *bias, float *y, int M, int epi, const float *aux, float *part,
                          hipStream_t st);
 size_t fh3k_gemm_part_bytes(int N, int K, int M, int epi);
+// Prepared rows k_gemm reads for M tokens (its tiles cover 128 or 256
+// tokens; at most round_up(M, fh3k_gemm_row_pad())).
+int fh3k_gemm_rows(int M);
 
 // Middle M (1 <= M <= fh3k_midm_max_tokens()): K split into S windows, partial
 // sums in part (fh3k_midm_part_bytes(N, K, M) bytes), then an ordered sum with

@@ -1779,13 +1779,15 @@ __device__ __forceinline__ void gemm_dequant(half8 (*ldsb)[64], const GemmRaw &r
 // Activation fragments of K step s for k_gemm: xr covers the wavefront's two
 // token blocks, xoff is the lane's byte offset, tbs the byte stride of a token
 // block.
+template <int TBW>
 __device__ __forceinline__ void gemm_load_xs(__amdgpu_buffer_rsrc_t xr, uint32_t xoff, int tbs, int s,
-                                             half8 (&xf)[2][4]) {
+                                             half8 (&xf)[TBW][4]) {
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const int so = (s * 4 + k) * 1024;
-        xf[0][k] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)xoff, so, 0));
-        xf[1][k] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)xoff, so + tbs, 0));
+#pragma unroll
+        for (int a = 0; a < TBW; a++)
+            xf[a][k] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)xoff, so + a * tbs, 0));
     }
 }
 
@@ -1797,18 +1799,19 @@ __device__ __forceinline__ void gemm_load_x(const half8 *xa0, const half8 *xa1, 
     }
 }
 
-__device__ __forceinline__ void gemm_mfma(half8 (*ldsb)[64], int lane, const half8 (&xf)[2][4],
-                                          f32x16 (&acc)[2][4]) {
+template <int TBW>
+__device__ __forceinline__ void gemm_mfma(half8 (*ldsb)[64], int lane, const half8 (&xf)[TBW][4],
+                                          f32x16 (&acc)[TBW][4]) {
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         half8 bfr[4];
 #pragma unroll
         for (int ob = 0; ob < 4; ob++) bfr[ob] = ldsb[ob * 4 + k][lane];
 #pragma unroll
-        for (int ob = 0; ob < 4; ob++) {
-            acc[0][ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf[0][k], bfr[ob], acc[0][ob], 0, 0, 0);
-            acc[1][ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf[1][k], bfr[ob], acc[1][ob], 0, 0, 0);
-        }
+        for (int ob = 0; ob < 4; ob++)
+#pragma unroll
+            for (int a = 0; a < TBW; a++)
+                acc[a][ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf[a][k], bfr[ob], acc[a][ob], 0, 0, 0);
     }
 }
 
@@ -1821,21 +1824,32 @@ __device__ __forceinline__ void gemm_mfma(half8 (*ldsb)[64], int lane, const hal
 // per three MFMAs and the LDS writes after MFMA 20 (the best of a sweep of
 // these counts on the DiT shapes).  Without it the compiler clusters the
 // loads and the dequant into runs that stall the matrix pipe.
-template <int I>
+// With one token block per wavefront (TBW = 1: 16 MFMAs and 6 loads per step)
+// the same pattern is compressed: eight VALU per MFMA, the 12 remaining
+// B-fragment reads on three of every four MFMAs, a load every third MFMA and
+// the LDS writes after MFMA 10.
+template <int TBW, int I>
 __device__ __forceinline__ void gemm_pipe_slot() {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
-    if constexpr (I % 2 == 1 && I < 24) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-    if constexpr (I % 3 == 0 && I < 30) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
-    if constexpr (I >= 20 && I < 24) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);     // DS write
-    if constexpr (I + 1 < 32) gemm_pipe_slot<I + 1>();
+    constexpr int NM = 16 * TBW;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);               // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, 128 / NM, 0);        // VALU
+    if constexpr (TBW == 2 ? (I % 2 == 1 && I < 24) : (I % 4 != 0))  // DS read
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    if constexpr (I % 3 == 0 && I < 3 * (2 + 4 * TBW)) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+    if constexpr (I >= 10 * TBW && I < 10 * TBW + 4) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // DS write
+    if constexpr (I + 1 < NM) gemm_pipe_slot<TBW, I + 1>();
 }
 
+template <int TBW>
 __device__ __forceinline__ void gemm_pipe() {
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // B fragments of the first k-slice
-    gemm_pipe_slot<0>();
+    gemm_pipe_slot<TBW, 0>();
 }
 
+// TBW: 32-token blocks per wavefront; the workgroup's tile is 128 * TBW tokens
+// x 128 weight rows (TBW = 1 for at most 128 tokens: half the matrix work of
+// the 256-token tile per K step, whose lower half such products leave empty).
+template <int TBW>
 __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, int64_t row_bytes,
                                                  int N, int K, const half8 *__restrict__ X16,
                                                  const float *__restrict__ xs_inv,
@@ -1855,7 +1869,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
     const int L = (id < per * 8) ? (id & 7) * per + (id >> 3) : id;
     const int ks = L / tiles, tl = L - ks * tiles;
     const int mt = tl / n_tiles, nt = tl - mt * n_tiles;
-    const int m0 = mt * GEMM_BM, n0 = nt * GEMM_BN;
+    constexpr int BM = 128 * TBW;
+    const int m0 = mt * BM, n0 = nt * GEMM_BN;
 
     // weight-loader role: rows n0..n0+127, or (SwiGLU) 64 val rows from
     // nt*64 and the 64 gate rows F + nt*64..  Offsets from the first row fit
@@ -1874,24 +1889,25 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
     const int wf = (r >> 5) * 4;   // first LDS fragment of this row's 32-row block
     const int wl = r & 31;
 
-    // activation fragments of this wavefront: token blocks T0, T0+1
+    // activation fragments of this wavefront: token blocks T0 .. T0+TBW-1
     const int kf_n = K / 16;
     const int tbs = kf_n * 1024;
-    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(X16 + ((size_t)(m0 / 32 + 2 * wave) * kf_n) * 64, 2u * (uint32_t)tbs);
+    const __amdgpu_buffer_rsrc_t xr =
+        buf_rsrc(X16 + ((size_t)(m0 / 32 + TBW * wave) * kf_n) * 64, (uint32_t)TBW * (uint32_t)tbs);
     const uint32_t xoff = (uint32_t)lane * 16u;
 
     // super-blocks [sb0, sb1) of K: all of them, or this workgroup's window
     const int nsb = K / 256;
     const int sb0 = ks * C;
     const int sb1 = sb0 + C < nsb ? sb0 + C : nsb;
-    f32x16 acc[2][4];
+    f32x16 acc[TBW][4];
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < TBW; a++)
 #pragma unroll
         for (int b = 0; b < 4; b++) acc[a][b] = f32x16{};
 
-    GemmRaw re, ro;            // raw weights of even / odd steps
-    half8 xe[2][4], xo[2][4];  // activations of even / odd steps
+    GemmRaw re, ro;                // raw weights of even / odd steps
+    half8 xe[TBW][4], xo[TBW][4];  // activations of even / odd steps
     gemm_load_raw<0>(wr, woff, woffq, sb0, re, re);
     gemm_load_xs(xr, xoff, tbs, 4 * sb0, xe);
     gemm_load_raw<1>(wr, woff, woffq, sb0, ro, re);
@@ -1910,7 +1926,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
         gemm_dequant(lds[1], ro, 1, wf, wl, h);
         __builtin_amdgcn_s_setprio(2);
         gemm_mfma(lds[0], lane, xe, acc);
-        gemm_pipe();
+        gemm_pipe<TBW>();
         __builtin_amdgcn_s_setprio(0);
         __syncthreads();
         // step s+1 (chunk 1): MFMA from lds[1]; dequant chunk 2 into lds[0]
@@ -1919,7 +1935,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
         gemm_dequant(lds[0], re, 2, wf, wl, h);
         __builtin_amdgcn_s_setprio(2);
         gemm_mfma(lds[1], lane, xo, acc);
-        gemm_pipe();
+        gemm_pipe<TBW>();
         __builtin_amdgcn_s_setprio(0);
         __syncthreads();
         // step s+2 (chunk 2): MFMA from lds[0]; dequant chunk 3 into lds[1]
@@ -1928,7 +1944,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
         gemm_dequant(lds[1], ro, 3, wf, wl, h);
         __builtin_amdgcn_s_setprio(2);
         gemm_mfma(lds[0], lane, xe, acc);
-        gemm_pipe();
+        gemm_pipe<TBW>();
         __builtin_amdgcn_s_setprio(0);
         __syncthreads();
         // step s+3 (chunk 3): MFMA from lds[1]; dequant the next chunk 0 into lds[0]
@@ -1937,7 +1953,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
         gemm_dequant(lds[0], re, 0, wf, wl, h);
         __builtin_amdgcn_s_setprio(2);
         gemm_mfma(lds[1], lane, xo, acc);
-        gemm_pipe();
+        gemm_pipe<TBW>();
         __builtin_amdgcn_s_setprio(0);
         __syncthreads();
     }
@@ -1973,7 +1989,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
         }
         __builtin_amdgcn_wave_barrier();
     };
-    const bool rows_in = m0 + 64 * wave + 64 <= M;
+    const int wt0 = m0 + 32 * TBW * wave;  // this wavefront's first token
+    const bool rows_in = wt0 + 32 * TBW <= M;
     // 16-byte stores and gate reads need 16-byte aligned Y and aux (the
     // entry points accept any float pointer for them; part is the library's)
     const bool out16 = ((reinterpret_cast<uintptr_t>(Y) | reinterpret_cast<uintptr_t>(aux)) & 15) == 0;
@@ -1983,8 +2000,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
                          (epi == EPI_SWIGLU ? nt * 64 + 64 <= F : n0 + 128 <= N);
         if (vec) {
 #pragma unroll
-            for (int tb = 0; tb < 2; tb++) {
-                const int tb0 = m0 + 64 * wave + 32 * tb;
+            for (int tb = 0; tb < TBW; tb++) {
+                const int tb0 = wt0 + 32 * tb;
 #pragma unroll
                 for (int ob = 0; ob < 4; ob++) {
                     const int c0 = epi == EPI_SWIGLU ? (ob < 2 ? nt * 64 + 32 * ob : F + nt * 64 + 32 * (ob - 2))
@@ -1998,8 +2015,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
             return;
         }
 #pragma unroll
-        for (int tb = 0; tb < 2; tb++) {
-            const int tbase = m0 + 64 * wave + 32 * tb + 4 * (lane >> 5);
+        for (int tb = 0; tb < TBW; tb++) {
+            const int tbase = wt0 + 32 * tb + 4 * (lane >> 5);
 #pragma unroll
             for (int ob = 0; ob < 4; ob++) {
                 int o = n0 + 32 * ob + (lane & 31);
@@ -2020,8 +2037,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
         // matching gate rows
         if (rows_in && out16 && (F & 3) == 0 && nt * 64 + 64 <= F) {
 #pragma unroll
-            for (int tb = 0; tb < 2; tb++) {
-                const int tb0 = m0 + 64 * wave + 32 * tb;
+            for (int tb = 0; tb < TBW; tb++) {
+                const int tb0 = wt0 + 32 * tb;
 #pragma unroll
                 for (int ob = 0; ob < 2; ob++) {
                     const int o = nt * 64 + 32 * ob + (lane & 31);
@@ -2038,8 +2055,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
             return;
         }
 #pragma unroll
-        for (int tb = 0; tb < 2; tb++) {
-            const int tbase = m0 + 64 * wave + 32 * tb + 4 * (lane >> 5);
+        for (int tb = 0; tb < TBW; tb++) {
+            const int tbase = wt0 + 32 * tb + 4 * (lane >> 5);
 #pragma unroll
             for (int ob = 0; ob < 2; ob++) {
                 const int o = nt * 64 + 32 * ob + (lane & 31);
@@ -2057,8 +2074,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
     }
     if (rows_in && out16 && (N & 3) == 0 && n0 + 128 <= N) {
 #pragma unroll
-        for (int tb = 0; tb < 2; tb++) {
-            const int tb0 = m0 + 64 * wave + 32 * tb;
+        for (int tb = 0; tb < TBW; tb++) {
+            const int tb0 = wt0 + 32 * tb;
 #pragma unroll
             for (int ob = 0; ob < 4; ob++) {
                 const int o = n0 + 32 * ob + (lane & 31);
@@ -2075,8 +2092,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
         return;
     }
 #pragma unroll
-    for (int tb = 0; tb < 2; tb++) {
-        const int tbase = m0 + 64 * wave + 32 * tb + 4 * (lane >> 5);
+    for (int tb = 0; tb < TBW; tb++) {
+        const int tbase = wt0 + 32 * tb + 4 * (lane >> 5);
 #pragma unroll
         for (int ob = 0; ob < 4; ob++) {
             const int o = n0 + 32 * ob + (lane & 31);
@@ -2994,9 +3011,22 @@ extern "C" hipError_t fh3k_midm_epi(const void *W, int64_t row_bytes, int N, int
 // workgroup (~5 us): rounds of 512 resident workgroups x (C + 1), plus the
 // partial sums (written and read: S*M*N*8 bytes at ~5 TB/s) and the extra
 // launch.
+// 32-token blocks per k_gemm wavefront: one (128-token tiles) up to 128 tokens.
+// (Measured, K = 5120, calls incl. preparation and ordered sum: at N = 5120,
+// 65-128 tokens 26.6-28.3 us against 31.6-32.9 with 256-token tiles; at
+// N = 17408 46.7-52.3 against 62.8-67.8.  From 160 tokens the 256-token tile
+// is as fast or faster at N = 17408.)
+static int gemm_tbw(int M) { return M <= 128 ? 1 : 2; }
+
+extern "C" int fh3k_gemm_rows(int M) {
+    const int BM = 128 * gemm_tbw(M);
+    return (M + BM - 1) / BM * BM;
+}
+
 static void gemm_split(int M, int N, int K, int epi, int &C, int &S) {
     const int nsb = K / 256;
-    const int m_tiles = (M + GEMM_BM - 1) / GEMM_BM;
+    const int BM = 128 * gemm_tbw(M);
+    const int m_tiles = (M + BM - 1) / BM;
     const int n_tiles = epi == EPI_SWIGLU ? (N / 2) / 64 : (N + GEMM_BN - 1) / GEMM_BN;
     const int64_t tiles = (int64_t)m_tiles * n_tiles;
     const int smax = nsb >= 4 ? nsb / 2 : 1;
@@ -3027,11 +3057,17 @@ extern "C" hipError_t fh3k_gemm_epi(const void *W, int64_t row_bytes, int N, int
     int C, S;
     gemm_split(M, N, K, epi, C, S);
     if (S > 1 && !part) return hipErrorInvalidValue;
-    const int m_tiles = (M + GEMM_BM - 1) / GEMM_BM;
+    const int tbw = gemm_tbw(M), BM = 128 * tbw;
+    const int m_tiles = (M + BM - 1) / BM;
     const int n_tiles = epi == EPI_SWIGLU ? (N / 2) / 64 : (N + GEMM_BN - 1) / GEMM_BN;
-    hipLaunchKernelGGL(k_gemm, dim3((unsigned)(m_tiles * n_tiles * S)), dim3(256), 0, st,
-                       (const uint8_t *)W, row_bytes, N, K, (const half8 *)x16, xs_inv, bias, y, M,
-                       m_tiles, n_tiles, epi, aux, C, S > 1 ? part : nullptr);
+    if (tbw == 1)
+        hipLaunchKernelGGL(k_gemm<1>, dim3((unsigned)(m_tiles * n_tiles * S)), dim3(256), 0, st,
+                           (const uint8_t *)W, row_bytes, N, K, (const half8 *)x16, xs_inv, bias, y, M,
+                           m_tiles, n_tiles, epi, aux, C, S > 1 ? part : nullptr);
+    else
+        hipLaunchKernelGGL(k_gemm<2>, dim3((unsigned)(m_tiles * n_tiles * S)), dim3(256), 0, st,
+                           (const uint8_t *)W, row_bytes, N, K, (const half8 *)x16, xs_inv, bias, y, M,
+                           m_tiles, n_tiles, epi, aux, C, S > 1 ? part : nullptr);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || S == 1) return e;
     const int width = epi == EPI_SWIGLU ? N / 2 : N;

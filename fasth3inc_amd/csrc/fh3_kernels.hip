@@ -3011,21 +3011,27 @@ extern "C" hipError_t fh3k_midm_epi(const void *W, int64_t row_bytes, int N, int
 // workgroup (~5 us): rounds of 512 resident workgroups x (C + 1), plus the
 // partial sums (written and read: S*M*N*8 bytes at ~5 TB/s) and the extra
 // launch.
-// 32-token blocks per k_gemm wavefront: one (128-token tiles) up to 128 tokens.
-// (Measured, K = 5120, calls incl. preparation and ordered sum: at N = 5120,
-// 65-128 tokens 26.6-28.3 us against 31.6-32.9 with 256-token tiles; at
-// N = 17408 46.7-52.3 against 62.8-67.8.  From 160 tokens the 256-token tile
-// is as fast or faster at N = 17408.)
-static int gemm_tbw(int M) { return M <= 128 ? 1 : 2; }
+// 32-token blocks per k_gemm wavefront: one (128-token tiles) up to 128
+// tokens, and up to 256 while the 128-token tiles number at most 128; two
+// (256-token tiles) otherwise.  (Measured, K = 5120, calls incl. preparation
+// and ordered sum: at N = 5120, 65-128 tokens 26.2-28.4 us against 32.2-34.3
+// with 256-token tiles, 192 / 256 tokens 34.8 / 36.2 against 37.6 / 40.4; at
+// N = 17408, 65-128 tokens 46-54 against 63-68, while at 192 / 256 tokens the
+// 256-token tiles are faster, 76 / 82 against 88 / 92 us.)
+static int gemm_tbw(int M, int N, int epi) {
+    if (M <= 128) return 1;
+    const int n_tiles = epi == EPI_SWIGLU ? (N / 2) / 64 : (N + GEMM_BN - 1) / GEMM_BN;
+    return M <= 256 && 2 * n_tiles <= 128 ? 1 : 2;
+}
 
 extern "C" int fh3k_gemm_rows(int M) {
-    const int BM = 128 * gemm_tbw(M);
+    const int BM = M <= 128 ? 128 : 256;
     return (M + BM - 1) / BM * BM;
 }
 
 static void gemm_split(int M, int N, int K, int epi, int &C, int &S) {
     const int nsb = K / 256;
-    const int BM = 128 * gemm_tbw(M);
+    const int BM = 128 * gemm_tbw(M, N, epi);
     const int m_tiles = (M + BM - 1) / BM;
     const int n_tiles = epi == EPI_SWIGLU ? (N / 2) / 64 : (N + GEMM_BN - 1) / GEMM_BN;
     const int64_t tiles = (int64_t)m_tiles * n_tiles;
@@ -3057,7 +3063,7 @@ extern "C" hipError_t fh3k_gemm_epi(const void *W, int64_t row_bytes, int N, int
     int C, S;
     gemm_split(M, N, K, epi, C, S);
     if (S > 1 && !part) return hipErrorInvalidValue;
-    const int tbw = gemm_tbw(M), BM = 128 * tbw;
+    const int tbw = gemm_tbw(M, N, epi), BM = 128 * tbw;
     const int m_tiles = (M + BM - 1) / BM;
     const int n_tiles = epi == EPI_SWIGLU ? (N / 2) / 64 : (N + GEMM_BN - 1) / GEMM_BN;
     if (tbw == 1)

@@ -44,7 +44,7 @@ METRIC = "Q4_K GEMM TFLOP/s + GEMV weight GB/s (% roofline); DiT block linear ms
 # Summaries: profiles/gemv_k_gemv8_k_sweep_m1-16_k5120.md,
 # profiles/k_gemm_dit_attention_m8192_k5120.md, profiles/hbm_counters_copy_256MiB.md.
 # Re-measure when the kernels change.
-TRAFFIC_GEMV_MEAN = 33628228        # mean over the six GEMV shapes (algorithmic mean 32899072)
+TRAFFIC_GEMV_MEAN = 33644983        # mean over the six GEMV shapes (algorithmic mean 32899072)
 TRAFFIC_GEMM = {"attn_qkv": 2324594574, "attn_out": 703181960}
 
 
@@ -175,17 +175,12 @@ def _stream_legs(ev, st, path, n_blocks, products, legs, passes, block_wbytes, b
             # is in its steady state when the GPU reaches the start event
             run_pass(tr, compute, fused)
             u0, h0 = tr.dev_stats().uploads, tr.stats()
-            w0 = time.perf_counter()
             ms = ev.time_ms(lambda i: run_pass(tr, compute, fused), passes, st)
             F.synchronize()
-            wall = (time.perf_counter() - w0) / passes
             ups = tr.dev_stats().uploads - u0
             h1 = tr.stats()
         per_block = ms / n_blocks
-        # wall clock from the start of the timed passes, which also covers the
-        # tail of the untimed pass still on the GPU
-        entry = {"ms_per_block": round(per_block, 3), "wall_ms_per_block": round(wall * 1e3 / n_blocks, 3),
-                 "uploads_per_pass": ups // passes}
+        entry = {"ms_per_block": round(per_block, 3), "uploads_per_pass": ups // passes}
         if host_budget == 0:
             nb = passes * n_blocks
             entry["host_reads_per_pass"] = (h1.misses - h0.misses) // passes
@@ -658,6 +653,27 @@ def main():
                                                "note": "algorithmic bytes = Q4_K weights + fp32 x + fp32 y over "
                                                        "the kernel time (k_skinny, four token blocks)"}}
     g1.free()
+    # the same product with the weights rotated over copies past the MALL, as
+    # the GEMV shapes are timed (graph of 64 calls)
+    c1 = Gemv(64, 4096, 4096, seed=0)
+    c1.call(0)
+    c1.kernel(0)
+    F.synchronize()
+    gk = F.capture(lambda: [c1.kernel(i) for i in range(64)])
+    gc = F.capture(lambda: [c1.call(i) for i in range(64)])
+    gk.launch()
+    gc.launch()
+    t_k = ev.time_ms(lambda i: gk.launch(), 4, st) / 64
+    t_c = ev.time_ms(lambda i: gc.launch(), 4, st) / 64
+    gk.close()
+    gc.close()
+    extra["single_matmul_M64"]["rotated"] = {"copies": c1.copies, "kernel_us": round(t_k * 1e3, 2),
+                                             "call_us": round(t_c * 1e3, 2),
+                                             "hbm_frac": round(alg1 / (t_k * 1e-3) / HBM_PEAK, 4)}
+    for b in c1.w + [c1.dx, c1.dy, c1.prep]:
+        b.close()
+    log("[bench] 64x4096x4096: kernel %.2f us warm, %.2f us rotated" % (extra["single_matmul_M64"]["kernel_us"],
+                                                                      t_k * 1e3))
 
     # ---------------- 17..64-token products (k_sweep with 2-4 token blocks) -
     # text-encoder prompt lengths between the headline's 16 and the GEMM's 65
@@ -686,19 +702,32 @@ def main():
     log("[bench] 17..64 tokens: %s" % ", ".join("M=%d N=%d %.1f us" % (r["M"], r["N"], r["call_us"]) for r in prompt))
 
     # ---------------- few-hundred-token products (split-K GEMM path) -------
-    # text-encoder prompt lengths: 65..512 tokens at K = N = 5120, where the
-    # 256 x 128 GEMM tiles alone would leave most CUs idle
+    # text-encoder prompt lengths: 65..512 tokens at K = 5120, where the GEMM
+    # tiles alone would leave most CUs idle (128-token tiles up to 128 tokens,
+    # and up to 256 while they are few; K split, then the ordered sum); graph
+    # of 32 calls, weights rotated past the MALL, beside the 64-token call
     mid = []
-    for M in (65, 128, 256, 512):
-        gm = Gemm("mid_%d" % M, M, 5120, 5120, "normal", 0.0, seed=0)
-        for i in range(5):
-            gm.call(i)
-        t_k = ev.time_ms(gm.kernel, 50, st)
-        mid.append({"M": M, "K": 5120, "N": 5120, "path": F.matmul_path(M, 5120), "kernel_us": round(t_k * 1e3, 2),
-                    "kernel_TFLOPs": round(gm.flop / (t_k * 1e-3) / 1e12, 1)})
-        gm.free()
+    for N in (5120, 17408):
+        for M in (64, 65, 96, 128, 192, 256, 512):
+            c = Gemv(M, 5120, N, seed=0)
+            c.call(0)
+            c.kernel(0)
+            F.synchronize()
+            gk = F.capture(lambda c=c: [c.kernel(i) for i in range(32)])
+            gc = F.capture(lambda c=c: [c.call(i) for i in range(32)])
+            gk.launch()
+            gc.launch()
+            t_k = ev.time_ms(lambda i: gk.launch(), 4, st) / 32
+            t_c = ev.time_ms(lambda i: gc.launch(), 4, st) / 32
+            gk.close()
+            gc.close()
+            flop = 2.0 * M * N * 5120
+            mid.append({"M": M, "K": 5120, "N": N, "path": F.matmul_path(M, 5120), "kernel_us": round(t_k * 1e3, 2),
+                        "call_us": round(t_c * 1e3, 2), "call_TFLOPs": round(flop / (t_c * 1e-3) / 1e12, 1)})
+            for b in c.w + [c.dx, c.dy, c.prep]:
+                b.close()
     extra["gemm_few_hundred_tokens"] = mid
-    log("[bench] GEMM 65..512 tokens: %s" % ", ".join("M=%d %.1f us" % (r["M"], r["kernel_us"]) for r in mid))
+    log("[bench] 64..512 tokens: %s" % ", ".join("M=%d N=%d %.1f us" % (r["M"], r["N"], r["call_us"]) for r in mid))
 
     # ---------------- DiT GEMMs --------------------------------------------
     shapes = [("attn_qkv", 8192, 5120, 15360, "outliers", 0.0), ("attn_out", 8192, 5120, 5120, "outliers", 0.0)]

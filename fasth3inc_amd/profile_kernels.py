@@ -22,6 +22,9 @@ Workloads (each launch sequence is preceded by one untimed warmup launch):
   prompt 17 to 64 tokens at K = 5120 (M in {17, 32, 48, 64}, N in {5120,
          17408}): fh3_hip_matmul_prepared_dev -> k_sweep with two to four
          token blocks; weights rotated as for gemv
+  mid    65, 128 and 256 tokens at K = 5120 (N in {5120, 17408}):
+         fh3_hip_matmul_prepared_dev -> k_gemm with 128- or 256-token tiles
+         and a K split, then k_midm_sum; weights rotated as for gemv
   single the 64 x 4096 x 4096 product of the reference's bench_matmul.c, one
          weight copy (warm in the Infinity Cache after the first launch, as the
          benchmark runs it): fh3_hip_matmul_prepared_dev -> k_skinny
@@ -162,6 +165,10 @@ def prompt(reps):
     _rotated_products("prompt", [(M, 5120, N) for N in (5120, 17408) for M in (17, 32, 48, 64)], reps)
 
 
+def mid(reps):
+    _rotated_products("mid", [(M, 5120, N) for N in (5120, 17408) for M in (65, 128, 256)], reps)
+
+
 def gemm(reps):
     M, K = 8192, 5120
     dx = F.DeviceBuffer.from_array(F.synth_x("outliers", 1, 400 + K, M, K))
@@ -244,7 +251,7 @@ def vsa(reps, heads=56, hd=128, rot=96):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("workload", choices=("gemv", "te", "prompt", "single", "q56", "gemm", "mlp", "copy", "attn", "vsa",
+    ap.add_argument("workload", choices=("gemv", "te", "prompt", "mid", "single", "q56", "gemm", "mlp", "copy", "attn", "vsa",
                                          "all"))
     ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args(argv)

@@ -233,9 +233,14 @@ size_t fh3_hip_matmul_workspace_bytes(const Fh3W *w, int n_tok, int epi, int pre
  * process ends).  The call allocates and frees nothing; it returns
  * FH3_E_INVALID when the library is not initialised, for another weight
  * type, or when the shape needs more workspace than the array holds (the
- * message gives the size): every n_tok <= 64 at in <= 32768, and more tokens
- * while prepared activations (about 2 * round_up(n_tok, 256) * in bytes) plus
- * partial sums fit.  The array keeps the last call's contents; every call on
+ * message gives the size), or for rows of more than 32768 values.  The need
+ * is the prepared activations (about 2 * round_up(n_tok, 256) * in bytes,
+ * 16.3 MB at 64 tokens and in = 32768) plus the K-split partial sums
+ * (4 * S * n_tok * out bytes, S up to in / 2048 from 33 tokens); see
+ * fh3_hip_matmul_workspace_bytes.  Every n_tok <= 64 fits the real DiT and
+ * text-encoder shapes (out <= 28672 at in <= 14336, out = 5120 at
+ * in = 25600); at in = 32768 and 64 tokens, out up to 12208 fits.  The array
+ * keeps the last call's contents; every call on
  * a device shares it, so calls that overlap on one device (different streams,
  * threads, or graph replays) race and must be serialised by the caller. */
 #define FH3_HIP_NOALLOC_SCRATCH_BYTES (64u << 20)

@@ -62,6 +62,16 @@ def test_noalloc_refuses_what_does_not_fit(gpu):
     with pytest.raises(F.Fh3Error) as ei:
         F.matmul_noalloc_dev(dw, K, N, dx, dy, M)
     assert ei.value.code == F.FH3_E_INVALID and "scratch" in str(ei.value)
+    # up to 64 tokens, long rows: the K-split partial sums set the need
+    K2, N2, M2 = 32768, 12224, 64
+    assert F.matmul_workspace_bytes(K2, N2, M2) > F.NOALLOC_SCRATCH_BYTES
+    assert F.matmul_workspace_bytes(K2, 12208, M2) <= F.NOALLOC_SCRATCH_BYTES
+    dw2 = F.DeviceBuffer(N2 * (K2 // 256) * 144)
+    dx2 = F.DeviceBuffer(M2 * K2 * 4)
+    dy2 = F.DeviceBuffer(M2 * N2 * 4)
+    with pytest.raises(F.Fh3Error) as ei:
+        F.matmul_noalloc_dev(dw2, K2, N2, dx2, dy2, M2)
+    assert ei.value.code == F.FH3_E_INVALID and "scratch" in str(ei.value)
     with pytest.raises(F.Fh3Error) as ei:          # Q4_K only
         F.matmul_noalloc_dev(dw, 256, 16, dx, dy, 4, qtype=F.FH3_QUANT_Q6_K)
     assert ei.value.code == F.FH3_E_INVALID

@@ -1157,7 +1157,13 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
     // offsets below are relative to the slice's first super-block sbb
     const int nsb_all = K >> 8, kf_n = K >> 4;
     const int SL = (nsb_all + S - 1) / S;
-    const int ks = (int)blockIdx.x % S, gw = (int)blockIdx.x / S, GW = (int)gridDim.x / S;
+    // Token groups: M above 16 TB tokens (rows of at most 16 super-blocks)
+    // is split into TG groups of 16 TB tokens, each swept by its own
+    // workgroups, which then hold only their group's activations.
+    const int TG = (M + 16 * TB - 1) / (16 * TB);
+    const int ks = (int)blockIdx.x % S, rs = (int)blockIdx.x / S;
+    const int tg = rs % TG, gw = rs / TG, GW = (int)gridDim.x / (S * TG);
+    const int t0 = tg * 16 * TB;  // first token of this workgroup's group
     const int sbb = ks * SL;
     const int nsb = SL < nsb_all - sbb ? SL : nsb_all - sbb;
     const int own = wave * C;
@@ -1191,7 +1197,7 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
         const float *xs[TB];
 #pragma unroll
         for (int tb = 0; tb < TB; tb++) {
-            const int t = 16 * tb + j < M ? 16 * tb + j : M - 1;
+            const int t = t0 + 16 * tb + j < M ? t0 + 16 * tb + j : M - 1;
             xq[tb] = X16 + ((size_t)(t >> 5) * kf_n + (size_t)(sbb + s0) * 16 + 4 * q) * 64 + (t & 31);
             xs[tb] = xsum + (size_t)t * (K >> 5) + (size_t)(sbb + s0) * 8 + q;
         }
@@ -1219,7 +1225,7 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
     // threads of the workgroup take the TB x 256 outputs in turn (st_all).
     const bool st_all = blockDim.x < 256 || part || TB > 1;
     const int st_l = (int)threadIdx.x & 63, st_v = (int)threadIdx.x >> 6;
-    const int st_t = 4 * (st_l >> 4) + st_v, st_j = st_l & 15;
+    const int st_t = t0 + 4 * (st_l >> 4) + st_v, st_j = st_l & 15;
     const bool storer = !st_all && (int)threadIdx.x < 256 && st_t < M && (EPI != EPI_SWIGLU || st_j < 8);
     const size_t mn = (size_t)M * N;
     const float st_xs = storer ? xs_inv[st_t] : 0.f;
@@ -1295,7 +1301,7 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
         if (part) {  // K slices: this slice's raw sums of every row of the block
             for (int idx = (int)threadIdx.x; idx < TB * 256; idx += (int)blockDim.x) {
                 const int tb = idx >> 8, l = idx & 63, v = (idx >> 6) & 3, jj = l & 15;
-                const int t = 16 * tb + 4 * (l >> 4) + v;
+                const int t = t0 + 16 * tb + 4 * (l >> 4) + v;
                 const int col = EPI == EPI_SWIGLU ? o0 + (jj & 7) : o0 + jj;
                 if (t >= M || col >= (EPI == EPI_SWIGLU ? F : N)) continue;
                 const f32x4 *rt = rb + tb * 64;
@@ -1306,7 +1312,7 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
         } else if (st_all) {
             for (int idx = (int)threadIdx.x; idx < TB * 256; idx += (int)blockDim.x) {
                 const int tb = idx >> 8, l = idx & 63, v = (idx >> 6) & 3;
-                const int t = 16 * tb + 4 * (l >> 4) + v, o = o0 + (l & 15);
+                const int t = t0 + 16 * tb + 4 * (l >> 4) + v, o = o0 + (l & 15);
                 if (t >= M || o >= N || (EPI == EPI_SWIGLU && (l & 15) >= 8)) continue;
                 const float b = bias ? bias[o] : 0.f, bg = (bias && EPI == EPI_SWIGLU) ? bias[F + o] : 0.f;
                 const float ax = EPI == EPI_GATE_RES ? aux[(size_t)t * N + o] : 0.f;
@@ -2706,7 +2712,8 @@ extern "C" hipError_t fh3k_gemv8(const void *W, int64_t row_bytes, int N, int K,
 }
 
 // k_sweep: up to 16 tokens (one token block) with C = 2 super-blocks per
-// wavefront, 17..32 tokens (two token blocks) with C = 1; either way the
+// wavefront, 17..32 tokens (two token blocks) with C = 1 (on rows of at most
+// 16 super-blocks: see sweep_groups); either way the
 // activation fragments of a wavefront's window take 64 VGPRs and at most 10
 // wavefronts run at <= 168 VGPRs (about 160 used; C = 3 would spill), so a
 // K slice holds at most 10 C super-blocks.  Longer rows (to K = 32768) are
@@ -2716,7 +2723,18 @@ extern "C" hipError_t fh3k_gemv8(const void *W, int64_t row_bytes, int N, int K,
 // K = 25600 five of 20 beat four of 25 and seven of 15; K = 5120 stays whole).
 static int sweep_tb(int M) { return (M + 15) / 16; }
 
+// 17..64 tokens on rows of at most 16 super-blocks: groups of 32 tokens (two
+// token blocks) swept by their own workgroups, two super-blocks per
+// wavefront (128 VGPRs of activations, at most 8 wavefronts), no K split.
+// Each CU then reads the fp16 activations of one group only (64 x 4096:
+// 256 KB instead of 512 KB).
+static bool sweep_groups(int nsb, int M) { return M > 16 && nsb <= 16; }
+
 static void sweep_split(int nsb, int M, int &S, int &SL) {
+    if (sweep_groups(nsb, M)) {
+        S = 1, SL = nsb;
+        return;
+    }
     const int tb = sweep_tb(M);
     const int cap = tb == 1 ? 20 : (tb == 2 ? 10 : 8);
     S = (nsb + cap - 1) / cap;
@@ -2750,8 +2768,9 @@ static hipError_t launch_sweep_c(const void *W, int64_t rb, int N, int K, const 
     sweep_split(K / 256, M, S, SL);
     const int NW = (SL + C - 1) / C;
     const int nblk = (int)row_blocks16(N, EPI);
-    const int per = device_cus() / S;  // workgroups per slice
-    const int grid = (nblk < per ? nblk : per) * S;
+    const int TG = (M + 16 * TB - 1) / (16 * TB);  // token groups (k_sweep)
+    const int per = device_cus() / (S * TG);      // workgroups per slice and group
+    const int grid = (nblk < per ? nblk : per) * S * TG;
     const size_t lds = 2 * (size_t)NW * TB * 64 * sizeof(f32x4);
     if (NW * 64 > (LB < 640 ? LB : 640) || SL < C || nblk < 1 || grid < S || (S > 1 && !part))
         return hipErrorInvalidValue;
@@ -2770,6 +2789,8 @@ template <int EPI>
 static hipError_t launch_sweep_e(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,
                                  const float *xsum, const float *bias, float *y, int M, const float *aux, float *part,
                                  hipStream_t st) {
+    if (sweep_groups(K / 256, M))
+        return launch_sweep_c<2, 2, 512, EPI>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
     switch (sweep_tb(M)) {
         case 1: return launch_sweep_c<2, 1, 768, EPI>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
         case 2: return launch_sweep_c<1, 2, 768, EPI>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);

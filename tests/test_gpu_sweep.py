@@ -1,7 +1,9 @@
 """GPU parity of the persistent small-M kernel (FH3_HIP_PATH_SWEEP: up to 64
 tokens in one to four token blocks, 512 <= K <= 32768; fp16 activations held in registers, exact fp16
 sc*q weights, the offsets dmin*m from the prepared group sums; rows of more
-than 20 super-blocks in K slices whose partial sums are added in slice order)
+than 20 super-blocks in K slices whose partial sums are added in slice order;
+17-64 tokens on rows of at most 16 super-blocks in groups of 32 tokens, each
+group swept by its own workgroups)
 against the CPU oracle, through the C-ABI.
 
 Bars as for the other product kernels: rel-Frobenius <= 2e-3 against the
@@ -57,11 +59,11 @@ CASES = [
     (3, 13824, 130, "outliers", 0.0, False),      # three slices (18 each); past the int8 kernel's window
     (1, 25600, 64, "normal", 2.0, True),          # five slices of 20 (the text encoder's down-projection)
     (16, 25600, 520, "normal", 0.0, False),
-    (17, 1024, 48, "normal", 0.0, True),          # two token blocks, one super-block per wavefront
+    (17, 1024, 48, "normal", 0.0, True),          # one group of 32 tokens (two token blocks), the second with one token
     (24, 5120, 300, "outliers", 1.0, False),      # two token blocks, two K slices
     (32, 5120, 17408, "normal", 0.0, True),       # text-encoder MLP shape at 32 tokens (sampled rows)
     (29, 25600, 200, "silu_gated", 2.0, False),   # two token blocks in ten slices of ten super-blocks
-    (33, 2048, 96, "normal", 0.0, True),          # three token blocks, the third with one token
+    (33, 2048, 96, "normal", 0.0, True),          # two token groups, the second with one token
     (48, 5120, 640, "outliers", 1.0, True),       # three token blocks in three slices (7, 7, 6)
     (64, 8192, 200, "silu_gated", 0.0, False),    # four token blocks in four slices of eight
     (64, 5120, 17408, "normal", 0.0, False),      # text-encoder MLP shape at 64 tokens (sampled rows)

@@ -1231,12 +1231,15 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
     const float st_xs = storer ? xs_inv[st_t] : 0.f;
     // one output (token t, column o = o0 + jj) from the NW partial sums of
     // result lane l, register v (rb: this token block's [NW][TB][64] slice)
+    // (the partial sums are read as floats: register v of lane l is float
+    // 4 l + v, one 4-byte LDS read each instead of a 16-byte read and a select)
     auto store = [&](const f32x4 *rb, int l, int v, int t, int o, float xs, float b, float bg, float ax, float y0) {
-        float s = rb[l][v];
-        for (int w = 1; w < NW; w++) s += rb[w * TB * 64 + l][v];
+        const float *rf = reinterpret_cast<const float *>(rb) + v;
+        float s = rf[4 * l];
+        for (int w = 1; w < NW; w++) s += rf[4 * (w * TB * 64 + l)];
         if (EPI == EPI_SWIGLU) {  // the gate of column l % 16 is row l % 16 + 8 of the block
-            float sg = rb[l + 8][v];
-            for (int w = 1; w < NW; w++) sg += rb[w * TB * 64 + l + 8][v];
+            float sg = rf[4 * (l + 8)];
+            for (int w = 1; w < NW; w++) sg += rf[4 * (w * TB * 64 + l + 8)];
             Y[(size_t)t * F + o] = (s * xs + b) * silu_f32(sg * xs + bg);
         } else if (EPI == EPI_GATE_RES) {
             Y[(size_t)t * N + o] = __builtin_fmaf(ax, s * xs + b, y0);
@@ -1304,9 +1307,9 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
                 const int t = t0 + 16 * tb + 4 * (l >> 4) + v;
                 const int col = EPI == EPI_SWIGLU ? o0 + (jj & 7) : o0 + jj;
                 if (t >= M || col >= (EPI == EPI_SWIGLU ? F : N)) continue;
-                const f32x4 *rt = rb + tb * 64;
-                float sv = rt[l][v];
-                for (int w = 1; w < NW; w++) sv += rt[w * TB * 64 + l][v];
+                const float *rt = reinterpret_cast<const float *>(rb + tb * 64) + v;
+                float sv = rt[4 * l];
+                for (int w = 1; w < NW; w++) sv += rt[4 * (w * TB * 64 + l)];
                 part[(size_t)ks * mn + (size_t)t * N + (EPI == EPI_SWIGLU && jj >= 8 ? F + col : col)] = sv;
             }
         } else if (st_all) {

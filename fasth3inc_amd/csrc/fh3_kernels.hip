@@ -750,6 +750,52 @@ __device__ __forceinline__ void skinny_superblock(const u32x4 hv, const u32x4 ca
             acc[tb][v] = __builtin_fmaf(d, aq[tb][v], __builtin_fmaf(-dmin, am[tb][v], acc[tb][v]));
 }
 
+// skinny_superblock for one activation buffer (two or more token blocks):
+// as soon as MFMA step m has used its fragments a[m][*], they are reloaded
+// with super-block `next` of the window (next < 0: none), so the next
+// super-block's activations arrive while this one computes.  Same
+// arithmetic and order as skinny_superblock.
+template <int TB, int HI = 2>
+__device__ __forceinline__ void skinny_superblock_pf(const u32x4 hv, const u32x4 ca, const u32x4 cb, bool valid,
+                                                     const Q4kField flo, const Q4kField fhi, half8 (&a)[8][TB],
+                                                     f32x4 acc[TB], const half8 *const xq[TB], int next) {
+    const float d = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(hv.x & 0xFFFFu)) : 0.f;
+    const float dmin = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(hv.x >> 16)) : 0.f;
+    const uint32_t sclo = q4k_sc(hv, flo), schi = q4k_sc(hv, fhi);
+    const half2v sc_lo = splat2(sclo), sc_hi = splat2(schi);
+    const half2v nsc_lo = splat2(sclo) * (_Float16)-1024.0f, nsc_hi = splat2(schi) * (_Float16)-1024.0f;
+    const half2v m_lo = splat2(q4k_mn(hv, flo)), m_hi = splat2(q4k_mn(hv, fhi));
+    const half8 bm_lo = half8{m_lo[0], m_lo[1], m_lo[0], m_lo[1], m_lo[0], m_lo[1], m_lo[0], m_lo[1]};
+    const half8 bm_hi = half8{m_hi[0], m_hi[1], m_hi[0], m_hi[1], m_hi[0], m_hi[1], m_hi[0], m_hi[1]};
+    f32x4 aq[TB], am[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++) aq[tb] = am[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        const int part = m & 3;
+        const bool hi = m >= 4;
+        const u32x4 cv = part < 2 ? ca : cb;
+        const uint32_t u0 = (part & 1) ? cv.z : cv.x;
+        const uint32_t u1 = (part & 1) ? cv.w : cv.y;
+        const half8 b = q4k_scq8_f16(u0, u1, hi, hi ? sc_hi : sc_lo, hi ? nsc_hi : nsc_lo);
+#pragma unroll
+        for (int tb = 0; tb < TB; tb++) {
+            aq[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][tb], b, aq[tb], 0, 0, 0);
+            am[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][tb], hi ? bm_hi : bm_lo, am[tb], 0, 0, 0);
+        }
+        if (next >= 0) {
+            const int off = (next * 16 + (m >= 4 ? HI : 0) + ((m & 3) >> 1)) * 64 + (m & 1) * 32;
+#pragma unroll
+            for (int tb = 0; tb < TB; tb++) a[m][tb] = xq[tb][off];
+        }
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++)
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+            acc[tb][v] = __builtin_fmaf(d, aq[tb][v], __builtin_fmaf(-dmin, am[tb][v], acc[tb][v]));
+}
+
 // Raw bytes one lane holds for one super-block in k_skinny, per weight type,
 // and their loads.  wh points at the super-block, wa / wb at this lane's
 // pieces of it (set once per launch, so every load has a compile-time offset).
@@ -991,13 +1037,20 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) vo
     for (int i = 0; i < C; i++) {
         const int s = i % RING;
         const int ab = AB == 2 ? (i & 1) : 0;
+        // Q4_K with one buffer and short windows (longer ones spill): the
+        // fragments of super-block i were loaded during super-block i - 1
+        // (skinny_superblock_pf)
+        constexpr bool PF = AB == 1 && QT == FH3K_Q4_K && C <= 4;
         if (AB == 2 && i + 1 < C) {
             skinny_load_a<TB, AHI>(xq, i + 1, a[(i + 1) & 1]);
-        } else if (AB == 1 && i > 0) {
+        } else if (AB == 1 && i > 0 && !PF) {
             skinny_load_a<TB, AHI>(xq, i, a[0]);
         }
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (QT == FH3K_Q5_K)
+        if constexpr (PF)
+            skinny_superblock_pf<TB, AHI>(raw[s].hv, raw[s].ca, raw[s].cb, s0 + i >= own, flo, fhi, a[0], acc, xq,
+                                          i + 1 < C ? i + 1 : -1);
+        else if constexpr (QT == FH3K_Q5_K)
             sk5_superblock<TB>(raw[s], s0 + i >= own, q, flo, fhi, a[ab], acc);
         else if constexpr (QT == FH3K_Q6_K)
             sk6_superblock<TB>(raw[s], s0 + i >= own, q, a[ab], acc);
@@ -2518,16 +2571,20 @@ extern "C" hipError_t fh3k_scratch_bind(void **ptr) {
 
 // Super-blocks per wavefront C (compile-time, C <= nsb) and wavefronts per
 // workgroup NW (<= 8, runtime) for K/256 = nsb super-blocks: the fewest
-// padding super-blocks NW*C - nsb, then C closest to 5 (the best measured
-// balance of per-wave work and parallelism at K = 5120).
+// padding super-blocks NW*C - nsb, then, for one token block, C closest to 5
+// (the best measured balance of per-wave work and parallelism at K = 5120),
+// for more the smallest C (most wavefronts: each super-block's activation
+// fragments, 32 VGPRs per token block, are loaded and waited for in turn;
+// 64 x 4096 -> 4096: 14.8 us per call at C = 2, 15.7 at C = 4; 64 x 3072:
+// 12.3 against 13.5).
 static const int kSkinnyC[] = {1, 2, 3, 4, 5, 6, 7, 8, 10, 13, 16};
 
-static void skinny_split(int nsb, int &C, int &NW) {
+static void skinny_split(int nsb, int tb, int &C, int &NW) {
     int best = -1, bw = 1 << 30, bd = 1 << 30;
     for (int i = 0; i < (int)(sizeof kSkinnyC / sizeof kSkinnyC[0]); i++) {
         const int c = kSkinnyC[i], nw = (nsb + c - 1) / c;
         if (nw > 8 || c > nsb) continue;
-        const int waste = nw * c - nsb, dist = c > 5 ? c - 5 : 5 - c;
+        const int waste = nw * c - nsb, dist = tb > 1 ? c : (c > 5 ? c - 5 : 5 - c);
         if (waste < bw || (waste == bw && dist < bd)) best = i, bw = waste, bd = dist;
     }
     C = best >= 0 ? kSkinnyC[best] : 0;
@@ -2555,7 +2612,7 @@ static hipError_t launch_skinny(const void *W, int64_t rb, int N, int K, const v
                                 const float *xs_inv, const float *bias, float *y, int M, int epi, const float *aux,
                                 hipStream_t st) {
     int C, NW;
-    skinny_split(K / 256, C, NW);
+    skinny_split(K / 256, TB, C, NW);
     switch (C) {
         case 1: return launch_skinny_c<QT, TB, 1>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
         case 2: return launch_skinny_c<QT, TB, 2>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
@@ -3174,7 +3231,7 @@ template <int TB>
 static hipError_t launch_skinny16(const void *W16, int N, int K, const void *x16, const float *xs_inv,
                                   const float *bias, float *y, int M, hipStream_t st) {
     int C, NW;
-    skinny_split(K / 256, C, NW);
+    skinny_split(K / 256, 1, C, NW);  // the one-token-block rule (not measured otherwise here)
     switch (C) {
         case 1: return launch_skinny16_c<TB, 1>(W16, N, K, x16, xs_inv, bias, y, M, NW, st);
         case 2: return launch_skinny16_c<TB, 2>(W16, N, K, x16, xs_inv, bias, y, M, NW, st);

@@ -164,11 +164,11 @@ int choose_path(int n_tok, int64_t in) {
     // (measured 10-20 % faster than k_skinny at M = 16, K = 5120, 1.2-1.5x at
     // K = 25600; at 17..64 tokens 0-25 % faster than k_skinny and k_midm at
     // K = 5120, 1.1-1.4x over k_midm at K = 25600; at K = 4096 more than 16
-    // tokens need a K split and the ordered sum, and k_skinny is 10-15 %
-    // faster; on rows of at most 2560 the sweep splits 17..64 tokens into
-    // groups of 32 instead, each with its own workgroups and no K split:
-    // 10-40 % faster than k_skinny at K = 1024-2560, N = 1024-4096)
-    if (sw && (n_tok <= 16 || in >= 5120 || in <= 2560)) return FH3_HIP_PATH_SWEEP;
+    // tokens need a K split and the ordered sum, or (rows of at most 4096)
+    // groups of 32 tokens with their own workgroups, and k_skinny, eight
+    // wavefronts with the next super-block's activations loaded while one
+    // computes, is 0-25 % faster at K = 1024-4096, N = 1024-4096)
+    if (sw && (n_tok <= 16 || in >= 5120)) return FH3_HIP_PATH_SWEEP;
     // long rows (K >= 8192) with 17..64 tokens (when not taken above): the
     // split-K kernel reads the
     // activations once per 128 rows instead of once per 16 (measured 25-45 %

@@ -255,8 +255,8 @@ int fh3_hip_matmul_noalloc_dev(const Fh3W *w, const float *d_x, float *d_y, int 
  *     the kernel, integer MFMA on the raw 4-bit weights, no preparation launch
  *     and no workspace;
  *   - FH3_HIP_PATH_SWEEP for the other n_tok <= 16 when 512 <= in <= 32768,
- *     and n_tok <= 64 when 5120 <= in <= 32768 or 512 <= in <= 2560 (there
- *     in groups of 32 tokens, each swept by its own workgroups):
+ *     and n_tok <= 64 when 5120 <= in <= 32768 (forced on shorter rows: in
+ *     groups of 32 tokens, each swept by its own workgroups, up to 4096):
  *     fp16 activations with their group sums (prepared), exact fp16 sc*q
  *     weights, persistent workgroups that keep each wavefront's activations in
  *     registers while they sweep the weight rows; rows of more than 5120

@@ -110,8 +110,8 @@ def test_matmul_path_selection(fh3):
     kernel takes one to four tokens while its window fits (K <= 20480 for one
     or two tokens, K <= 12288 for three or four), the persistent fp16 sweep up
     to 16 tokens for 512 <= K <= 32768 and up to 64 from K = 5120 (long rows
-    in K slices) or up to K = 2560 (groups of 32 tokens), the fp16 GEMV up to
-    64 tokens on the rows between and below 512, the GEMM above; a forced path that cannot take a shape falls back to the
+    in K slices), the fp16 GEMV up to 64 tokens on shorter rows, the
+    GEMM above; a forced path that cannot take a shape falls back to the
     automatic choice."""
     F = fh3
     G8, SK, GM, SW = F.PATH_GEMV8, F.PATH_SKINNY, F.PATH_GEMM, F.PATH_SWEEP
@@ -125,7 +125,7 @@ def test_matmul_path_selection(fh3):
     assert F.matmul_path(5, 256) == SK and F.matmul_path(17, 5120) == SW and F.matmul_path(32, 25600) == SW
     assert F.matmul_path(33, 5120) == SW and F.matmul_path(64, 5120) == SW and F.matmul_path(64, 256) == SK
     assert F.matmul_path(17, 4864) == SK and F.matmul_path(64, 4096) == SK and F.matmul_path(16, 4096) == SW
-    assert F.matmul_path(17, 2560) == SW and F.matmul_path(64, 512) == SW and F.matmul_path(33, 2816) == SK
+    assert F.matmul_path(17, 2560) == SK and F.matmul_path(64, 512) == SK and F.matmul_path(33, 2816) == SK
     assert F.matmul_path(65, 5120) == GM
     MD = F.PATH_MIDM
     assert F.matmul_path(33, 8192) == SW and F.matmul_path(64, 13824) == SW and F.matmul_path(17, 8192) == SW

@@ -138,6 +138,13 @@ CASES = [
     (17, 1024, 96, "skinny", "normal", 0.0, False),
     (33, 1536, 130, "skinny", "outliers", 2.0, True),
     (64, 4096, 256, "skinny", "normal", 0.0, False),
+    # two to four token blocks: windows of 2-4 super-blocks whose activation
+    # fragments are loaded one super-block ahead (the last window moved back
+    # inside the row at K = 3328)
+    (24, 6144, 160, "skinny", "outliers", 1.0, True),
+    (40, 8192, 96, "skinny", "silu_gated", 0.0, False),
+    (50, 3328, 200, "skinny", "normal", 2.0, True),
+    (64, 5376, 80, "skinny", "normal", 0.0, True),
     (1, 512, 128, "gemm", "normal", 0.0, False),
     (65, 1024, 384, "gemm", "normal", 0.0, True),
     (300, 5120, 256, "gemm", "outliers", 0.0, False),
@@ -195,6 +202,24 @@ def test_matmul_deterministic_and_paths_agree(gpu, oracle):
     # the GEMM rounds dequantised weights to fp16 once
     assert H.rel_fro(a, yo) <= 3e-4
     assert H.rel_fro(c, yo) <= 6e-4
+
+
+@pytest.mark.parametrize("M,K", [(20, 3072), (40, 6144), (64, 8192), (33, 3328), (64, 2304)])
+def test_skinny_token_blocks_bitwise_repeatable_and_close_to_sweep(gpu, M, K):
+    """k_skinny with two to four token blocks (activations of the next
+    super-block loaded during the current one) is bitwise repeatable and
+    agrees with the sweep, which multiplies the same fp16 activations by the
+    same exact weights, to fp32 summation order: a fragment taken from the
+    wrong super-block or token would show as an O(1) difference."""
+    rng = np.random.default_rng(M * 7 + K)
+    N = 144
+    raw = H.random_q4k(rng, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    a = _dev_matmul(gpu, raw, K, N, x, path=gpu.PATH_SKINNY)
+    b = _dev_matmul(gpu, raw, K, N, x, path=gpu.PATH_SKINNY)
+    assert _bits_equal(a, b)
+    s = _dev_matmul(gpu, raw, K, N, x, path=gpu.PATH_SWEEP)
+    assert H.rel_fro(a, s) <= 1e-5
 
 
 def test_matmul_row_scaling_extreme_magnitudes(gpu, oracle):

@@ -64,6 +64,7 @@ CASES = [
     (32, 5120, 17408, "normal", 0.0, True),       # text-encoder MLP shape at 32 tokens (sampled rows)
     (29, 25600, 200, "silu_gated", 2.0, False),   # two token blocks in ten slices of ten super-blocks
     (33, 2048, 96, "normal", 0.0, True),          # two token groups, the second with one token
+    (64, 4096, 200, "outliers", 1.0, True),       # two full token groups, eight wavefronts of two super-blocks
     (48, 5120, 640, "outliers", 1.0, True),       # three token blocks in three slices (7, 7, 6)
     (64, 8192, 200, "silu_gated", 0.0, False),    # four token blocks in four slices of eight
     (64, 5120, 17408, "normal", 0.0, False),      # text-encoder MLP shape at 64 tokens (sampled rows)

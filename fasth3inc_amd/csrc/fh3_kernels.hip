@@ -712,53 +712,14 @@ __device__ __forceinline__ void skinny_load_a(const half8 *const xq[TB], int i, 
 // two MFMA chains over the same activation fragments (B = sc*q, and B = m
 // broadcast over each group), scaled by d and dmin in fp32 afterwards.
 // `valid` false (a padding super-block) contributes zero.
-template <int TB>
-__device__ __forceinline__ void skinny_superblock(const u32x4 hv, const u32x4 ca, const u32x4 cb, bool valid,
-                                                  const Q4kField flo, const Q4kField fhi,
-                                                  const half8 (&a)[8][TB], f32x4 acc[TB]) {
-    const float d = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(hv.x & 0xFFFFu)) : 0.f;
-    const float dmin = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(hv.x >> 16)) : 0.f;
-    const uint32_t sclo = q4k_sc(hv, flo), schi = q4k_sc(hv, fhi);
-    const half2v sc_lo = splat2(sclo), sc_hi = splat2(schi);
-    const half2v nsc_lo = splat2(sclo) * (_Float16)-1024.0f, nsc_hi = splat2(schi) * (_Float16)-1024.0f;
-    const half2v m_lo = splat2(q4k_mn(hv, flo)), m_hi = splat2(q4k_mn(hv, fhi));
-    const half8 bm_lo = half8{m_lo[0], m_lo[1], m_lo[0], m_lo[1], m_lo[0], m_lo[1], m_lo[0], m_lo[1]};
-    const half8 bm_hi = half8{m_hi[0], m_hi[1], m_hi[0], m_hi[1], m_hi[0], m_hi[1], m_hi[0], m_hi[1]};
-    f32x4 aq[TB], am[TB];
-#pragma unroll
-    for (int tb = 0; tb < TB; tb++) aq[tb] = am[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int m = 0; m < 8; m++) {
-        const int part = m & 3;
-        const bool hi = m >= 4;
-        const u32x4 cv = part < 2 ? ca : cb;
-        const uint32_t u0 = (part & 1) ? cv.z : cv.x;
-        const uint32_t u1 = (part & 1) ? cv.w : cv.y;
-        const half8 b = q4k_scq8_f16(u0, u1, hi, hi ? sc_hi : sc_lo, hi ? nsc_hi : nsc_lo);
-#pragma unroll
-        for (int tb = 0; tb < TB; tb++) {
-            aq[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][tb], b, aq[tb], 0, 0, 0);
-            am[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][tb], hi ? bm_hi : bm_lo, am[tb], 0, 0, 0);
-        }
-    }
-    // d and dmin belong to the weight row j = lane % 16, which is the output
-    // column this lane holds
-#pragma unroll
-    for (int tb = 0; tb < TB; tb++)
-#pragma unroll
-        for (int v = 0; v < 4; v++)
-            acc[tb][v] = __builtin_fmaf(d, aq[tb][v], __builtin_fmaf(-dmin, am[tb][v], acc[tb][v]));
-}
-
-// skinny_superblock for one activation buffer (two or more token blocks):
-// as soon as MFMA step m has used its fragments a[m][*], they are reloaded
-// with super-block `next` of the window (next < 0: none), so the next
-// super-block's activations arrive while this one computes.  Same
-// arithmetic and order as skinny_superblock.
+// With next >= 0 (one activation buffer: two or more token blocks), each MFMA
+// step's fragments a[m][*] are reloaded with super-block `next` of the window
+// (xq as in skinny_load_a) as soon as the step has used them, so the next
+// super-block's activations arrive while this one computes.
 template <int TB, int HI = 2>
-__device__ __forceinline__ void skinny_superblock_pf(const u32x4 hv, const u32x4 ca, const u32x4 cb, bool valid,
-                                                     const Q4kField flo, const Q4kField fhi, half8 (&a)[8][TB],
-                                                     f32x4 acc[TB], const half8 *const xq[TB], int next) {
+__device__ __forceinline__ void skinny_superblock(const u32x4 hv, const u32x4 ca, const u32x4 cb, bool valid,
+                                                  const Q4kField flo, const Q4kField fhi, half8 (&a)[8][TB],
+                                                  f32x4 acc[TB], const half8 *const *xq = nullptr, int next = -1) {
     const float d = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(hv.x & 0xFFFFu)) : 0.f;
     const float dmin = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(hv.x >> 16)) : 0.f;
     const uint32_t sclo = q4k_sc(hv, flo), schi = q4k_sc(hv, fhi);
@@ -789,6 +750,8 @@ __device__ __forceinline__ void skinny_superblock_pf(const u32x4 hv, const u32x4
             for (int tb = 0; tb < TB; tb++) a[m][tb] = xq[tb][off];
         }
     }
+    // d and dmin belong to the weight row j = lane % 16, which is the output
+    // column this lane holds
 #pragma unroll
     for (int tb = 0; tb < TB; tb++)
 #pragma unroll
@@ -1039,7 +1002,7 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) vo
         const int ab = AB == 2 ? (i & 1) : 0;
         // Q4_K with one buffer and short windows (longer ones spill): the
         // fragments of super-block i were loaded during super-block i - 1
-        // (skinny_superblock_pf)
+        // (skinny_superblock's next)
         constexpr bool PF = AB == 1 && QT == FH3K_Q4_K && C <= 4;
         if (AB == 2 && i + 1 < C) {
             skinny_load_a<TB, AHI>(xq, i + 1, a[(i + 1) & 1]);
@@ -1048,8 +1011,8 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) vo
         }
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (PF)
-            skinny_superblock_pf<TB, AHI>(raw[s].hv, raw[s].ca, raw[s].cb, s0 + i >= own, flo, fhi, a[0], acc, xq,
-                                          i + 1 < C ? i + 1 : -1);
+            skinny_superblock<TB, AHI>(raw[s].hv, raw[s].ca, raw[s].cb, s0 + i >= own, flo, fhi, a[0], acc, xq,
+                                       i + 1 < C ? i + 1 : -1);
         else if constexpr (QT == FH3K_Q5_K)
             sk5_superblock<TB>(raw[s], s0 + i >= own, q, flo, fhi, a[ab], acc);
         else if constexpr (QT == FH3K_Q6_K)

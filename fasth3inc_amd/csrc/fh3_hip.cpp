@@ -529,12 +529,14 @@ extern "C" int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, vo
 }
 
 // Weights of another type than Q4_K, and general rows of any type: Q5_K and
-// Q6_K rows of whole super-blocks up to 64 tokens are read in place by
-// k_skinny; otherwise fp16 rows of kpad(in) columns (the weight itself for
-// F16 rows of whole super-blocks, else decoded, zero-padded, into the
-// library's w16 buffer), then k_skinny16 / k_gemm16.
+// Q6_K rows of whole super-blocks are read in place, by k_skinny up to 64
+// tokens and by k_gemm above; otherwise fp16 rows of kpad(in) columns (the
+// weight itself for F16 rows of whole super-blocks, else decoded, zero-padded,
+// into the library's w16 buffer), then k_skinny16 / k_gemm16.
 static bool reads_in_place_q(const Fh3W *w, int n_tok) {
-    return !general_rows(w->in) && path16(n_tok, w->in) == FH3_HIP_PATH_SKINNY && fh3k_skinny_q_takes(w->type);
+    if (general_rows(w->in)) return false;
+    return path16(n_tok, w->in) == FH3_HIP_PATH_SKINNY ? fh3k_skinny_q_takes(w->type) != 0
+                                                        : fh3k_gemm_q_takes(w->type) != 0;
 }
 
 static size_t w16_bytes(const Fh3W *w, int n_tok) {
@@ -542,12 +544,29 @@ static size_t w16_bytes(const Fh3W *w, int n_tok) {
     return (size_t)w->out * (size_t)kpad(w->in) * 2;
 }
 
+// Partial sums of the in-place Q5_K / Q6_K GEMM (0 when it does not split K).
+static size_t part16_bytes(const Fh3W *w, int n_tok) {
+    if (!reads_in_place_q(w, n_tok) || path16(n_tok, w->in) != FH3_HIP_PATH_GEMM) return 0;
+    return fh3k_gemm_part_bytes((int)w->out, (int)w->in, n_tok, FH3_EPI_NONE);
+}
+
+// Called with g.mu held (it may grow the library's buffers).
 static int product16(const Fh3W *w, const void *x16, const float *xs_inv, int n_tok, const float *bias, float *d_y,
                      hipStream_t st) {
     const int K = (int)w->in, Kp = (int)kpad(w->in), N = (int)w->out;
     if (reads_in_place_q(w, n_tok)) {
-        FH3_HIPCALL(fh3k_skinny_q(w->type, w->data, (int64_t)fh3_row_bytes(w->type, w->in), N, K, x16, xs_inv, bias,
-                                  d_y, n_tok, st));
+        const int64_t rb = (int64_t)fh3_row_bytes(w->type, w->in);
+        if (path16(n_tok, w->in) == FH3_HIP_PATH_SKINNY) {
+            FH3_HIPCALL(fh3k_skinny_q(w->type, w->data, rb, N, K, x16, xs_inv, bias, d_y, n_tok, st));
+            return FH3_OK;
+        }
+        float *part = nullptr;
+        if (const size_t pb = part16_bytes(w, n_tok)) {
+            int rc = grow(g.part, pb, st);
+            if (rc != FH3_OK) return rc;
+            part = (float *)g.part.p;
+        }
+        FH3_HIPCALL(fh3k_gemm_q(w->type, w->data, rb, N, K, x16, xs_inv, bias, d_y, n_tok, part, st));
         return FH3_OK;
     }
     const void *w16 = w->data;
@@ -721,7 +740,7 @@ extern "C" size_t fh3_hip_matmul_workspace_bytes(const Fh3W *w, int n_tok, int e
     const size_t prep = fh3_hip_prepared_bytes(n_tok, w->in);
     if (w->type != FH3_QUANT_Q4_K || general_rows(w->in)) {
         const bool own_prep = !prepared || choose_path(n_tok, w->in) == FH3_HIP_PATH_GEMV8;
-        return w16_bytes(w, n_tok) + (own_prep ? prep : 0);
+        return w16_bytes(w, n_tok) + part16_bytes(w, n_tok) + (own_prep ? prep : 0);
     }
     const bool gemv8 = choose_path(n_tok, w->in) == FH3_HIP_PATH_GEMV8;
     return (prepared || gemv8 ? 0 : prep) + part_bytes(w, n_tok, epi);

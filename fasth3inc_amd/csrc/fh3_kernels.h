@@ -96,6 +96,12 @@ hipError_t fh3k_gemm_epi(const void *W, int64_t row_bytes, int N, int K, const v
                          const float *bias, float *y, int M, int epi, const float *aux, float *part,
                          hipStream_t st);
 size_t fh3k_gemm_part_bytes(int N, int K, int M, int epi);
+// Q5_K / Q6_K weights read in place by k_gemm (fh3k_gemm_q_takes), no
+// epilogue: same fragments, tiles, K split and partial-sum bytes
+// (fh3k_gemm_part_bytes with epi 0) as fh3k_gemm_epi.
+hipError_t fh3k_gemm_q(int type, const void *W, int64_t row_bytes, int N, int K, const void *x16,
+                       const float *xs_inv, const float *bias, float *y, int M, float *part, hipStream_t st);
+int fh3k_gemm_q_takes(int type);
 // Prepared rows k_gemm reads for M tokens (its tiles cover 128 or 256
 // tokens; at most round_up(M, fh3k_gemm_row_pad())).
 int fh3k_gemm_rows(int M);

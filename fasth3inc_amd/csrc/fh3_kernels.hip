@@ -40,6 +40,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 namespace {
 
@@ -1705,7 +1706,7 @@ __global__ __launch_bounds__(LB) void k_gemv8(const uint8_t *__restrict__ W, int
 // Large-M kernel.  Output tile 256 tokens x 128 weight rows, 4 wavefronts, each
 // owning 64 tokens x all 128 rows (2 x 4 tiles of 32x32, 128 fp32 accumulators
 // per lane).  Per K step s of 64 (one Q4_K chunk: groups 2c and 2c+1):
-//   - thread (r = tid%128, h = tid/128) holds 16 raw bytes of row r's chunk
+//   - thread (r = tid/2, h = tid%2) holds 16 raw bytes of row r's chunk
 //     and writes 32 dequantised fp16 weights into the LDS B-fragments;
 //   - each wavefront loads its X16 fragments straight from global memory
 //     (1 KiB contiguous per load);
@@ -1720,11 +1721,19 @@ __global__ __launch_bounds__(LB) void k_gemv8(const uint8_t *__restrict__ W, int
 constexpr int GEMM_BM = 256;
 constexpr int GEMM_BN = 128;
 
-// Raw Q4_K bytes one thread needs for K step s: the super-block header and 16
-// bytes of chunk s%4 (the header is reused within a super-block).
-struct GemmRaw {
-    u32x4 hv, qv;
-};
+// Raw bytes one thread needs for K step s (chunk c = s%4 of a super-block),
+// per weight type; what does not change within a super-block (or, for Q6_K,
+// within one of its halves) is loaded once and carried from step to step.
+//   Q4_K (144 B): the 16-byte header and 16 bytes of chunk c.
+//   Q5_K (176 B, src/core/fh3_quant.c:198-237): the same header, qh bytes
+//     16h..16h+15 (the high bits of this thread's element positions, one bit
+//     per group) and 16 bytes of chunk c of the low nibbles at 48.
+//   Q6_K (210 B, src/core/fh3_quant.c:239-282): 16 ql bytes of chunk c (see
+//     gemm_dequant), the 16 qh bytes of the chunk's half, that half's eight
+//     int8 scales and d.
+template <int QT> struct GemmRaw { u32x4 hv, qv; };
+template <> struct GemmRaw<FH3K_Q5_K> { u32x4 hv, hb, qv; };
+template <> struct GemmRaw<FH3K_Q6_K> { u32x4 hb, qv; u32x2 sc; uint32_t d; };
 
 // CH (the chunk, s % 4) is a compile-time constant, so the header load of
 // chunk 0 is not a branch and a K step is one basic block.
@@ -1736,12 +1745,37 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uin
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-template <int CH>
-__device__ __forceinline__ void gemm_load_raw(__amdgpu_buffer_rsrc_t wr, uint32_t woff, uint32_t woffq, int sb,
-                                              GemmRaw &r, const GemmRaw &prev) {
-    const int so = sb * 144;
-    r.hv = CH == 0 ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)woff, so, 0)) : prev.hv;
-    r.qv = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)woffq + 32 * CH, so, 0));
+// Q6_K super-blocks are only 2-byte aligned, so its pieces are read with
+// unaligned global loads (as k_skinny reads them) from wbase, the workgroup's
+// first weight row, plus the super-block offset (uniform) plus the thread's
+// 32-bit offset; every byte read lies inside the super-block.
+typedef uint32_t u32x2u __attribute__((ext_vector_type(2), aligned(2)));
+template <int QT, int CH>
+__device__ __forceinline__ void gemm_load_raw(__amdgpu_buffer_rsrc_t wr, const uint8_t *wbase, uint32_t woff,
+                                              uint32_t woffq, int sb, GemmRaw<QT> &r, const GemmRaw<QT> &prev) {
+    if constexpr (QT == FH3K_Q6_K) {
+        // woffq = woff + 16h: ql bytes 64(c/2) + 32(c%2) + 16h, qh bytes
+        // 128 + 32(c/2) + 16h, scales 192 + 8(c/2)
+        const uint8_t *b = wbase + (size_t)sb * 210;
+        r.qv = ld16u(b + woffq + (64 * (CH >> 1) + 32 * (CH & 1)));
+        if constexpr ((CH & 1) == 0) {
+            r.hb = ld16u(b + woffq + (128 + 32 * (CH >> 1)));
+            r.sc = *reinterpret_cast<const u32x2u *>(b + woff + (192 + 8 * (CH >> 1)));
+        } else {
+            r.hb = prev.hb;
+            r.sc = prev.sc;
+        }
+        r.d = CH == 0 ? ld_u16(b + woff + 208) : prev.d;
+    } else {
+        const int so = sb * (QT == FH3K_Q5_K ? 176 : 144);
+        r.hv = CH == 0 ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)woff, so, 0))
+                       : prev.hv;
+        r.qv = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)woffq + 32 * CH, so, 0));
+        if constexpr (QT == FH3K_Q5_K)  // qh bytes 16 + 16h = woffq - 32
+            r.hb = CH == 0 ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)woffq - 32, so,
+                                                                                              0))
+                           : prev.hb;
+    }
 }
 
 // B-fragment layout: fragment rb*4 + kk holds rows 32rb..32rb+31 x k 16kk..16kk+15
@@ -1762,6 +1796,17 @@ __device__ __forceinline__ void q4k_group_j(const u32x4 hdr, bool upper, int j, 
     const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x >> 16));
     D = d * (float)sc;
     C = -(dmin * (float)mn + 1024.0f * D);
+}
+
+// Eight fp16 fma(D, 1024 + v, C) from eight byte values v (a = bytes 0-3, b =
+// bytes 4-7), each rounded once.
+__device__ __forceinline__ half8 deq8_bytes(uint32_t a, uint32_t b, float D, float C) {
+    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u);
+    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u);
+    const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u);
+    const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u);
+    const u32x4 q = {fma_mix_pair(D, p0, C), fma_mix_pair(D, p1, C), fma_mix_pair(D, p2, C), fma_mix_pair(D, p3, C)};
+    return __builtin_bit_cast(half8, q);
 }
 
 // q4k_deq8_f16 with the nibble half as a shift (0 low, 4 high) that may
@@ -1788,28 +1833,81 @@ __device__ __forceinline__ float lane_swap1(float x) {
 // 2c + h only and takes the other group's (D, C) from its neighbour, then
 // writes its own nibble half first: low nibbles to fragment wf + h, high
 // nibbles to wf + 2 + h.
-__device__ __forceinline__ void gemm_dequant(half8 (*ldsb)[64], const GemmRaw &r, int s, int wf, int wl, int h) {
-    const int c = s & 3;
-    float Dm, Cm;
-    q4k_group_j(r.hv, c >= 2, ((2 * c) & 3) + h, Dm, Cm);
-    const float Do = lane_swap1(Dm), Co = lane_swap1(Cm);
-    const int own = wf + 3 * h, oth = wf + 2 - h;
-    const int sho = 4 * h, sht = 4 - 4 * h;
-    ldsb[own][wl] = q4k_deq8_sh(r.qv.x, r.qv.y, sho, Dm, Cm);
-    ldsb[own][wl + 32] = q4k_deq8_sh(r.qv.z, r.qv.w, sho, Dm, Cm);
-    ldsb[oth][wl] = q4k_deq8_sh(r.qv.x, r.qv.y, sht, Do, Co);
-    ldsb[oth][wl + 32] = q4k_deq8_sh(r.qv.z, r.qv.w, sht, Do, Co);
+// Q5_K: the same with bit g of each qh byte (h0, h1: the qh bytes of the same
+// element positions) as bit 4 of q, q <= 31.
+__device__ __forceinline__ half8 q5k_deq8_sh(uint32_t u0, uint32_t u1, uint32_t h0, uint32_t h1, int sh, int g,
+                                             float D, float C) {
+    return deq8_bytes(((u0 >> sh) & 0x0F0F0F0Fu) | (((h0 >> g) & 0x01010101u) << 4),
+                      ((u1 >> sh) & 0x0F0F0F0Fu) | (((h1 >> g) & 0x01010101u) << 4), D, C);
+}
+
+// Q6_K: q = nibble (shift SH) | bits HS..HS+1 of the qh byte << 4, weight
+// D * (q - 32) with D = d * sc.  fma(D, 1024 + q, -1056 D) is that value
+// exactly in fp32 (D = fp16 * int8 has at most 18 significant bits, 1056 D and
+// D * (q - 32) at most 24), so each weight is the reference's fp32 value
+// rounded once to fp16.
+template <int SH, int HS>
+__device__ __forceinline__ half8 q6k_deq8(uint32_t u0, uint32_t u1, uint32_t h0, uint32_t h1, float D) {
+    auto hi2 = [](uint32_t h) { return (HS >= 4 ? h >> (HS - 4) : h << (4 - HS)) & 0x30303030u; };
+    return deq8_bytes(((u0 >> SH) & 0x0F0F0F0Fu) | hi2(h0), ((u1 >> SH) & 0x0F0F0F0Fu) | hi2(h1), D, -1056.0f * D);
+}
+
+template <int QT, int CH>
+__device__ __forceinline__ void gemm_dequant(half8 (*ldsb)[64], const GemmRaw<QT> &r, int wf, int wl, int h) {
+    constexpr int c = CH;
+    if constexpr (QT == FH3K_Q6_K) {
+        // chunk c = (half c/2, quarter c%2) holds ql bytes 64(c/2) + 32(c%2) +
+        // b, b = 0..31: low nibble = element 128(c/2) + 32(c%2) + b (k step
+        // offset b), high nibble = element 128(c/2) + 64 + 32(c%2) + b (offset
+        // 32 + b); their 2 high bits are bits 2(c%2) and 4 + 2(c%2) of qh
+        // byte 32(c/2) + b and their scales sub-groups 8(c/2) + 2(c%2) + b/16
+        // and that + 4.  This thread has b = 16h..16h+15: low nibbles to
+        // fragment wf + h, high nibbles to wf + 2 + h.
+        const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.d & 0xFFFFu));
+        const int sb8 = 8 * (2 * (c & 1) + h);
+        const float Dl = d * (float)(int)(int8_t)(uint8_t)(r.sc.x >> sb8);
+        const float Dh = d * (float)(int)(int8_t)(uint8_t)(r.sc.y >> sb8);
+        constexpr int hs = 2 * (c & 1);
+        ldsb[wf + h][wl] = q6k_deq8<0, hs>(r.qv.x, r.qv.y, r.hb.x, r.hb.y, Dl);
+        ldsb[wf + h][wl + 32] = q6k_deq8<0, hs>(r.qv.z, r.qv.w, r.hb.z, r.hb.w, Dl);
+        ldsb[wf + 2 + h][wl] = q6k_deq8<4, hs + 4>(r.qv.x, r.qv.y, r.hb.x, r.hb.y, Dh);
+        ldsb[wf + 2 + h][wl + 32] = q6k_deq8<4, hs + 4>(r.qv.z, r.qv.w, r.hb.z, r.hb.w, Dh);
+    } else {
+        float Dm, Cm;
+        q4k_group_j(r.hv, c >= 2, ((2 * c) & 3) + h, Dm, Cm);
+        const float Do = lane_swap1(Dm), Co = lane_swap1(Cm);
+        const int own = wf + 3 * h, oth = wf + 2 - h;
+        const int sho = 4 * h, sht = 4 - 4 * h;
+        if constexpr (QT == FH3K_Q5_K) {
+            // the high bit of group 2c + h (own) / 2c + 1 - h (other)
+            const int go = 2 * c + h, gt = 2 * c + 1 - h;
+            ldsb[own][wl] = q5k_deq8_sh(r.qv.x, r.qv.y, r.hb.x, r.hb.y, sho, go, Dm, Cm);
+            ldsb[own][wl + 32] = q5k_deq8_sh(r.qv.z, r.qv.w, r.hb.z, r.hb.w, sho, go, Dm, Cm);
+            ldsb[oth][wl] = q5k_deq8_sh(r.qv.x, r.qv.y, r.hb.x, r.hb.y, sht, gt, Do, Co);
+            ldsb[oth][wl + 32] = q5k_deq8_sh(r.qv.z, r.qv.w, r.hb.z, r.hb.w, sht, gt, Do, Co);
+        } else {
+            ldsb[own][wl] = q4k_deq8_sh(r.qv.x, r.qv.y, sho, Dm, Cm);
+            ldsb[own][wl + 32] = q4k_deq8_sh(r.qv.z, r.qv.w, sho, Dm, Cm);
+            ldsb[oth][wl] = q4k_deq8_sh(r.qv.x, r.qv.y, sht, Do, Co);
+            ldsb[oth][wl + 32] = q4k_deq8_sh(r.qv.z, r.qv.w, sht, Do, Co);
+        }
+    }
 }
 
 // Activation fragments of K step s for k_gemm: xr covers the wavefront's two
 // token blocks, xoff is the lane's byte offset, tbs the byte stride of a token
 // block.
-template <int TBW>
+// The step's fragment k is X16 fragment 4s + k (Q4_K, Q5_K: the step is 64
+// consecutive k), or for Q6_K (see gemm_dequant) 16(s/4) + 8(c/2) + 2(c%2) +
+// k%2 + 4(k/2), c = s%4.
+template <int TBW, int QT = FH3K_Q4_K>
 __device__ __forceinline__ void gemm_load_xs(__amdgpu_buffer_rsrc_t xr, uint32_t xoff, int tbs, int s,
                                              half8 (&xf)[TBW][4]) {
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        const int so = (s * 4 + k) * 1024;
+        const int f = QT == FH3K_Q6_K ? 16 * (s >> 2) + 8 * ((s >> 1) & 1) + 2 * (s & 1) + (k & 1) + 4 * (k >> 1)
+                                      : s * 4 + k;
+        const int so = f * 1024;
 #pragma unroll
         for (int a = 0; a < TBW; a++)
             xf[a][k] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)xoff, so + a * tbs, 0));
@@ -1874,7 +1972,9 @@ __device__ __forceinline__ void gemm_pipe() {
 // TBW: 32-token blocks per wavefront; the workgroup's tile is 128 * TBW tokens
 // x 128 weight rows (TBW = 1 for at most 128 tokens: half the matrix work of
 // the 256-token tile per K step, whose lower half such products leave empty).
-template <int TBW>
+// QT: the weight type, Q4_K, or Q5_K / Q6_K read in place (GemmRaw,
+// gemm_dequant); the tile, pipeline and epilogue are the same.
+template <int TBW, int QT = FH3K_Q4_K>
 __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, int64_t row_bytes,
                                                  int N, int K, const half8 *__restrict__ X16,
                                                  const float *__restrict__ xs_inv,
@@ -1910,7 +2010,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
     const __amdgpu_buffer_rsrc_t wr =
         buf_rsrc(W + (size_t)rowbase * row_bytes, (uint32_t)((size_t)(N - rowbase) * row_bytes));
     const uint32_t woff = (uint32_t)(orow - rowbase) * (uint32_t)row_bytes;
-    const uint32_t woffq = woff + 16u + 16u * (uint32_t)h;
+    const uint32_t woffq = woff + (QT == FH3K_Q5_K ? 48u : (QT == FH3K_Q6_K ? 0u : 16u)) + 16u * (uint32_t)h;
+    const uint8_t *wbase = W + (size_t)rowbase * row_bytes;
     const int wf = (r >> 5) * 4;   // first LDS fragment of this row's 32-row block
     const int wl = r & 31;
 
@@ -1931,12 +2032,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
 #pragma unroll
         for (int b = 0; b < 4; b++) acc[a][b] = f32x16{};
 
-    GemmRaw re, ro;                // raw weights of even / odd steps
+    GemmRaw<QT> re, ro;              // raw weights of even / odd steps
     half8 xe[TBW][4], xo[TBW][4];  // activations of even / odd steps
-    gemm_load_raw<0>(wr, woff, woffq, sb0, re, re);
-    gemm_load_xs(xr, xoff, tbs, 4 * sb0, xe);
-    gemm_load_raw<1>(wr, woff, woffq, sb0, ro, re);
-    gemm_dequant(lds[0], re, 0, wf, wl, h);
+    gemm_load_raw<QT, 0>(wr, wbase, woff, woffq, sb0, re, re);
+    gemm_load_xs<TBW, QT>(xr, xoff, tbs, 4 * sb0, xe);
+    gemm_load_raw<QT, 1>(wr, wbase, woff, woffq, sb0, ro, re);
+    gemm_dequant<QT, 0>(lds[0], re, wf, wl, h);
     __syncthreads();
     // one super-block (4 K steps) per iteration; the loads and the dequant of
     // the step after the last are clamped onto the last super-block (valid
@@ -1946,36 +2047,36 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, 
         const int s = 4 * sb;
         const int nb = sb + 1 < sb1 ? sb + 1 : sb;
         // step s (chunk 0): MFMA from lds[0]; dequant chunk 1 into lds[1]
-        gemm_load_xs(xr, xoff, tbs, s + 1, xo);
-        gemm_load_raw<2>(wr, woff, woffq, sb, re, ro);
-        gemm_dequant(lds[1], ro, 1, wf, wl, h);
+        gemm_load_xs<TBW, QT>(xr, xoff, tbs, s + 1, xo);
+        gemm_load_raw<QT, 2>(wr, wbase, woff, woffq, sb, re, ro);
+        gemm_dequant<QT, 1>(lds[1], ro, wf, wl, h);
         __builtin_amdgcn_s_setprio(2);
         gemm_mfma(lds[0], lane, xe, acc);
         gemm_pipe<TBW>();
         __builtin_amdgcn_s_setprio(0);
         __syncthreads();
         // step s+1 (chunk 1): MFMA from lds[1]; dequant chunk 2 into lds[0]
-        gemm_load_xs(xr, xoff, tbs, s + 2, xe);
-        gemm_load_raw<3>(wr, woff, woffq, sb, ro, re);
-        gemm_dequant(lds[0], re, 2, wf, wl, h);
+        gemm_load_xs<TBW, QT>(xr, xoff, tbs, s + 2, xe);
+        gemm_load_raw<QT, 3>(wr, wbase, woff, woffq, sb, ro, re);
+        gemm_dequant<QT, 2>(lds[0], re, wf, wl, h);
         __builtin_amdgcn_s_setprio(2);
         gemm_mfma(lds[1], lane, xo, acc);
         gemm_pipe<TBW>();
         __builtin_amdgcn_s_setprio(0);
         __syncthreads();
         // step s+2 (chunk 2): MFMA from lds[0]; dequant chunk 3 into lds[1]
-        gemm_load_xs(xr, xoff, tbs, s + 3, xo);
-        gemm_load_raw<0>(wr, woff, woffq, nb, re, ro);
-        gemm_dequant(lds[1], ro, 3, wf, wl, h);
+        gemm_load_xs<TBW, QT>(xr, xoff, tbs, s + 3, xo);
+        gemm_load_raw<QT, 0>(wr, wbase, woff, woffq, nb, re, ro);
+        gemm_dequant<QT, 3>(lds[1], ro, wf, wl, h);
         __builtin_amdgcn_s_setprio(2);
         gemm_mfma(lds[0], lane, xe, acc);
         gemm_pipe<TBW>();
         __builtin_amdgcn_s_setprio(0);
         __syncthreads();
         // step s+3 (chunk 3): MFMA from lds[1]; dequant the next chunk 0 into lds[0]
-        gemm_load_xs(xr, xoff, tbs, 4 * nb, xe);
-        gemm_load_raw<1>(wr, woff, woffq, nb, ro, re);
-        gemm_dequant(lds[0], re, 0, wf, wl, h);
+        gemm_load_xs<TBW, QT>(xr, xoff, tbs, 4 * nb, xe);
+        gemm_load_raw<QT, 1>(wr, wbase, woff, woffq, nb, ro, re);
+        gemm_dequant<QT, 0>(lds[0], re, wf, wl, h);
         __builtin_amdgcn_s_setprio(2);
         gemm_mfma(lds[1], lane, xo, acc);
         gemm_pipe<TBW>();
@@ -3099,9 +3200,10 @@ extern "C" size_t fh3k_gemm_part_bytes(int N, int K, int M, int epi) {
     return S > 1 ? (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
-extern "C" hipError_t fh3k_gemm_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16,
-                                    const float *xs_inv, const float *bias, float *y, int M, int epi,
-                                    const float *aux, float *part, hipStream_t st) {
+template <int QT>
+static hipError_t launch_gemm(const void *W, int64_t row_bytes, int N, int K, const void *x16, const float *xs_inv,
+                              const float *bias, float *y, int M, int epi, const float *aux, float *part,
+                              hipStream_t st) {
     if (epi == EPI_SWIGLU && (N % 128)) return hipErrorInvalidValue;
     if ((uint64_t)N * (uint64_t)row_bytes >= (1ull << 32)) return hipErrorInvalidValue;  // 32-bit row offsets
     int C, S;
@@ -3111,11 +3213,11 @@ extern "C" hipError_t fh3k_gemm_epi(const void *W, int64_t row_bytes, int N, int
     const int m_tiles = (M + BM - 1) / BM;
     const int n_tiles = epi == EPI_SWIGLU ? (N / 2) / 64 : (N + GEMM_BN - 1) / GEMM_BN;
     if (tbw == 1)
-        hipLaunchKernelGGL(k_gemm<1>, dim3((unsigned)(m_tiles * n_tiles * S)), dim3(256), 0, st,
+        hipLaunchKernelGGL((k_gemm<1, QT>), dim3((unsigned)(m_tiles * n_tiles * S)), dim3(256), 0, st,
                            (const uint8_t *)W, row_bytes, N, K, (const half8 *)x16, xs_inv, bias, y, M,
                            m_tiles, n_tiles, epi, aux, C, S > 1 ? part : nullptr);
     else
-        hipLaunchKernelGGL(k_gemm<2>, dim3((unsigned)(m_tiles * n_tiles * S)), dim3(256), 0, st,
+        hipLaunchKernelGGL((k_gemm<2, QT>), dim3((unsigned)(m_tiles * n_tiles * S)), dim3(256), 0, st,
                            (const uint8_t *)W, row_bytes, N, K, (const half8 *)x16, xs_inv, bias, y, M,
                            m_tiles, n_tiles, epi, aux, C, S > 1 ? part : nullptr);
     hipError_t e = hipGetLastError();
@@ -3125,6 +3227,25 @@ extern "C" hipError_t fh3k_gemm_epi(const void *W, int64_t row_bytes, int N, int
     hipLaunchKernelGGL(k_midm_sum, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, st, part, S, M, N, xs_inv,
                        bias, y, epi, aux);
     return hipGetLastError();
+}
+
+extern "C" hipError_t fh3k_gemm_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16,
+                                    const float *xs_inv, const float *bias, float *y, int M, int epi,
+                                    const float *aux, float *part, hipStream_t st) {
+    return launch_gemm<FH3K_Q4_K>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, epi, aux, part, st);
+}
+
+extern "C" int fh3k_gemm_q_takes(int type) { return type == FH3K_Q5_K || type == FH3K_Q6_K; }
+
+extern "C" hipError_t fh3k_gemm_q(int type, const void *W, int64_t row_bytes, int N, int K, const void *x16,
+                                  const float *xs_inv, const float *bias, float *y, int M, float *part,
+                                  hipStream_t st) {
+    if (K % 256 || K < 256 || N < 1 || M < 1) return hipErrorInvalidValue;
+    if (type == FH3K_Q5_K)
+        return launch_gemm<FH3K_Q5_K>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, part, st);
+    if (type == FH3K_Q6_K)
+        return launch_gemm<FH3K_Q6_K>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, part, st);
+    return hipErrorInvalidValue;
 }
 
 // ---------------------------------------------------------------------------

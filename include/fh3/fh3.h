@@ -114,8 +114,9 @@ void fh3_dequant(int type, const void *src, float *dst, int64_t n);
 /* y[n_tok][out] = x[n_tok][in] * W^T (+ bias[out]) on host buffers, computed
  * on the GPU (inputs are copied in and y out on every call).  NULL pointers or
  * non-positive sizes are a silent no-op, as in the reference.  Weight types:
- * every type fh3_dequant decodes (Q4_K on its own kernels; F32, F16, BF16,
- * Q8_0, Q2_K, Q3_K, Q5_K, Q6_K decoded per call to fp16 rows).  in is any
+ * every type fh3_dequant decodes (Q4_K, Q5_K and Q6_K rows of up to 32768
+ * values read in place by the product kernels; F32, F16, BF16, Q8_0, Q2_K,
+ * Q3_K and longer rows decoded per call to fp16 rows).  in is any
  * length for F32, F16 and BF16 (e.g. the DiT's 32- and 96-value patch rows),
  * a multiple of 32 for Q8_0 and of 256 for the K types (whole blocks, the
  * rows the reference defines), up to 2^24; other types or in print an error

@@ -55,13 +55,14 @@ int fh3_hip_dequant_dev(int type, const void *d_src, float *d_dst, int64_t rows,
  * large-M kernel).  w->in: any length up to 2^24 for F32, F16 and BF16, a
  * multiple of 32 for Q8_0, of 256 for the K types (FH3_E_INVALID otherwise).
  * Q4_K rows of whole super-blocks up to 32768 values run the kernels described
- * here; the other types fh3_dequant decodes, and rows of any type with
- * in % 256 != 0 or in > 32768, are first decoded to fp16 rows of
- * round_up(in, 256) columns, zero-padded (the exact value rounded once; F16
- * used as it is where in % 256 == 0), into a library buffer of
- * out * round_up(in, 256) * 2 bytes (none for Q5_K / Q6_K up to 64 tokens,
- * which are read in place), then multiplied with the same activation handling
- * (zeros past in) and fp32 accumulation.  Work is enqueued on `stream` and the call
+ * here, and Q5_K / Q6_K rows of that kind are read in place too (the
+ * FH3_HIP_PATH_SKINNY kernel up to 64 tokens, FH3_HIP_PATH_GEMM above); the
+ * other types fh3_dequant decodes, and rows of any type with in % 256 != 0 or
+ * in > 32768, are first decoded to fp16 rows of round_up(in, 256) columns,
+ * zero-padded (the exact value rounded once; F16 used as it is where
+ * in % 256 == 0), into a library buffer of out * round_up(in, 256) * 2 bytes,
+ * then multiplied with the same activation handling (zeros past in) and fp32
+ * accumulation.  Work is enqueued on `stream` and the call
  * returns without synchronising.  For one to four tokens (FH3_HIP_PATH_GEMV8
  * below) activations are quantised to int16 inside the product kernel and
  * weights enter an integer MFMA exactly; otherwise activations are converted to

@@ -1,15 +1,18 @@
-"""GPU parity of the Q5_K and Q6_K weights read in place by the small-M kernel
-(k_skinny with QT = Q5_K / Q6_K, up to 64 tokens), through the C-ABI, against
-the CPU oracle (fh3's fh3_matmul, src/core/fh3_ops.c:317-404, on the decoders
-of src/core/fh3_quant.c:198-282).
+"""GPU parity of the Q5_K and Q6_K weights read in place, by the small-M
+kernel (k_skinny with QT = Q5_K / Q6_K, up to 64 tokens) and by the GEMM
+(k_gemm with QT = Q5_K / Q6_K, above), through the C-ABI, against the CPU
+oracle (fh3's fh3_matmul, src/core/fh3_ops.c:317-404, on the decoders of
+src/core/fh3_quant.c:198-282).
 
 Bars: rel-Frobenius <= 2e-3 against the oracle, bitwise reproducible.  The
 one-hot cases pin the arithmetic itself: with one non-zero activation per
-token the product is one weight, which the native kernel forms as
-d * (sc * q) with the integer part exact in fp16 (Q5_K always; Q6_K while
+token the product is one weight.  The small-M kernel forms it as d * (sc * q)
+with the integer part exact in fp16 (Q5_K always; Q6_K while
 |sc * (q - 32)| <= 2048), so it matches the reference's fp32 value to fp32
 rounding, where a product on weights rounded to fp16 would miss it by up to
 2^-11 relative (Q6_K weights above that bound: at most that one rounding).
+The GEMM stages every weight in fp16: for Q6_K exactly the reference's fp32
+value rounded once, for Q5_K within one fp16 rounding of it.
 """
 import numpy as np
 import pytest
@@ -126,6 +129,61 @@ def test_native_weights_exact(gpu, oracle, name):
     assert rel[~exact].max(initial=0.0) <= 5e-4  # one fp16 rounding of an integer above 2048
 
 
+GEMM_CASES = [
+    # M, K, N, bias: one 128-token tile (one super-block; a partial row block),
+    # 129-256 tokens on 128-token tiles, 256-token tiles, K split into windows
+    # or not (2048 x 4096: enough tiles), odd super-block counts
+    (65, 256, 16, False),
+    (100, 1024, 80, True),
+    (128, 5376, 130, False),
+    (200, 2048, 200, True),
+    (300, 8192, 96, False),
+    (600, 5120, 300, True),
+    (2048, 1024, 4096, False),
+]
+
+
+@pytest.mark.parametrize("name", ["Q5_K", "Q6_K"])
+@pytest.mark.parametrize("M,K,N,use_bias", GEMM_CASES)
+def test_native_gemm_vs_oracle(gpu, oracle, name, M, K, N, use_bias):
+    """Above 64 tokens: the GEMM reads the blocks in place; oracle on up to 160
+    seeded output rows (rows are independent)."""
+    _say("native gemm %s M=%d K=%d N=%d bias=%d" % (name, M, K, N, use_bias))
+    rng = np.random.default_rng(_tid(name) * 7907 + M * 131 + K + N)
+    raw = H.random_blocks(rng, name, N, K, scale_lo=-12, scale_hi=-8)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32) if use_bias else None
+    assert gpu.matmul_workspace_bytes(K, N, M, qtype=_tid(name)) == gpu.matmul_workspace_bytes(K, N, M)
+    y = _dev(gpu, raw, _tid(name), K, N, x, bias)
+    rows = np.arange(N) if N <= 160 else np.sort(rng.choice(N, 160, replace=False))
+    yo = _oracle(oracle, raw, name, K, N, x, bias, rows=None if N <= 160 else rows)
+    err = H.rel_fro(y[:, rows], yo)
+    _say("  rel_fro = %.3e" % err)
+    assert np.isfinite(y).all()
+    assert err <= TOL
+    assert np.array_equal(y.view(np.uint32), _dev(gpu, raw, _tid(name), K, N, x, bias).view(np.uint32))
+
+
+@pytest.mark.parametrize("name", ["Q5_K", "Q6_K"])
+def test_native_gemm_weights(gpu, oracle, name):
+    """The identity as activations (512 tokens, K = 512) reads every weight of
+    64 rows through the GEMM: Q6_K gives the reference's fp32 weight rounded
+    once to fp16, bit for bit; Q5_K stays within one fp16 rounding of it."""
+    rng = np.random.default_rng(950 + _tid(name))
+    K, N = 512, 64
+    raw = H.random_blocks(rng, name, N, K, scale_lo=-12, scale_hi=-8)
+    x = np.eye(K, dtype=np.float32)
+    y = _dev(gpu, raw, _tid(name), K, N, x)  # y[k][row] = w[row][k]
+    w = H.oracle_dequant(oracle, raw, N, K, qtype=_tid(name)).T
+    if name == "Q6_K":
+        assert np.array_equal(y, w.astype(np.float16).astype(np.float32))
+    else:
+        err = np.abs(y - w)
+        _say("  max |y - w| / max |w| = %.3e, rel_fro %.3e" % (err.max() / np.abs(w).max(), H.rel_fro(y, w)))
+        assert err.max() <= 2.0 ** -11 * np.abs(w).max()
+        assert H.rel_fro(y, w) <= 5e-4
+
+
 # the text encoder's Q5_K / Q6_K tensor shapes (K -> N) at prompt lengths
 TE_CASES = [("Q5_K", 5120, 1024), ("Q6_K", 5120, 1024), ("Q6_K", 8192, 5120), ("Q6_K", 25600, 5120)]
 
@@ -133,11 +191,11 @@ TE_CASES = [("Q5_K", 5120, 1024), ("Q6_K", 5120, 1024), ("Q6_K", 8192, 5120), ("
 @pytest.mark.parametrize("name,K,N", TE_CASES)
 def test_text_encoder_shapes(gpu, oracle, name, K, N):
     """Oracle on 64 seeded output rows (rows are independent) for M = 1, 4, 16
-    and 64 tokens."""
+    and 64 tokens (k_skinny) and 65, 128, 300 and 600 (k_gemm)."""
     rng = np.random.default_rng(_tid(name) + K + N)
     raw = H.random_blocks(rng, name, N, K, scale_lo=-12, scale_hi=-8)
     rows = np.sort(rng.choice(N, 64, replace=False))
-    for M in (1, 4, 16, 64):
+    for M in (1, 4, 16, 64, 65, 128, 300, 600):
         _say("te %s K=%d N=%d M=%d" % (name, K, N, M))
         x = rng.standard_normal((M, K)).astype(np.float32)
         y = _dev(gpu, raw, _tid(name), K, N, x)
@@ -148,9 +206,9 @@ def test_text_encoder_shapes(gpu, oracle, name, K, N):
 
 
 @pytest.mark.parametrize("name", ["Q5_K", "Q6_K"])
-def test_native_agrees_with_decoded_rows(gpu, name):
-    """The native kernel and the decoded-row GEMM (forced path) agree to the
-    fp16 rounding of the weights."""
+def test_native_skinny_agrees_with_native_gemm(gpu, name):
+    """The small-M kernel and the GEMM (forced path), both reading the blocks
+    in place, agree to the fp16 rounding of the weights."""
     F = gpu
     rng = np.random.default_rng(77 + _tid(name))
     K, N, M = 3072, 112, 33

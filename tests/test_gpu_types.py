@@ -2,8 +2,9 @@
 type its fh3_dequant decodes: src/core/fh3_ops.c:317-404), on the GPU through
 the C-ABI, against the CPU oracle.  These weights are decoded per call to fp16
 rows (the exact value rounded once) and multiplied by k_skinny16 / k_gemm16,
-except Q5_K and Q6_K up to 64 tokens, which k_skinny reads in place
-(tests/test_gpu_native_q56.py covers that kernel on its own).
+except Q5_K and Q6_K, which k_skinny (up to 64 tokens) and k_gemm (above)
+read in place (tests/test_gpu_native_q56.py covers those kernels on their
+own).
 
 Bar: rel-Frobenius <= 2e-3 of the oracle, bitwise reproducible.
 """
@@ -90,8 +91,8 @@ def test_text_encoder_shape(gpu, oracle, name):
 
 
 def test_host_wrapper_and_forced_paths(gpu, oracle):
-    """fh3_matmul (host pointers) takes a Q6_K weight; both fp16-row kernels
-    give the oracle's result at the same shape."""
+    """fh3_matmul (host pointers) takes a Q6_K weight; both product kernels
+    (forced paths) give the oracle's result at the same shape."""
     t = _type_id("Q6_K")
     rng = np.random.default_rng(3)
     K, N, M = 1024, 96, 20

@@ -544,9 +544,11 @@ static size_t w16_bytes(const Fh3W *w, int n_tok) {
     return (size_t)w->out * (size_t)kpad(w->in) * 2;
 }
 
-// Partial sums of the in-place Q5_K / Q6_K GEMM (0 when it does not split K).
+// Partial sums of the in-place Q5_K / Q6_K products (0 when they do not split
+// K).
 static size_t part16_bytes(const Fh3W *w, int n_tok) {
-    if (!reads_in_place_q(w, n_tok) || path16(n_tok, w->in) != FH3_HIP_PATH_GEMM) return 0;
+    if (!reads_in_place_q(w, n_tok)) return 0;
+    if (path16(n_tok, w->in) == FH3_HIP_PATH_SKINNY) return fh3k_skinny_q_part_bytes((int)w->out, (int)w->in, n_tok);
     return fh3k_gemm_part_bytes((int)w->out, (int)w->in, n_tok, FH3_EPI_NONE);
 }
 
@@ -556,17 +558,16 @@ static int product16(const Fh3W *w, const void *x16, const float *xs_inv, int n_
     const int K = (int)w->in, Kp = (int)kpad(w->in), N = (int)w->out;
     if (reads_in_place_q(w, n_tok)) {
         const int64_t rb = (int64_t)fh3_row_bytes(w->type, w->in);
-        if (path16(n_tok, w->in) == FH3_HIP_PATH_SKINNY) {
-            FH3_HIPCALL(fh3k_skinny_q(w->type, w->data, rb, N, K, x16, xs_inv, bias, d_y, n_tok, st));
-            return FH3_OK;
-        }
         float *part = nullptr;
         if (const size_t pb = part16_bytes(w, n_tok)) {
             int rc = grow(g.part, pb, st);
             if (rc != FH3_OK) return rc;
             part = (float *)g.part.p;
         }
-        FH3_HIPCALL(fh3k_gemm_q(w->type, w->data, rb, N, K, x16, xs_inv, bias, d_y, n_tok, part, st));
+        if (path16(n_tok, w->in) == FH3_HIP_PATH_SKINNY)
+            FH3_HIPCALL(fh3k_skinny_q(w->type, w->data, rb, N, K, x16, xs_inv, bias, d_y, n_tok, part, st));
+        else
+            FH3_HIPCALL(fh3k_gemm_q(w->type, w->data, rb, N, K, x16, xs_inv, bias, d_y, n_tok, part, st));
         return FH3_OK;
     }
     const void *w16 = w->data;

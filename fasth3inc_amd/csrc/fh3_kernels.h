@@ -65,9 +65,12 @@ hipError_t fh3k_gemm16(const void *W16, int N, int K, const void *x16, const flo
                        float *y, int M, hipStream_t st);
 // Q5_K / Q6_K weights (type FH3K_Q5_K / FH3K_Q6_K) read in place by the
 // small-M kernel, M <= fh3k_skinny_max_tokens(), same fragments as fh3k_skinny;
-// fh3k_skinny_q_takes(type) says whether a type has this kernel.
+// fh3k_skinny_q_takes(type) says whether a type has this kernel.  Rows that
+// give fewer row blocks than the chip takes are split into K windows whose raw
+// sums go to part (fh3k_skinny_q_part_bytes(N, K, M) bytes; 0 = no split).
 hipError_t fh3k_skinny_q(int type, const void *W, int64_t row_bytes, int N, int K, const void *x16,
-                         const float *xs_inv, const float *bias, float *y, int M, hipStream_t st);
+                         const float *xs_inv, const float *bias, float *y, int M, float *part, hipStream_t st);
+size_t fh3k_skinny_q_part_bytes(int N, int K, int M);
 int fh3k_skinny_q_takes(int type);
 
 // Product epilogues (EPI_* of fh3_kernels.hip; FH3_EPI_* of fh3_hip.h): 0 plain

@@ -948,12 +948,19 @@ __device__ __forceinline__ void sk6_superblock(const SkRaw<FH3K_Q6_K> &r, bool v
 // (deterministic).
 // QT selects the weight type: Q4_K, or Q5_K / Q6_K read in place (the lane
 // pieces and products of SkRaw, sk5_superblock, sk6_superblock).
+// Q5_K / Q6_K rows may also be split into K windows of L super-blocks
+// (blockIdx.y = window; windows are what a workgroup's wavefronts divide, a
+// short last window borrows super-blocks of the one before it as padding):
+// each workgroup then writes its raw sums to part[window][t][o] and
+// k_midm_sum adds the windows in order.  part = nullptr: one window, the
+// epilogue here.
 // ---------------------------------------------------------------------------
 template <int QT, int TB, int C, int MAXT = 512, int RMAX = (TB == 1 ? 5 : 3)>
 __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_skinny(
     const uint8_t *__restrict__ W, int64_t row_bytes, int N, int K, const half8 *__restrict__ X16,
     const float *__restrict__ xs_inv, const float *__restrict__ bias, float *__restrict__ Y, int M, int epi,
-    const float *__restrict__ aux) {
+    const float *__restrict__ aux, int L = 0, float *__restrict__ part = nullptr) {
+    constexpr bool KW = QT != FH3K_Q4_K;  // K windows available
     extern __shared__ f32x4 red[];  // [NW][TB][64]
     constexpr int RING = C < RMAX ? C : RMAX;
     constexpr int AB = TB == 1 ? 2 : 1;  // activation buffers
@@ -967,8 +974,11 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) vo
     const int orow = epi == EPI_SWIGLU ? (j < 8 ? o0 + j : F + o0 + j - 8) : (o0 + j < N ? o0 + j : N - 1);
     const int nsb = K / 256;
     const int kf_n = K / 16;
-    const int own = wave * C;                          // first super-block this wave owns
-    const int s0 = own < nsb - C ? own : nsb - C;      // window start, inside the row
+    // the K window [kb, kb + kn): the whole row, or window blockIdx.y
+    const int kb = KW ? (int)blockIdx.y * L : 0;
+    const int kn = KW && part ? (L < nsb - kb ? L : nsb - kb) : nsb;
+    const int own = kb + wave * C;                         // first super-block this wave owns
+    const int s0 = own < kb + kn - C ? own : kb + kn - C;  // its super-blocks, inside the row
     constexpr int SB = sk_bytes<QT>();
     const uint8_t *wh = W + (size_t)orow * row_bytes + (size_t)s0 * SB;  // super-block s0
     const uint8_t *wa, *wb;                                              // this lane's pieces of it
@@ -1030,6 +1040,20 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(2, 8))) vo
     // 4*(l/16) + v; the workgroup may have fewer threads than TB*64
     for (int idx = threadIdx.x; idx < TB * 64; idx += blockDim.x) {
         const int tb = idx >> 6, l = idx & 63;
+        if (KW && part) {  // this window's raw sums
+            f32x4 s = red[tb * 64 + l];
+            for (int w = 1; w < NW; w++) s += red[(w * TB + tb) * 64 + l];
+            const int o = o0 + (l & 15);
+            if (o < N) {
+                float *pp = part + (size_t)blockIdx.y * M * N + o;
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int t = tb * 16 + 4 * (l >> 4) + v;
+                    if (t < M) pp[(size_t)t * N] = s[v];
+                }
+            }
+            continue;
+        }
         if (epi == EPI_SWIGLU) {
             if ((l & 15) >= 8) continue;  // the gate column of l is l + 8
             f32x4 sv = red[tb * 64 + l], sg = red[tb * 64 + l + 8];
@@ -2661,36 +2685,41 @@ static unsigned row_blocks16(int N, int epi) {
     return (unsigned)(epi == EPI_SWIGLU ? (N / 2) / 8 : (N + 15) / 16);
 }
 
+// S > 1 (Q5_K / Q6_K only): K windows of L super-blocks, raw sums to part.
 template <int QT, int TB, int C>
 static hipError_t launch_skinny_c(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,
                                   const float *bias, float *y, int M, int NW, int epi, const float *aux,
-                                  hipStream_t st) {
+                                  hipStream_t st, int L, int S, float *part) {
     const size_t lds = (size_t)NW * TB * 64 * sizeof(f32x4);
-    hipLaunchKernelGGL((k_skinny<QT, TB, C>), dim3(row_blocks16(N, epi)), dim3(NW * 64), lds, st, (const uint8_t *)W,
-                       rb, N, K, (const half8 *)x16, xs_inv, bias, y, M, epi, aux);
+    hipLaunchKernelGGL((k_skinny<QT, TB, C>), dim3(row_blocks16(N, epi), (unsigned)S), dim3(NW * 64), lds, st,
+                       (const uint8_t *)W, rb, N, K, (const half8 *)x16, xs_inv, bias, y, M, epi, aux, L,
+                       S > 1 ? part : nullptr);
     return hipGetLastError();
 }
 
 template <int TB, int QT = FH3K_Q4_K>
 static hipError_t launch_skinny(const void *W, int64_t rb, int N, int K, const void *x16,
                                 const float *xs_inv, const float *bias, float *y, int M, int epi, const float *aux,
-                                hipStream_t st) {
+                                hipStream_t st, int L = 0, int S = 1, float *part = nullptr) {
     int C, NW;
-    skinny_split(K / 256, TB, C, NW);
+    skinny_split(S > 1 ? L : K / 256, TB, C, NW);
+#define FH3_SKINNY_C(c)                                                                                            \
+    case c: return launch_skinny_c<QT, TB, c>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st, L, S, part)
     switch (C) {
-        case 1: return launch_skinny_c<QT, TB, 1>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 2: return launch_skinny_c<QT, TB, 2>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 3: return launch_skinny_c<QT, TB, 3>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 4: return launch_skinny_c<QT, TB, 4>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 5: return launch_skinny_c<QT, TB, 5>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 6: return launch_skinny_c<QT, TB, 6>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 7: return launch_skinny_c<QT, TB, 7>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 8: return launch_skinny_c<QT, TB, 8>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 10: return launch_skinny_c<QT, TB, 10>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 13: return launch_skinny_c<QT, TB, 13>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
-        case 16: return launch_skinny_c<QT, TB, 16>(W, rb, N, K, x16, xs_inv, bias, y, M, NW, epi, aux, st);
+        FH3_SKINNY_C(1);
+        FH3_SKINNY_C(2);
+        FH3_SKINNY_C(3);
+        FH3_SKINNY_C(4);
+        FH3_SKINNY_C(5);
+        FH3_SKINNY_C(6);
+        FH3_SKINNY_C(7);
+        FH3_SKINNY_C(8);
+        FH3_SKINNY_C(10);
+        FH3_SKINNY_C(13);
+        FH3_SKINNY_C(16);
         default: return hipErrorInvalidValue;
     }
+#undef FH3_SKINNY_C
 }
 
 extern "C" hipError_t fh3k_skinny_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16,
@@ -2714,26 +2743,79 @@ extern "C" hipError_t fh3k_skinny(const void *W, int64_t row_bytes, int N, int K
 
 extern "C" int fh3k_skinny_max_tokens(void) { return 64; }
 
+static int device_cus(void) {
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    }
+    return cus[dev];
+}
+
+namespace {
+__global__ __launch_bounds__(256) void k_midm_sum(const float *__restrict__ part, int S, int M, int N,
+                                                  const float *__restrict__ xs_inv, const float *__restrict__ bias,
+                                                  float *__restrict__ Y, int epi, const float *__restrict__ aux);
+}  // namespace
+
+// K windows of the Q5_K / Q6_K small-M product: when the 16-row blocks
+// number fewer than four per CU, S windows of L >= 4 super-blocks (S * L >= nsb,
+// every window non-empty), so that the grid fills the chip (Q6_K 25600 ->
+// 5120 is 320 row blocks, 1.25 rounds of 256 CUs at one workgroup per CU;
+// 5120 -> 1024 is 64).
+static void skinny_kwin(int N, int K, int &L, int &S) {
+    const int nsb = K / 256, rbs = (N + 15) / 16;
+    const int want = (4 * device_cus() + rbs - 1) / rbs;
+    S = want < nsb / 4 ? want : nsb / 4;
+    if (S < 2) {
+        S = 1, L = nsb;
+        return;
+    }
+    L = (nsb + S - 1) / S;
+    S = (nsb + L - 1) / L;
+}
+
+extern "C" size_t fh3k_skinny_q_part_bytes(int N, int K, int M) {
+    int L, S;
+    if (N < 1 || K < 256 || M < 1) return 0;
+    skinny_kwin(N, K, L, S);
+    return S > 1 ? (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
 // Q5_K / Q6_K rows read in place by k_skinny (n_tok <= 64): no decoded copy.
 template <int QT>
 static hipError_t launch_skinny_q(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,
-                                  const float *bias, float *y, int M, hipStream_t st) {
+                                  const float *bias, float *y, int M, float *part, hipStream_t st) {
+    int L, S;
+    skinny_kwin(N, K, L, S);
+    if (S > 1 && !part) return hipErrorInvalidValue;
+    hipError_t e;
     switch ((M + 15) / 16) {
-        case 1: return launch_skinny<1, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st);
-        case 2: return launch_skinny<2, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st);
-        case 3: return launch_skinny<3, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st);
-        case 4: return launch_skinny<4, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st);
+        case 1: e = launch_skinny<1, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st, L, S, part); break;
+        case 2: e = launch_skinny<2, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st, L, S, part); break;
+        case 3: e = launch_skinny<3, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st, L, S, part); break;
+        case 4: e = launch_skinny<4, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st, L, S, part); break;
         default: return hipErrorInvalidValue;
     }
+    if (e != hipSuccess || S == 1) return e;
+    const int64_t outs = (int64_t)M * N;
+    hipLaunchKernelGGL(k_midm_sum, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, st, part, S, M, N, xs_inv,
+                       bias, y, (int)EPI_NONE, (const float *)nullptr);
+    return hipGetLastError();
 }
 
 extern "C" int fh3k_skinny_q_takes(int type) { return type == FH3K_Q5_K || type == FH3K_Q6_K; }
 
 extern "C" hipError_t fh3k_skinny_q(int type, const void *W, int64_t row_bytes, int N, int K, const void *x16,
-                                    const float *xs_inv, const float *bias, float *y, int M, hipStream_t st) {
+                                    const float *xs_inv, const float *bias, float *y, int M, float *part,
+                                    hipStream_t st) {
     if (K % 256 || K < 256 || N < 1 || M < 1 || M > 64) return hipErrorInvalidValue;
-    if (type == FH3K_Q5_K) return launch_skinny_q<FH3K_Q5_K>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, st);
-    if (type == FH3K_Q6_K) return launch_skinny_q<FH3K_Q6_K>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, st);
+    if (type == FH3K_Q5_K)
+        return launch_skinny_q<FH3K_Q5_K>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, part, st);
+    if (type == FH3K_Q6_K)
+        return launch_skinny_q<FH3K_Q6_K>(W, row_bytes, N, K, x16, xs_inv, bias, y, M, part, st);
     return hipErrorInvalidValue;
 }
 
@@ -2762,17 +2844,6 @@ extern "C" int fh3k_gemv8_fits(int K, int M) {
     if (M < 1 || M > G8_MAX_TOKENS || K < 256 || K % 256) return 0;
     const size_t lds = gemv8_lds(K, M, C, NW);
     return lds > 0 && lds <= kGemv8MaxLds;
-}
-
-static int device_cus(void) {
-    static int cus[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cus[dev]) {
-        int n = 0;
-        cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
-    }
-    return cus[dev];
 }
 
 template <int MT, int C, int EPI>
@@ -2877,12 +2948,6 @@ extern "C" size_t fh3k_sweep_part_bytes(int N, int K, int M) {
     sweep_split(K / 256, M, S, SL);
     return S > 1 ? (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
-
-namespace {
-__global__ __launch_bounds__(256) void k_midm_sum(const float *__restrict__ part, int S, int M, int N,
-                                                  const float *__restrict__ xs_inv, const float *__restrict__ bias,
-                                                  float *__restrict__ Y, int epi, const float *__restrict__ aux);
-}  // namespace
 
 template <int C, int TB, int LB, int EPI>
 static hipError_t launch_sweep_c(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,

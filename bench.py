@@ -319,10 +319,10 @@ def real_dit_blocks_streamed(ev, st, n_blocks=4, Ms=(3016, 16384), passes=2):
 def te_other_types(ev, st, R=64):
     """The text encoder's long-row Q4_K products (o-projection 8192 -> 5120,
     down-projection 25600 -> 5120) and its Q5_K / Q6_K tensors (Q5_K 5120 ->
-    1024; Q6_K 5120 -> 1024, 8192 -> 5120, 25600 -> 5120) at M = 1, 16 and 64
-    tokens through fh3_hip_matmul_dev (Q4_K: k_gemv8, k_sweep in K slices,
-    k_skinny or k_midm by shape; Q5_K / Q6_K: k_skinny reading the blocks in
-    place).  Q4_K weights are the seeded N(0, 0.02) encoding, the others random
+    1024; Q6_K 5120 -> 1024, 8192 -> 5120, 25600 -> 5120) at M = 1, 16, 64 and
+    300 tokens through fh3_hip_matmul_dev (Q4_K: k_gemv8, k_sweep in K slices,
+    k_skinny or k_midm by shape, k_gemm at 300; Q5_K / Q6_K: k_skinny, in K
+    windows on the long rows, and k_gemm at 300, reading the blocks in place).  Q4_K weights are the seeded N(0, 0.02) encoding, the others random
     blocks with finite scales, all rotated over more than 256 MB of device
     copies; graph of R calls."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -343,7 +343,7 @@ def te_other_types(ev, st, R=64):
             b = F.DeviceBuffer(wb)
             F.lib().fh3_hip_memcpy_dtod(b.ptr, ws[0].ptr, wb)
             ws.append(b)
-        for M in (1, 16, 64):
+        for M in (1, 16, 64, 300):
             dx = F.DeviceBuffer.from_array(rng.standard_normal((M, K)).astype(np.float32))
             dy = F.DeviceBuffer(M * N * 4)
 
@@ -357,8 +357,8 @@ def te_other_types(ev, st, R=64):
             g.launch()
             t_c = ev.time_ms(lambda i: g.launch(), 8, st) / R
             g.close()
-            rows.append({"type": name, "M": M, "K": K, "N": N, "path": F.matmul_path(M, K) if name == "Q4_K" else 1,
-                         "call_us": round(t_c * 1e3, 2),
+            path = F.matmul_path(M, K) if name == "Q4_K" else (F.PATH_SKINNY if M <= 64 else F.PATH_GEMM)
+            rows.append({"type": name, "M": M, "K": K, "N": N, "path": path, "call_us": round(t_c * 1e3, 2),
                          "weight_GBps": round(wb / (t_c * 1e-3) / 1e9, 1),
                          "hbm_frac": round((wb + 4 * M * (K + N)) / (t_c * 1e-3) / HBM_PEAK, 4)})
             log("[bench] %s M=%d K=%d N=%d call %.2f us (%.0f GB/s of weights)"

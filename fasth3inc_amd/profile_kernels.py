@@ -30,8 +30,9 @@ Workloads (each launch sequence is preceded by one untimed warmup launch):
          benchmark runs it): fh3_hip_matmul_prepared_dev -> k_skinny
   q56    Q5_K and Q6_K weights read in place at the text encoder's shapes
          (Q5_K 5120 -> 1024, Q6_K 5120 -> 1024, 8192 -> 5120, 25600 -> 5120)
-         at M = 1 and 16: fh3_hip_matmul_prepared_dev -> k_skinny<Q5_K / Q6_K>;
-         weights rotated as for gemv
+         at M = 1, 16 and 300: fh3_hip_matmul_prepared_dev -> k_skinny<Q5_K /
+         Q6_K> (in K windows, then k_midm_sum, on the long rows) and k_gemm<TBW,
+         Q5_K / Q6_K> at 300; weights rotated as for gemv
   copy   hipMemcpy device-to-device of 256 MiB: a copy of known size that
          calibrates FETCH_SIZE / WRITE_SIZE against the bytes moved
   attn   the DiT attention branch at n = 16384 tokens, 40 heads of 128
@@ -146,7 +147,7 @@ def q56(reps):
         raw = _random_q56(qt, N, K, seed=5)
         copies = max(2, -(-(MALL_BYTES + (64 << 20)) // raw.nbytes))
         ws = [F.DeviceBuffer.from_array(raw) for _ in range(copies)]
-        for M in (1, 16):
+        for M in (1, 16, 300):
             dx = F.DeviceBuffer.from_array(F.synth_x("normal", 0, 200 + M, M, K))
             dy = F.DeviceBuffer(M * N * 4)
             prep = F.DeviceBuffer(F.prepared_bytes(M, K))

@@ -3227,15 +3227,20 @@ extern "C" hipError_t fh3k_midm_epi(const void *W, int64_t row_bytes, int N, int
 // and ordered sum: at N = 5120, 65-128 tokens 26.2-28.4 us against 32.2-34.3
 // with 256-token tiles, 192 / 256 tokens 34.8 / 36.2 against 37.6 / 40.4; at
 // N = 17408, 65-128 tokens 46-54 against 63-68, while at 192 / 256 tokens the
-// 256-token tiles are faster, 76 / 82 against 88 / 92 us.)
+// 256-token tiles are faster, 76 / 82 against 88 / 92 us.)  257-384 tokens
+// take 128-token tiles at every N: three of them pad to 384 rows where two
+// 256-token tiles pad to 512 (300 tokens, K = 5120: N = 1024 / 5120 / 17408
+// 25.3 / 44.4 / 103 us against 29.9 / 51.9 / 142; K = 8192-25600: 2-12 %
+// faster).  From 385 tokens both pad alike and the 256-token tiles are faster.
 static int gemm_tbw(int M, int N, int epi) {
     if (M <= 128) return 1;
+    if (M > 256) return M <= 384 ? 1 : 2;
     const int n_tiles = epi == EPI_SWIGLU ? (N / 2) / 64 : (N + GEMM_BN - 1) / GEMM_BN;
     return M <= 256 && 2 * n_tiles <= 128 ? 1 : 2;
 }
 
 extern "C" int fh3k_gemm_rows(int M) {
-    const int BM = M <= 128 ? 128 : 256;
+    const int BM = M <= 128 || (M > 256 && M <= 384) ? 128 : 256;
     return (M + BM - 1) / BM * BM;
 }
 

@@ -32,10 +32,13 @@ def _case(i):
 
 # and the boundaries the draws above can miss: 17-64 tokens on rows of 20 or
 # more super-blocks (the sweep in K slices), the GEMM on one super-block and
-# with a K split, the first and last token counts of each range
+# with a K split, the first and last token counts of each range, the GEMM's
+# tile-width changes
 CASES = [_case(i) for i in range(24)] + [
     (17, 5120, 300, True, 0), (33, 5376, 130, False, 1), (64, 8192, 200, True, 2), (65, 6144, 200, False, 0),
     (600, 256, 333, True, 1), (4, 8192, 100, False, 2), (5, 256, 17, True, 0), (16, 6400, 96, False, 1),
+    # the GEMM's tile width changes at 257 and 385 tokens
+    (257, 2048, 130, True, 0), (384, 5120, 200, False, 1), (385, 1024, 96, True, 2),
 ]
 
 

@@ -529,8 +529,8 @@ extern "C" int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, vo
 }
 
 // Weights of another type than Q4_K, and general rows of any type: Q5_K and
-// Q6_K rows of whole super-blocks are read in place, by k_skinny up to 64
-// tokens and by k_gemm above; otherwise fp16 rows of kpad(in) columns (the
+// Q6_K rows of whole super-blocks are read in place, by k_skinny (Q6_K: the
+// sweep where it applies, q_sweep) up to 64 tokens and by k_gemm above; otherwise fp16 rows of kpad(in) columns (the
 // weight itself for F16 rows of whole super-blocks, else decoded, zero-padded,
 // into the library's w16 buffer), then k_skinny16 / k_gemm16.
 static bool reads_in_place_q(const Fh3W *w, int n_tok) {
@@ -544,12 +544,24 @@ static size_t w16_bytes(const Fh3W *w, int n_tok) {
     return (size_t)w->out * (size_t)kpad(w->in) * 2;
 }
 
+// Up to 64 tokens Q6_K takes the sweep where Q4_K would (up to 16 tokens, or
+// 17-64 on rows of at least 5120 values), or when that path is forced; other
+// small-M in-place products run k_skinny.
+static bool q_sweep(const Fh3W *w, int n_tok) {
+    if (!fh3k_sweep_q_takes(w->type) || !fh3k_sweep_fits((int)w->in, n_tok)) return false;
+    if (g.path == FH3_HIP_PATH_SWEEP) return true;
+    return g.path == FH3_HIP_PATH_AUTO && (n_tok <= 16 || w->in >= 5120);
+}
+
 // Partial sums of the in-place Q5_K / Q6_K products (0 when they do not split
 // K).
 static size_t part16_bytes(const Fh3W *w, int n_tok) {
     if (!reads_in_place_q(w, n_tok)) return 0;
-    if (path16(n_tok, w->in) == FH3_HIP_PATH_SKINNY) return fh3k_skinny_q_part_bytes((int)w->out, (int)w->in, n_tok);
-    return fh3k_gemm_part_bytes((int)w->out, (int)w->in, n_tok, FH3_EPI_NONE);
+    const int K = (int)w->in, N = (int)w->out;
+    if (path16(n_tok, w->in) == FH3_HIP_PATH_SKINNY)
+        return q_sweep(w, n_tok) ? fh3k_sweep_q_part_bytes(w->type, N, K, n_tok)
+                                 : fh3k_skinny_q_part_bytes(N, K, n_tok);
+    return fh3k_gemm_part_bytes(N, K, n_tok, FH3_EPI_NONE);
 }
 
 // Called with g.mu held (it may grow the library's buffers).
@@ -564,7 +576,9 @@ static int product16(const Fh3W *w, const void *x16, const float *xs_inv, int n_
             if (rc != FH3_OK) return rc;
             part = (float *)g.part.p;
         }
-        if (path16(n_tok, w->in) == FH3_HIP_PATH_SKINNY)
+        if (path16(n_tok, w->in) == FH3_HIP_PATH_SKINNY && q_sweep(w, n_tok))
+            FH3_HIPCALL(fh3k_sweep_q(w->type, w->data, rb, N, K, x16, xs_inv, bias, d_y, n_tok, part, st));
+        else if (path16(n_tok, w->in) == FH3_HIP_PATH_SKINNY)
             FH3_HIPCALL(fh3k_skinny_q(w->type, w->data, rb, N, K, x16, xs_inv, bias, d_y, n_tok, part, st));
         else
             FH3_HIPCALL(fh3k_gemm_q(w->type, w->data, rb, N, K, x16, xs_inv, bias, d_y, n_tok, part, st));

@@ -91,6 +91,13 @@ hipError_t fh3k_sweep_epi(const void *W, int64_t row_bytes, int N, int K, const 
 size_t fh3k_sweep_part_bytes(int N, int K, int M);
 int fh3k_sweep_fits(int K, int M);
 int fh3k_sweep_max_tokens(void);
+// Q6_K weights read in place by the sweep (fh3k_sweep_q_takes), no epilogue:
+// same fragments and launch rules as fh3k_sweep_epi without the group sums;
+// partial sums of its K slices in part (fh3k_sweep_q_part_bytes bytes).
+hipError_t fh3k_sweep_q(int type, const void *W, int64_t row_bytes, int N, int K, const void *x16,
+                        const float *xs_inv, const float *bias, float *y, int M, float *part, hipStream_t st);
+size_t fh3k_sweep_q_part_bytes(int type, int N, int K, int M);
+int fh3k_sweep_q_takes(int type);
 // Large M.  When the 256 x 128 tiles alone would not fill the chip, K is split
 // into windows whose raw sums go to part (fh3k_gemm_part_bytes bytes; 0 = no
 // split) and are added in window order with the epilogue; x16 must hold

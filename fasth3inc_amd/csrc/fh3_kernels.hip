@@ -879,45 +879,63 @@ __device__ __forceinline__ void sk5_superblock(const SkRaw<FH3K_Q5_K> &r, bool v
 // the low (m < 4) or high nibbles: k = 128h + 32(q%2) + 64(m/4) + 8(m%4),
 // fragment 8h + 2(q%2) + 4(m/4) + (m%4)/2 (skinny_load_a with HI = 4), and
 // sub-group 8h + 2(q%2) + 4(m/4) + (m%4)/2, i.e. byte 2(q%2) + (m%4)/2 of
-// scale word 2h + m/4.  B = (1024 + q - 1056) * sc: the difference is exact,
-// the product |sc*(q-32)| <= 4096 is rounded once to fp16 (exact below 2048;
-// the same single rounding k_gemm applies to every weight), then scaled by d
-// in fp32.
+// scale word 2h + m/4.
+// B = sc * (q - 32) per pair as one fused op on exact fp16 operands:
+// q sits in mantissa bits 4-9 of 0x6400 | q << 4 = 1024 + 16q (the nibble in
+// bits 4-7 of the low byte, the 2 high bits in bits 0-1 of the high byte, one
+// v_perm per pair), and fma(1024 + 16q, sc/16, -96 sc) = sc * (q - 32) with
+// sc/16 and -96 sc exact (|96 sc| <= 12288), rounded once: exact while
+// |sc * (q - 32)| <= 2048 (the same single rounding k_gemm applies to every
+// Q4_K weight), then scaled by d in fp32.  One token block after another
+// reads the same B.
+struct Sk6Ops { half2v s16[4], c96[4]; };
+
+__device__ __forceinline__ Sk6Ops sk6_scale_ops(const SkRaw<FH3K_Q6_K> &r, int q) {
+    const uint32_t w0 = (q >> 1) ? r.sc.z : r.sc.x, w1 = (q >> 1) ? r.sc.w : r.sc.y;
+    const int sb = 16 * (q & 1);
+    Sk6Ops o;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t w = i < 2 ? w0 : w1;
+        const float sv = (float)(int)(int8_t)(uint8_t)((w >> (sb + 8 * (i & 1))) & 0xFFu);
+        const _Float16 a = (_Float16)(sv * 0.0625f), c = (_Float16)(sv * -96.0f);
+        o.s16[i] = half2v{a, a};
+        o.c96[i] = half2v{c, c};
+    }
+    return o;
+}
+
+// B operand of MFMA m (see above): 8 fp16 sc * (q - 32)
+__device__ __forceinline__ half8 sk6_b(const SkRaw<FH3K_Q6_K> &r, int q, const Sk6Ops &o, int m) {
+    const int part = m & 3;
+    const bool hi = m >= 4;
+    const u32x4 lq = part < 2 ? r.l0 : r.l1, hq = part < 2 ? r.h0 : r.h1;
+    const uint32_t u0 = (part & 1) ? lq.z : lq.x, u1 = (part & 1) ? lq.w : lq.y;
+    const uint32_t h0 = (part & 1) ? hq.z : hq.x, h1 = (part & 1) ? hq.w : hq.y;
+    const int hs = 2 * (q & 1) + (hi ? 4 : 0);
+    // nibble in bits 4-7 of each byte; 0x64 | high bits in each byte
+    const uint32_t n0 = hi ? (u0 & 0xF0F0F0F0u) : ((u0 << 4) & 0xF0F0F0F0u);
+    const uint32_t n1 = hi ? (u1 & 0xF0F0F0F0u) : ((u1 << 4) & 0xF0F0F0F0u);
+    const uint32_t e0 = ((h0 >> hs) & 0x03030303u) | 0x64646464u, e1 = ((h1 >> hs) & 0x03030303u) | 0x64646464u;
+    const half2v s = o.s16[(hi ? 2 : 0) + (part >> 1)], c = o.c96[(hi ? 2 : 0) + (part >> 1)];
+    const half2v p0 = __builtin_elementwise_fma(__builtin_bit_cast(half2v, __builtin_amdgcn_perm(e0, n0, 0x05010400u)), s, c);
+    const half2v p1 = __builtin_elementwise_fma(__builtin_bit_cast(half2v, __builtin_amdgcn_perm(e0, n0, 0x07030602u)), s, c);
+    const half2v p2 = __builtin_elementwise_fma(__builtin_bit_cast(half2v, __builtin_amdgcn_perm(e1, n1, 0x05010400u)), s, c);
+    const half2v p3 = __builtin_elementwise_fma(__builtin_bit_cast(half2v, __builtin_amdgcn_perm(e1, n1, 0x07030602u)), s, c);
+    return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
 template <int TB>
 __device__ __forceinline__ void sk6_superblock(const SkRaw<FH3K_Q6_K> &r, bool valid, int q,
                                                const half8 (&a)[8][TB], f32x4 acc[TB]) {
     const float d = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(r.d & 0xFFFFu)) : 0.f;
-    const uint32_t w0 = (q >> 1) ? r.sc.z : r.sc.x, w1 = (q >> 1) ? r.sc.w : r.sc.y;
-    const int sb = 16 * (q & 1);
-    half2v scv[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t w = i < 2 ? w0 : w1;
-        const int sv = (int)(int8_t)(uint8_t)((w >> (sb + 8 * (i & 1))) & 0xFFu);
-        const _Float16 h = (_Float16)(float)sv;
-        scv[i] = half2v{h, h};
-    }
-    const half2v off = half2v{(_Float16)-1056.0f, (_Float16)-1056.0f};
-    const int sh = 2 * (q & 1);
+    const Sk6Ops o = sk6_scale_ops(r, q);
     f32x4 aq[TB];
 #pragma unroll
     for (int tb = 0; tb < TB; tb++) aq[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < 8; m++) {
-        const int part = m & 3;
-        const bool hi = m >= 4;
-        const u32x4 lq = part < 2 ? r.l0 : r.l1, hq = part < 2 ? r.h0 : r.h1;
-        const uint32_t u0 = (part & 1) ? lq.z : lq.x, u1 = (part & 1) ? lq.w : lq.y;
-        const uint32_t h0 = (part & 1) ? hq.z : hq.x, h1 = (part & 1) ? hq.w : hq.y;
-        const int hs = sh + (hi ? 4 : 0);
-        const uint32_t b0 = ((hi ? u0 >> 4 : u0) & 0x0F0F0F0Fu) | (((h0 >> hs) & 0x03030303u) << 4);
-        const uint32_t b1 = ((hi ? u1 >> 4 : u1) & 0x0F0F0F0Fu) | (((h1 >> hs) & 0x03030303u) << 4);
-        const half2v s = scv[(hi ? 2 : 0) + (part >> 1)];
-        const half2v p0 = (q4k_magic_pair(b0, 0x04010400u) + off) * s;
-        const half2v p1 = (q4k_magic_pair(b0, 0x04030402u) + off) * s;
-        const half2v p2 = (q4k_magic_pair(b1, 0x04010400u) + off) * s;
-        const half2v p3 = (q4k_magic_pair(b1, 0x04030402u) + off) * s;
-        const half8 b = half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+        const half8 b = sk6_b(r, q, o, m);
 #pragma unroll
         for (int tb = 0; tb < TB; tb++) aq[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m][tb], b, aq[tb], 0, 0, 0);
     }
@@ -1180,7 +1198,10 @@ __device__ __forceinline__ void sweep_scq(const u32x4 hv, const u32x4 ca, const 
     }
 }
 
-template <int C, int TB, int LB, int EPI>
+// QT: Q4_K, or Q6_K read in place (the ring holds SkRaw<Q6_K> pieces, the
+// activation fragments follow sk6_superblock's k order, and there is no min
+// term, so no group sums).
+template <int C, int TB, int LB, int EPI, int QT = FH3K_Q4_K>
 __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int K,
                                               const half8 *__restrict__ X16, const float *__restrict__ xs_inv,
                                               const float *__restrict__ xsum, const float *__restrict__ bias,
@@ -1217,10 +1238,17 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
         const int o0 = (gw + it * GW) * ROWS;
         int orow = EPI == EPI_SWIGLU ? (j < 8 ? o0 + j : F + o0 + j - 8) : o0 + j;
         orow = orow < N ? orow : N - 1;
-        return W + (size_t)orow * row_bytes + (size_t)(sbb + s0) * 144;
+        return W + (size_t)orow * row_bytes + (size_t)(sbb + s0) * sk_bytes<QT>();
     };
+    constexpr bool Q6 = QT == FH3K_Q6_K;
     u32x4 hv[C], ca[C], cb[C];
-    {
+    SkRaw<FH3K_Q6_K> r6[Q6 ? C : 1];
+    if constexpr (Q6) {
+        const uint8_t *wh = wptr(0), *wa, *wb;
+        sk_lane_ptrs<FH3K_Q6_K>(wh, q, wa, wb);
+#pragma unroll
+        for (int s = 0; s < C; s++) sk_load<FH3K_Q6_K>(r6[s], wh, wa, wb, s);
+    } else {
         const uint8_t *wh = wptr(0), *wc = wh + 16 + 32 * q;
 #pragma unroll
         for (int s = 0; s < C; s++) {
@@ -1239,16 +1267,19 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
 #pragma unroll
         for (int tb = 0; tb < TB; tb++) {
             const int t = t0 + 16 * tb + j < M ? t0 + 16 * tb + j : M - 1;
-            xq[tb] = X16 + ((size_t)(t >> 5) * kf_n + (size_t)(sbb + s0) * 16 + 4 * q) * 64 + (t & 31);
-            xs[tb] = xsum + (size_t)t * (K >> 5) + (size_t)(sbb + s0) * 8 + q;
+            const int qf = Q6 ? 8 * (q >> 1) + 2 * (q & 1) : 4 * q;  // see skinny_load_a
+            xq[tb] = X16 + ((size_t)(t >> 5) * kf_n + (size_t)(sbb + s0) * 16 + qf) * 64 + (t & 31);
+            xs[tb] = Q6 ? nullptr : xsum + (size_t)t * (K >> 5) + (size_t)(sbb + s0) * 8 + q;
         }
 #pragma unroll
         for (int i = 0; i < C; i++) {
-            skinny_load_a<TB>(xq, i, a[i]);
+            skinny_load_a<TB, Q6 ? 4 : 2>(xq, i, a[i]);
+            if constexpr (!Q6) {
 #pragma unroll
-            for (int tb = 0; tb < TB; tb++) {
-                xg[i][tb][0] = xs[tb][i * 8];
-                xg[i][tb][1] = xs[tb][i * 8 + 4];
+                for (int tb = 0; tb < TB; tb++) {
+                    xg[i][tb][0] = xs[tb][i * 8];
+                    xg[i][tb][1] = xs[tb][i * 8 + 4];
+                }
             }
         }
     }
@@ -1309,8 +1340,17 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
 #pragma unroll
         for (int tb = 0; tb < TB; tb++) acc[tb] = accm[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
         const uint8_t *nh = wptr(MORE ? it + 1 : it), *nc = nh + 16 + 32 * q;
+        if constexpr (Q6) {
+            const uint8_t *na, *nb;
+            sk_lane_ptrs<FH3K_Q6_K>(nh, q, na, nb);
 #pragma unroll
-        for (int i = 0; i < C; i++) {
+            for (int i = 0; i < C; i++) {
+                sk6_superblock<TB>(r6[i], s0 + i >= own, q, a[i], acc);
+                if (MORE) sk_load<FH3K_Q6_K>(r6[i], nh, na, nb, i);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < (Q6 ? 0 : C); i++) {
             const u32x4 h = hv[i];
             const bool valid = s0 + i >= own;
             const float d = valid ? (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xFFFFu)) : 0.f;
@@ -2925,13 +2965,20 @@ static int sweep_tb(int M) { return (M + 15) / 16; }
 // 256 KB instead of 512 KB).
 static bool sweep_groups(int nsb, int M) { return M > 16 && nsb <= 16; }
 
-static void sweep_split(int nsb, int M, int &S, int &SL) {
+// qt: the weight type.  Q6_K with one token block: rows of at most 16
+// super-blocks whole, eight wavefronts of two (its larger weight ring leaves
+// no room for ten), longer rows in slices of at most 10, one super-block per
+// wavefront (K = 25600: 47.9 against 54.6 us per call in slices of 16, two
+// each; K = 3072 whole: 9.2 against 11.9 in two slices).
+static bool sweep_q6_one(int nsb, int qt) { return qt == FH3K_Q6_K && nsb > 16; }
+
+static void sweep_split(int nsb, int M, int &S, int &SL, int qt = FH3K_Q4_K) {
     if (sweep_groups(nsb, M)) {
         S = 1, SL = nsb;
         return;
     }
     const int tb = sweep_tb(M);
-    const int cap = tb == 1 ? 20 : (tb == 2 ? 10 : 8);
+    const int cap = tb == 1 ? (qt == FH3K_Q6_K ? (sweep_q6_one(nsb, qt) ? 10 : 16) : 20) : (tb == 2 ? 10 : 8);
     S = (nsb + cap - 1) / cap;
     SL = (nsb + S - 1) / S;
 }
@@ -2949,12 +2996,12 @@ extern "C" size_t fh3k_sweep_part_bytes(int N, int K, int M) {
     return S > 1 ? (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
-template <int C, int TB, int LB, int EPI>
+template <int C, int TB, int LB, int EPI, int QT = FH3K_Q4_K>
 static hipError_t launch_sweep_c(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,
                                  const float *xsum, const float *bias, float *y, int M, const float *aux, float *part,
                                  hipStream_t st) {
     int S, SL;
-    sweep_split(K / 256, M, S, SL);
+    sweep_split(K / 256, M, S, SL, QT);
     const int NW = (SL + C - 1) / C;
     const int nblk = (int)row_blocks16(N, EPI);
     const int TG = (M + 16 * TB - 1) / (16 * TB);  // token groups (k_sweep)
@@ -2964,8 +3011,8 @@ static hipError_t launch_sweep_c(const void *W, int64_t rb, int N, int K, const 
     if (NW * 64 > (LB < 640 ? LB : 640) || SL < C || nblk < 1 || grid < S || (S > 1 && !part))
         return hipErrorInvalidValue;
     float *pp = S > 1 ? part : nullptr;
-    hipLaunchKernelGGL((k_sweep<C, TB, LB, EPI>), dim3(grid), dim3(NW * 64), lds, st, (const uint8_t *)W, rb, N, K,
-                       (const half8 *)x16, xs_inv, xsum, bias, y, M, aux, nblk, S, pp);
+    hipLaunchKernelGGL((k_sweep<C, TB, LB, EPI, QT>), dim3(grid), dim3(NW * 64), lds, st, (const uint8_t *)W, rb, N,
+                       K, (const half8 *)x16, xs_inv, xsum, bias, y, M, aux, nblk, S, pp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || S == 1) return e;
     const int64_t outs = (int64_t)M * (EPI == EPI_SWIGLU ? N / 2 : N);
@@ -2974,20 +3021,42 @@ static hipError_t launch_sweep_c(const void *W, int64_t rb, int N, int K, const 
     return hipGetLastError();
 }
 
-template <int EPI>
+template <int EPI, int QT = FH3K_Q4_K>
 static hipError_t launch_sweep_e(const void *W, int64_t rb, int N, int K, const void *x16, const float *xs_inv,
                                  const float *xsum, const float *bias, float *y, int M, const float *aux, float *part,
                                  hipStream_t st) {
+    constexpr int LB1 = QT == FH3K_Q6_K ? 512 : 768;  // one token block: see sweep_split
     if (sweep_groups(K / 256, M))
-        return launch_sweep_c<2, 2, 512, EPI>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
+        return launch_sweep_c<2, 2, 512, EPI, QT>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
     switch (sweep_tb(M)) {
-        case 1: return launch_sweep_c<2, 1, 768, EPI>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
-        case 2: return launch_sweep_c<1, 2, 768, EPI>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
+        case 1:
+            if (sweep_q6_one(K / 256, QT))
+                return launch_sweep_c<1, 1, 768, EPI, QT>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
+            return launch_sweep_c<2, 1, LB1, EPI, QT>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
+        case 2: return launch_sweep_c<1, 2, 768, EPI, QT>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
         // three or four token blocks: 96 / 128 VGPRs of activations, so at most
         // 8 wavefronts (two per SIMD, 256 VGPRs each)
-        case 3: return launch_sweep_c<1, 3, 512, EPI>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
-        default: return launch_sweep_c<1, 4, 512, EPI>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
+        case 3: return launch_sweep_c<1, 3, 512, EPI, QT>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
+        default: return launch_sweep_c<1, 4, 512, EPI, QT>(W, rb, N, K, x16, xs_inv, xsum, bias, y, M, aux, part, st);
     }
+}
+
+// Q6_K weights read in place by the sweep (no epilogue, no group sums).
+extern "C" int fh3k_sweep_q_takes(int type) { return type == FH3K_Q6_K; }
+
+extern "C" size_t fh3k_sweep_q_part_bytes(int type, int N, int K, int M) {
+    int S, SL;
+    if (!fh3k_sweep_q_takes(type) || !fh3k_sweep_fits(K, M) || N < 1) return 0;
+    sweep_split(K / 256, M, S, SL, type);
+    return S > 1 ? (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+extern "C" hipError_t fh3k_sweep_q(int type, const void *W, int64_t row_bytes, int N, int K, const void *x16,
+                                   const float *xs_inv, const float *bias, float *y, int M, float *part,
+                                   hipStream_t st) {
+    if (!fh3k_sweep_q_takes(type) || !fh3k_sweep_fits(K, M) || N < 1) return hipErrorInvalidValue;
+    return launch_sweep_e<EPI_NONE, FH3K_Q6_K>(W, row_bytes, N, K, x16, xs_inv, nullptr, bias, y, M, nullptr, part,
+                                                st);
 }
 
 extern "C" hipError_t fh3k_sweep_epi(const void *W, int64_t row_bytes, int N, int K, const void *x16,

@@ -1,6 +1,7 @@
 """GPU parity of the Q5_K and Q6_K weights read in place, by the small-M
-kernel (k_skinny with QT = Q5_K / Q6_K, up to 64 tokens) and by the GEMM
-(k_gemm with QT = Q5_K / Q6_K, above), through the C-ABI, against the CPU
+kernels (k_skinny with QT = Q5_K / Q6_K, and for Q6_K the sweep, k_sweep with
+QT = Q6_K, up to 64 tokens) and by the GEMM (k_gemm with QT = Q5_K / Q6_K,
+above), through the C-ABI, against the CPU
 oracle (fh3's fh3_matmul, src/core/fh3_ops.c:317-404, on the decoders of
 src/core/fh3_quant.c:198-282).
 
@@ -89,6 +90,28 @@ def test_native_vs_oracle(gpu, oracle, name, M, K, N, use_bias):
     assert np.isfinite(y).all()
     assert err <= TOL
     assert np.array_equal(y.view(np.uint32), _dev(gpu, raw, _tid(name), K, N, x, bias).view(np.uint32))
+
+
+@pytest.mark.parametrize("M,K,N,use_bias", CASES + [(4, 25600, 96, True), (17, 6144, 64, False)])
+def test_native_q6k_both_small_m_kernels(gpu, oracle, M, K, N, use_bias):
+    """Q6_K up to 64 tokens on each of its kernels (forced): the sweep (weights
+    in a ring, activations in registers, K slices past 16 super-blocks) and
+    k_skinny (K windows when the row blocks are few), against the oracle;
+    each bitwise repeatable."""
+    F = gpu
+    name = "Q6_K"
+    rng = np.random.default_rng(4409 + M * 131 + K + N)
+    raw = H.random_blocks(rng, name, N, K, scale_lo=-12, scale_hi=-8)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32) if use_bias else None
+    yo = _oracle(oracle, raw, name, K, N, x, bias)
+    for path in (F.PATH_SWEEP, F.PATH_SKINNY):
+        _say("q6k M=%d K=%d N=%d path=%d" % (M, K, N, path))
+        y = _dev(F, raw, _tid(name), K, N, x, bias, path=path)
+        err = H.rel_fro(y, yo)
+        _say("  rel_fro = %.3e" % err)
+        assert np.isfinite(y).all() and err <= TOL
+        assert np.array_equal(y.view(np.uint32), _dev(F, raw, _tid(name), K, N, x, bias, path=path).view(np.uint32))
 
 
 def _onehot_weights(rng, name, N, K):

@@ -321,8 +321,8 @@ def te_other_types(ev, st, R=64):
     down-projection 25600 -> 5120) and its Q5_K / Q6_K tensors (Q5_K 5120 ->
     1024; Q6_K 5120 -> 1024, 8192 -> 5120, 25600 -> 5120) at M = 1, 16, 64 and
     300 tokens through fh3_hip_matmul_dev (Q4_K: k_gemv8, k_sweep in K slices,
-    k_skinny or k_midm by shape, k_gemm at 300; Q5_K / Q6_K: k_skinny, in K
-    windows on the long rows, and k_gemm at 300, reading the blocks in place).  Q4_K weights are the seeded N(0, 0.02) encoding, the others random
+    k_skinny or k_midm by shape, k_gemm at 300; Q6_K: k_sweep, Q5_K: k_skinny,
+    and both k_gemm at 300, reading the blocks in place).  Q4_K weights are the seeded N(0, 0.02) encoding, the others random
     blocks with finite scales, all rotated over more than 256 MB of device
     copies; graph of R calls."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -357,7 +357,7 @@ def te_other_types(ev, st, R=64):
             g.launch()
             t_c = ev.time_ms(lambda i: g.launch(), 8, st) / R
             g.close()
-            path = F.matmul_path(M, K) if name == "Q4_K" else (F.PATH_SKINNY if M <= 64 else F.PATH_GEMM)
+            path = F.matmul_path(M, K) if name in ("Q4_K", "Q6_K") else (F.PATH_SKINNY if M <= 64 else F.PATH_GEMM)
             rows.append({"type": name, "M": M, "K": K, "N": N, "path": path, "call_us": round(t_c * 1e3, 2),
                          "weight_GBps": round(wb / (t_c * 1e-3) / 1e9, 1),
                          "hbm_frac": round((wb + 4 * M * (K + N)) / (t_c * 1e-3) / HBM_PEAK, 4)})

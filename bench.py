@@ -357,7 +357,8 @@ def te_other_types(ev, st, R=64):
             g.launch()
             t_c = ev.time_ms(lambda i: g.launch(), 8, st) / R
             g.close()
-            path = F.matmul_path(M, K) if name in ("Q4_K", "Q6_K") else (F.PATH_SKINNY if M <= 64 else F.PATH_GEMM)
+            small = F.PATH_SWEEP if name == "Q6_K" and (M <= 16 or K >= 5120) else F.PATH_SKINNY
+            path = F.matmul_path(M, K) if name == "Q4_K" else (small if M <= 64 else F.PATH_GEMM)
             rows.append({"type": name, "M": M, "K": K, "N": N, "path": path, "call_us": round(t_c * 1e3, 2),
                          "weight_GBps": round(wb / (t_c * 1e-3) / 1e9, 1),
                          "hbm_frac": round((wb + 4 * M * (K + N)) / (t_c * 1e-3) / HBM_PEAK, 4)})

@@ -30,9 +30,10 @@ Workloads (each launch sequence is preceded by one untimed warmup launch):
          benchmark runs it): fh3_hip_matmul_prepared_dev -> k_skinny
   q56    Q5_K and Q6_K weights read in place at the text encoder's shapes
          (Q5_K 5120 -> 1024, Q6_K 5120 -> 1024, 8192 -> 5120, 25600 -> 5120)
-         at M = 1, 16 and 300: fh3_hip_matmul_prepared_dev -> k_skinny<Q5_K /
-         Q6_K> (in K windows, then k_midm_sum, on the long rows) and k_gemm<TBW,
-         Q5_K / Q6_K> at 300; weights rotated as for gemv
+         at M = 1, 16 and 300: fh3_hip_matmul_prepared_dev -> k_sweep<Q6_K>
+         and k_skinny<Q5_K> (K slices / windows, then k_midm_sum, where they
+         split K) and k_gemm<TBW, Q5_K / Q6_K> at 300; weights rotated as for
+         gemv
   copy   hipMemcpy device-to-device of 256 MiB: a copy of known size that
          calibrates FETCH_SIZE / WRITE_SIZE against the bytes moved
   attn   the DiT attention branch at n = 16384 tokens, 40 heads of 128

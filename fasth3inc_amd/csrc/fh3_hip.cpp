@@ -617,12 +617,13 @@ static int product(const Fh3W *w, const void *prep, int n_tok, const float *bias
     if (w->type != FH3_QUANT_Q4_K || general_rows(w->in)) {
         std::lock_guard<std::recursive_mutex> lk(g.mu);
         if (choose_path(n_tok, w->in) == FH3_HIP_PATH_GEMV8) {
-            // the prepared form is then a copy of x: make the fragments here
+            // the prepared form is then a copy of x: make the fragments here,
+            // the rows the chosen kernel reads (as fh3_hip_matmul_dev does)
             int rc = grow(g.ws2, fh3_hip_prepared_bytes(n_tok, w->in), st);
             if (rc != FH3_OK) return rc;
             float *xs = (float *)prep_scales(g.ws2.p, n_tok, w->in);
-            FH3_HIPCALL(fh3k_xprep((const float *)prep, n_tok, (int)w->in, (int)prep_rows(n_tok), g.ws2.p, xs,
-                                   nullptr, st));
+            const int64_t rows = path16(n_tok, w->in) == FH3_HIP_PATH_SKINNY ? round_up(n_tok, 32) : prep_rows(n_tok);
+            FH3_HIPCALL(fh3k_xprep((const float *)prep, n_tok, (int)w->in, (int)rows, g.ws2.p, xs, nullptr, st));
             return product16(w, g.ws2.p, xs, n_tok, bias, d_y, st);
         }
         return product16(w, prep, prep_scales(prep, n_tok, w->in), n_tok, bias, d_y, st);

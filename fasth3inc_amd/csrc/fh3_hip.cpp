@@ -530,9 +530,10 @@ extern "C" int fh3_hip_prepare_x_dev(const float *d_x, int n_tok, int64_t in, vo
 
 // Weights of another type than Q4_K, and general rows of any type: Q5_K and
 // Q6_K rows of whole super-blocks are read in place, by k_skinny (Q6_K: the
-// sweep where it applies, q_sweep) up to 64 tokens and by k_gemm above; otherwise fp16 rows of kpad(in) columns (the
-// weight itself for F16 rows of whole super-blocks, else decoded, zero-padded,
-// into the library's w16 buffer), then k_skinny16 / k_gemm16.
+// sweep where it applies, q_sweep) up to 64 tokens and by k_gemm above;
+// otherwise fp16 rows of kpad(in) columns (the weight itself for F16 rows of
+// whole super-blocks, else decoded, zero-padded, into the library's w16
+// buffer), then k_skinny16 / k_gemm16.
 static bool reads_in_place_q(const Fh3W *w, int n_tok) {
     if (general_rows(w->in)) return false;
     return path16(n_tok, w->in) == FH3_HIP_PATH_SKINNY ? fh3k_skinny_q_takes(w->type) != 0

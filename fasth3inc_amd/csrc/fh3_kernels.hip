@@ -918,10 +918,12 @@ __device__ __forceinline__ half8 sk6_b(const SkRaw<FH3K_Q6_K> &r, int q, const S
     const uint32_t n1 = hi ? (u1 & 0xF0F0F0F0u) : ((u1 << 4) & 0xF0F0F0F0u);
     const uint32_t e0 = ((h0 >> hs) & 0x03030303u) | 0x64646464u, e1 = ((h1 >> hs) & 0x03030303u) | 0x64646464u;
     const half2v s = o.s16[(hi ? 2 : 0) + (part >> 1)], c = o.c96[(hi ? 2 : 0) + (part >> 1)];
-    const half2v p0 = __builtin_elementwise_fma(__builtin_bit_cast(half2v, __builtin_amdgcn_perm(e0, n0, 0x05010400u)), s, c);
-    const half2v p1 = __builtin_elementwise_fma(__builtin_bit_cast(half2v, __builtin_amdgcn_perm(e0, n0, 0x07030602u)), s, c);
-    const half2v p2 = __builtin_elementwise_fma(__builtin_bit_cast(half2v, __builtin_amdgcn_perm(e1, n1, 0x05010400u)), s, c);
-    const half2v p3 = __builtin_elementwise_fma(__builtin_bit_cast(half2v, __builtin_amdgcn_perm(e1, n1, 0x07030602u)), s, c);
+    // pair (2i, 2i + 1) of a word: bytes [n.b2i, e.b2i, n.b2i+1, e.b2i+1]
+    auto pair = [&](uint32_t e, uint32_t n, uint32_t sel) {
+        return __builtin_elementwise_fma(__builtin_bit_cast(half2v, __builtin_amdgcn_perm(e, n, sel)), s, c);
+    };
+    const half2v p0 = pair(e0, n0, 0x05010400u), p1 = pair(e0, n0, 0x07030602u);
+    const half2v p2 = pair(e1, n1, 0x05010400u), p3 = pair(e1, n1, 0x07030602u);
     return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
@@ -2789,7 +2791,8 @@ static int device_cus(void) {
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
     if (!cus[dev]) {
         int n = 0;
-        cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+        const bool ok = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess;
+        cus[dev] = ok && n > 0 ? n : 256;
     }
     return cus[dev];
 }
@@ -2832,13 +2835,16 @@ static hipError_t launch_skinny_q(const void *W, int64_t rb, int N, int K, const
     skinny_kwin(N, K, L, S);
     if (S > 1 && !part) return hipErrorInvalidValue;
     hipError_t e;
+#define FH3_SKINNY_Q(tb)                                                                                          \
+    case tb: e = launch_skinny<tb, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st, L, S, part); break
     switch ((M + 15) / 16) {
-        case 1: e = launch_skinny<1, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st, L, S, part); break;
-        case 2: e = launch_skinny<2, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st, L, S, part); break;
-        case 3: e = launch_skinny<3, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st, L, S, part); break;
-        case 4: e = launch_skinny<4, QT>(W, rb, N, K, x16, xs_inv, bias, y, M, EPI_NONE, nullptr, st, L, S, part); break;
+        FH3_SKINNY_Q(1);
+        FH3_SKINNY_Q(2);
+        FH3_SKINNY_Q(3);
+        FH3_SKINNY_Q(4);
         default: return hipErrorInvalidValue;
     }
+#undef FH3_SKINNY_Q
     if (e != hipSuccess || S == 1) return e;
     const int64_t outs = (int64_t)M * N;
     hipLaunchKernelGGL(k_midm_sum, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, st, part, S, M, N, xs_inv,

@@ -1295,16 +1295,16 @@ __global__ __launch_bounds__(LB) void k_sweep(const uint8_t *__restrict__ W, int
 
     // the output this thread stores after each block, if any: lane st_l of
     // the 16x16 result holds column st_l % 16 and tokens 4 (st_l / 16) + v.
-    // The four storing wavefronts (one per v) are 2, 3, 6 and 7 when there
-    // are eight or more: waves w and w + 4 share a SIMD, so with ten the
-    // stores go to the two SIMDs that hold two wavefronts instead of three,
-    // off the path to the next barrier (16 tokens, N = 17408: 16.7-17.0
+    // The four storing wavefronts (one per v) are 0-3, one per SIMD, except
+    // with ten: waves w and w + 4 share a SIMD, so ten put three on SIMDs 0
+    // and 1 and two on SIMDs 2 and 3, and the stores go to waves 2, 3, 6 and
+    // 7, off the path to the next barrier (16 tokens, N = 17408: 16.7-17.0
     // against 17.3-17.5 us; the same bits).  With fewer than four wavefronts
     // (in <= 1536), or two token blocks, the threads of the workgroup take the
     // TB x 256 outputs in turn (st_all).
     const bool st_all = blockDim.x < 256 || part || TB > 1;
     const int sw = (int)threadIdx.x >> 6;
-    const int st_v = NW >= 8 ? (sw == 2 ? 0 : sw == 3 ? 1 : sw == 6 ? 2 : sw == 7 ? 3 : -1) : (sw < 4 ? sw : -1);
+    const int st_v = NW == 10 ? (sw == 2 ? 0 : sw == 3 ? 1 : sw == 6 ? 2 : sw == 7 ? 3 : -1) : (sw < 4 ? sw : -1);
     const int st_l = (int)threadIdx.x & 63;
     const int st_t = t0 + 4 * (st_l >> 4) + (st_v < 0 ? 0 : st_v), st_j = st_l & 15;
     const bool storer = !st_all && st_v >= 0 && st_t < M && (EPI != EPI_SWIGLU || st_j < 8);

@@ -92,7 +92,10 @@ def test_native_vs_oracle(gpu, oracle, name, M, K, N, use_bias):
     assert np.array_equal(y.view(np.uint32), _dev(gpu, raw, _tid(name), K, N, x, bias).view(np.uint32))
 
 
-@pytest.mark.parametrize("M,K,N,use_bias", CASES + [(4, 25600, 96, True), (17, 6144, 64, False)])
+# plus the sweep's shortest row (two super-blocks), slices with a short last
+# one (54 super-blocks in slices of 10), a long row at one token
+@pytest.mark.parametrize("M,K,N,use_bias", CASES + [(4, 25600, 96, True), (17, 6144, 64, False), (2, 512, 40, True),
+                                                    (16, 13824, 64, False)])
 def test_native_q6k_both_small_m_kernels(gpu, oracle, M, K, N, use_bias):
     """Q6_K up to 64 tokens on each of its kernels (forced): the sweep (weights
     in a ring, activations in registers, K slices past 16 super-blocks) and

@@ -4,7 +4,8 @@
     python -m fasth3inc_amd.build --check  # also print kernel resource usage
 
 C99 host files are compiled with gcc (-std=gnu99, OpenMP), HIP sources with
-hipcc for gfx950 only, and linked into fasth3inc_amd/lib/libfh3hip.so.  The
+hipcc for gfx950 only, and linked into fasth3inc_amd/lib/libfh3hip.so; the
+matrix-core calibration program goes to fasth3inc_amd/lib/fh3_mfma_peak.  The
 oracle (oracle/libfh3_oracle.so) and, when the reference tree is present, the
 reference build (oracle/_ref/libfh3_ref.so) are made by oracle/Makefile.
 """
@@ -82,6 +83,18 @@ def build_lib(check=False, quiet=False):
     return LIB
 
 
+MFMA_PEAK_SRC = os.path.join(CSRC, "fh3_mfma_peak.hip")
+MFMA_PEAK = os.path.join(LIBDIR, "fh3_mfma_peak")
+
+
+def build_mfma_peak(quiet=False):
+    """The matrix-core calibration program (fp16 / bf16 / int8 MFMA rates and
+    the clock they imply), which the profiles quote beside the kernels."""
+    os.makedirs(LIBDIR, exist_ok=True)
+    _run([HIPCC] + HIP_FLAGS + [MFMA_PEAK_SRC, "-o", MFMA_PEAK], quiet)
+    return MFMA_PEAK
+
+
 C_CALLER_SRC = os.path.join(ROOT, "tests", "c", "fh3_c_caller.c")
 C_CALLER = os.path.join(ROOT, "tests", "c", "fh3_c_caller")
 
@@ -100,6 +113,7 @@ def build(check=False, quiet=False):
     build_oracle(quiet)
     lib = build_lib(check, quiet)
     build_c_caller(quiet)
+    build_mfma_peak(quiet)
     return lib
 
 

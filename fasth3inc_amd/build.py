@@ -5,7 +5,7 @@
 
 C99 host files are compiled with gcc (-std=gnu99, OpenMP), HIP sources with
 hipcc for gfx950 only, and linked into fasth3inc_amd/lib/libfh3hip.so; the
-matrix-core calibration program goes to fasth3inc_amd/lib/fh3_mfma_peak.  The
+calibration program (MFMA and HBM rates) goes to fasth3inc_amd/lib/fh3_calib.  The
 oracle (oracle/libfh3_oracle.so) and, when the reference tree is present, the
 reference build (oracle/_ref/libfh3_ref.so) are made by oracle/Makefile.
 """
@@ -83,16 +83,17 @@ def build_lib(check=False, quiet=False):
     return LIB
 
 
-MFMA_PEAK_SRC = os.path.join(CSRC, "fh3_mfma_peak.hip")
-MFMA_PEAK = os.path.join(LIBDIR, "fh3_mfma_peak")
+CALIB_SRC = os.path.join(CSRC, "fh3_calib.hip")
+CALIB = os.path.join(LIBDIR, "fh3_calib")
 
 
-def build_mfma_peak(quiet=False):
-    """The matrix-core calibration program (fp16 / bf16 / int8 MFMA rates and
-    the clock they imply), which the profiles quote beside the kernels."""
+def build_calib(quiet=False):
+    """The calibration program (fp16 / bf16 / int8 MFMA rates and the clock
+    they imply; the load-only HBM stream), which the profiles quote beside the
+    kernels."""
     os.makedirs(LIBDIR, exist_ok=True)
-    _run([HIPCC] + HIP_FLAGS + [MFMA_PEAK_SRC, "-o", MFMA_PEAK], quiet)
-    return MFMA_PEAK
+    _run([HIPCC] + HIP_FLAGS + [CALIB_SRC, "-o", CALIB], quiet)
+    return CALIB
 
 
 C_CALLER_SRC = os.path.join(ROOT, "tests", "c", "fh3_c_caller.c")
@@ -113,7 +114,7 @@ def build(check=False, quiet=False):
     build_oracle(quiet)
     lib = build_lib(check, quiet)
     build_c_caller(quiet)
-    build_mfma_peak(quiet)
+    build_calib(quiet)
     return lib
 
 

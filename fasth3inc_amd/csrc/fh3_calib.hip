@@ -1,27 +1,39 @@
-// fh3_mfma_peak.hip -- matrix-core calibration for the rooflines of the
-// product kernels.
+// fh3_calib.hip -- calibration of the rooflines the product kernels are
+// measured against: what the matrix cores and HBM sustain on this GPU.
 //
-// Every SIMD of the chip issues back-to-back MFMAs of one kind (the kinds the
-// kernels use: fp16 32x32x16 in k_gemm and the attention, fp16 16x16x32 in
-// k_skinny / k_sweep, int8 16x16x64 in k_gemv8; bf16 32x32x16 for the bf16
-// figure), on register operands, in independent accumulator chains (each
-// chain's next MFMA issues 128 or more clocks after its last), with no memory
-// traffic but one store per wavefront at the end.  One workgroup per CU (its
-// LDS request leaves room for no second one), 4 or 8 wavefronts.  Prints the
-// rate of each kind against the published dense peak (fp16 / bf16 2.5 PFLOP/s,
-// int8 5.0 POP/s, both at a 2.4 GHz clock) and the clock the rate implies at
-// a fully busy matrix pipe: measured / peak * 2.4 GHz.
+// mfma: every SIMD of the chip issues back-to-back MFMAs of one kind (the
+// kinds the kernels use: fp16 32x32x16 in k_gemm and the attention, fp16
+// 16x16x32 in k_skinny / k_sweep, int8 16x16x64 in k_gemv8; bf16 32x32x16 for
+// the bf16 figure), on register operands, in independent accumulator chains
+// (each chain's next MFMA issues 128 or more clocks after its last), with no
+// memory traffic but one store per wavefront at the end.  One workgroup per
+// CU (its LDS request leaves room for no second one), 4 or 8 wavefronts.
+// Prints the rate of each kind against the published dense peak (fp16 / bf16
+// 2.5 PFLOP/s, int8 5.0 POP/s, both at a 2.4 GHz clock) and the clock the
+// rate implies at a fully busy matrix pipe: measured / peak * 2.4 GHz.
 //
-//   fasth3inc_amd/lib/fh3_mfma_peak [iterations]   (default 20000 per launch)
+// hbm: one launch reads a contiguous run of S bytes with 16-byte loads and
+// keeps nothing (a load-only stream), S = the Q4_K weights of the GEMV shapes
+// (5120 x 5120: 14,745,600 B; 17408 x 5120: 50,135,040 B), 256 MiB and 1 GiB;
+// successive launches read successive runs of a 2 GiB buffer, so no launch
+// finds its bytes in the 256 MB Infinity Cache.  Prints the mean time per
+// launch and the rate against the published 8 TB/s: the shortest time one
+// launch needs to stream a weight matrix of that size.
+//
+//   fasth3inc_amd/lib/fh3_calib [mfma|hbm|all] [iterations]
+//   (iterations: MFMA loop trips per launch, default 20000)
 #include <hip/hip_runtime.h>
 #include <stdio.h>
+#include <stdint.h>
 #include <stdlib.h>
+#include <string.h>
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 enum { K_F16_32 = 0, K_F16_16 = 1, K_BF16_32 = 2, K_I8_16 = 3, NKIND = 4 };
 
@@ -93,6 +105,24 @@ __global__ __launch_bounds__(512) void k_mfma_loop(int iters, float *__restrict_
     if (lane == 0) out[blockIdx.x * 8 + (threadIdx.x >> 6)] = s;
 }
 
+// Load-only stream over n16 16-byte pieces: grid-stride, eight loads in flight
+// per thread; the XOR of everything read is stored only if it equals a value
+// the zero-filled buffer cannot give (so the loads are not dead code).
+__global__ __launch_bounds__(512) void k_hbm_stream(const u32x4 *__restrict__ p, size_t n16, u32x4 *__restrict__ out) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    for (; i + 7 * stride < n16; i += 8 * stride) {
+        u32x4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = p[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc ^= v[u];
+    }
+    for (; i < n16; i += stride) acc ^= p[i];
+    if (acc.x == 0x9E3779B9u && acc.y == 0x7F4A7C15u) out[0] = acc;
+}
+
 struct Kind {
     const char *name;
     double ops_per_inst;   // 2 * m * n * k
@@ -101,14 +131,7 @@ struct Kind {
     void (*kern)(int, float *);
 };
 
-int main(int argc, char **argv) {
-    const int iters = argc > 1 ? atoi(argv[1]) : 20000;
-    if (iters < 1 || iters > 10000000) {
-        fprintf(stderr, "iterations must be in 1..10000000\n");
-        return 2;
-    }
-    hipDeviceProp_t prop;
-    CK(hipGetDeviceProperties(&prop, 0));
+static void run_mfma(const hipDeviceProp_t &prop, int iters) {
     const int cus = prop.multiProcessorCount;
     // more than half the CU's LDS: one workgroup per CU
     const size_t lds = prop.sharedMemPerMultiprocessor / 2 + 1024;
@@ -151,5 +174,68 @@ int main(int argc, char **argv) {
         }
     }
     CK(hipFree(out));
+    CK(hipEventDestroy(a));
+    CK(hipEventDestroy(b));
+}
+
+static void run_hbm(const hipDeviceProp_t &prop) {
+    const int cus = prop.multiProcessorCount;
+    const size_t region = (size_t)2 << 30;
+    uint8_t *buf;
+    u32x4 *out;
+    CK(hipMalloc(&buf, region));
+    CK(hipMemset(buf, 0, region));
+    CK(hipMalloc(&out, sizeof(u32x4)));
+    hipEvent_t a, b;
+    CK(hipEventCreate(&a));
+    CK(hipEventCreate(&b));
+    const size_t sizes[] = {14745600, 50135040, (size_t)256 << 20, (size_t)1 << 30};
+    printf("%s: %d CUs, load-only stream, runs rotated over %zu MiB\n", prop.gcnArchName, cus, region >> 20);
+    for (size_t bytes : sizes) {
+        // successive runs at successive 4 KiB-aligned offsets, every run inside the region
+        const size_t step = (bytes + 4095) & ~(size_t)4095;
+        const size_t nrun = region / step;
+        for (int wpc : {1, 2, 4}) {
+            const unsigned grid = (unsigned)(cus * wpc);
+            size_t run = 0;
+            auto launch = [&]() {
+                const u32x4 *p = (const u32x4 *)(buf + (run % nrun) * step);
+                run++;
+                hipLaunchKernelGGL(k_hbm_stream, dim3(grid), dim3(512), 0, 0, p, bytes / 16, out);
+            };
+            launch();
+            CK(hipGetLastError());
+            CK(hipDeviceSynchronize());
+            const int reps = bytes >= ((size_t)256 << 20) ? 8 : 40;
+            CK(hipEventRecord(a, 0));
+            for (int r = 0; r < reps; r++) launch();
+            CK(hipEventRecord(b, 0));
+            CK(hipEventSynchronize(b));
+            CK(hipGetLastError());
+            float ms = 0.f;
+            CK(hipEventElapsedTime(&ms, a, b));
+            const double sec = (double)ms * 1e-3 / reps;
+            printf("%11zu B, %4u workgroups of 512: %9.2f us per launch, %7.1f GB/s, %.3f of 8 TB/s\n", bytes, grid,
+                   sec * 1e6, bytes / sec * 1e-9, bytes / sec / 8e12);
+        }
+    }
+    CK(hipFree(buf));
+    CK(hipFree(out));
+    CK(hipEventDestroy(a));
+    CK(hipEventDestroy(b));
+}
+
+int main(int argc, char **argv) {
+    const char *mode = argc > 1 ? argv[1] : "all";
+    const int iters = argc > 2 ? atoi(argv[2]) : 20000;
+    const bool m = !strcmp(mode, "mfma") || !strcmp(mode, "all"), h = !strcmp(mode, "hbm") || !strcmp(mode, "all");
+    if ((!m && !h) || iters < 1 || iters > 10000000) {
+        fprintf(stderr, "usage: fh3_calib [mfma|hbm|all] [iterations 1..10000000]\n");
+        return 2;
+    }
+    hipDeviceProp_t prop;
+    CK(hipGetDeviceProperties(&prop, 0));
+    if (m) run_mfma(prop, iters);
+    if (h) run_hbm(prop);
     return 0;
 }

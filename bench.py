@@ -21,6 +21,7 @@ import ctypes
 import json
 import os
 import platform
+import re
 import subprocess
 import sys
 import time
@@ -462,6 +463,35 @@ def _time_cpu(H, lib, fn, raw, K, N, x, iters):
     return min(ts), sum(ts) / len(ts)
 
 
+CALIB = os.path.join(ROOT, "fasth3inc_amd", "lib", "fh3_calib")
+
+
+def load_only_ceiling(wbytes, k_bytes, k_time_ms):
+    """The least time one-launch kernels need for the step's weights on this
+    GPU: the calibration program (a child process on the same GPU, after the
+    timed GEMV work) streams each GEMV weight matrix with load-only kernels of
+    two load forms and three grid sizes, weights rotated past the Infinity
+    Cache, and reports the best mean time per launch; summed over the step's
+    shapes.  None when the program is not built."""
+    if not os.path.exists(CALIB):
+        return None
+    r = subprocess.run([CALIB, "gemv"], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=120)
+    if r.returncode != 0:
+        return {"error": r.stdout[-400:]}
+    best = {int(m.group(1)): float(m.group(2))
+            for m in re.finditer(r"^\s*(\d+) B best:\s+([\d.]+) us", r.stdout, re.M)}
+    if any(b not in best for b in wbytes):
+        return {"error": "no stream time for every weight size: " + r.stdout[-400:]}
+    us = sum(best[b] for b in wbytes)
+    return {"us_per_step": round(us, 2),
+            "alg_GBps": round(k_bytes / (us * 1e-6) / 1e9, 1),
+            "frac": round(k_bytes / (us * 1e-6) / HBM_PEAK, 4),
+            "kernels_over_ceiling": round(k_time_ms * 1e3 / us, 3),
+            "best_us_per_launch": {str(b): t for b, t in sorted(best.items())},
+            "source": "fasth3inc_amd/lib/fh3_calib gemv: load-only stream per weight matrix, best of 8 or 1 "
+                      "loads per trip at 256/512/1024 workgroups, mean of 40 back-to-back launches"}
+
+
 def cpu_baseline(cases, iters=5, big_iters=2, sample_tokens=(128, 512)):
     """fh3's CPU matmul on this host's cores, as benchmarks/bench_matmul.c
     times it (1 warmup, then best and mean of N runs): the six GEMV shapes and
@@ -624,6 +654,14 @@ def main():
                 "kernel": "k_gemv8 (n_tok<=4) and k_sweep (n_tok<=16), fh3_hip_matmul_prepared_dev",
                 "note": "algorithmic bytes N*K/256*144 + 4MK + 4MN per launch over the mean launch time "
                         "(graph of 64 back-to-back launches, rotating weight copies) of the six shapes"}
+
+    try:
+        roofline["load_only_ceiling"] = load_only_ceiling([c.wbytes for c in gemv], k_bytes, k_time)
+    except Exception as e:  # the calibration is context, not the measurement
+        roofline["load_only_ceiling"] = {"error": repr(e)}
+    if roofline["load_only_ceiling"] and "us_per_step" in roofline["load_only_ceiling"]:
+        log("[bench] load-only ceiling of the six weight matrices: %.2f us per step (kernels %.2fx)" % (
+            roofline["load_only_ceiling"]["us_per_step"], roofline["load_only_ceiling"]["kernels_over_ceiling"]))
 
     cpu = None if args.no_cpu else cpu_baseline(gemv)
     if cpu:

@@ -21,8 +21,9 @@
 // launch and the rate against the published 8 TB/s: the shortest time one
 // launch needs to stream a weight matrix of that size.
 //
-//   fasth3inc_amd/lib/fh3_calib [mfma|hbm|all] [iterations]
-//   (iterations: MFMA loop trips per launch, default 20000)
+//   fasth3inc_amd/lib/fh3_calib [mfma|hbm|gemv|all] [iterations]
+//   (gemv: the hbm mode at the two GEMV weight sizes only; iterations: MFMA
+//   loop trips per launch, default 20000)
 #include <hip/hip_runtime.h>
 #include <stdio.h>
 #include <stdint.h>
@@ -181,7 +182,7 @@ static void run_mfma(const hipDeviceProp_t &prop, int iters) {
     CK(hipEventDestroy(b));
 }
 
-static void run_hbm(const hipDeviceProp_t &prop) {
+static void run_hbm(const hipDeviceProp_t &prop, bool gemv_only) {
     const int cus = prop.multiProcessorCount;
     const size_t region = (size_t)2 << 30;
     uint8_t *buf;
@@ -192,9 +193,11 @@ static void run_hbm(const hipDeviceProp_t &prop) {
     hipEvent_t a, b;
     CK(hipEventCreate(&a));
     CK(hipEventCreate(&b));
-    const size_t sizes[] = {14745600, 50135040, (size_t)256 << 20, (size_t)1 << 30};
+    const size_t all_sizes[] = {14745600, 50135040, (size_t)256 << 20, (size_t)1 << 30};
+    const int nsizes = gemv_only ? 2 : 4;
     printf("%s: %d CUs, load-only stream, runs rotated over %zu MiB\n", prop.gcnArchName, cus, region >> 20);
-    for (size_t bytes : sizes) {
+    for (int si = 0; si < nsizes; si++) {
+        const size_t bytes = all_sizes[si];
         // successive runs at successive 4 KiB-aligned offsets, every run inside the region
         const size_t step = (bytes + 4095) & ~(size_t)4095;
         const size_t nrun = region / step;
@@ -239,14 +242,15 @@ static void run_hbm(const hipDeviceProp_t &prop) {
 int main(int argc, char **argv) {
     const char *mode = argc > 1 ? argv[1] : "all";
     const int iters = argc > 2 ? atoi(argv[2]) : 20000;
+    const bool g = !strcmp(mode, "gemv");
     const bool m = !strcmp(mode, "mfma") || !strcmp(mode, "all"), h = !strcmp(mode, "hbm") || !strcmp(mode, "all");
-    if ((!m && !h) || iters < 1 || iters > 10000000) {
-        fprintf(stderr, "usage: fh3_calib [mfma|hbm|all] [iterations 1..10000000]\n");
+    if ((!m && !h && !g) || iters < 1 || iters > 10000000) {
+        fprintf(stderr, "usage: fh3_calib [mfma|hbm|gemv|all] [iterations 1..10000000]\n");
         return 2;
     }
     hipDeviceProp_t prop;
     CK(hipGetDeviceProperties(&prop, 0));
     if (m) run_mfma(prop, iters);
-    if (h) run_hbm(prop);
+    if (h || g) run_hbm(prop, g);
     return 0;
 }

@@ -69,13 +69,15 @@ int fh3_hip_dequant_dev(int type, const void *d_src, float *d_dst, int64_t rows,
  * fp16 with a per-row power-of-two scale and weights enter an fp16 MFMA (exact
  * sc*q for n_tok <= 64, dequantised in fp32 and rounded once to fp16 above),
  * with fp32 accumulation.  Deterministic: no atomics, fixed reduction order.
- * Non-finite activations give NaN outputs for that token on the GEMV8 path.
+ * A NaN or infinity in a token's activations makes every output of that
+ * token non-finite (NaN on the GEMV8 path), as in the reference, and leaves
+ * the other tokens' outputs as they would be without it.
  * Except on the GEMV8 path, uses a library-owned workspace of about
  * n_tok * in * 2 bytes, plus S * n_tok * out * 4 bytes of partial sums where
  * K is split (the FH3_HIP_PATH_MIDM path, S <= in / 512; the GEMM path when
  * its 256 x 128 tiles number fewer than about 512, S <= in / 512 and
- * S * tiles <= 4096); calls that overlap on different streams race on it.  Q4_K products of more than 64 tokens need
- * out * row_bytes < 2^32 (32-bit row offsets; 7.6e9 weights). */
+ * S * tiles <= 4096); calls that overlap on different streams race on it.  Q4_K, Q5_K and Q6_K products of more than 64
+ * tokens need out * row_bytes < 2^32 (32-bit row offsets; 7.6e9 Q4_K weights). */
 int fh3_hip_matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok,
                        const float *d_bias_or_null, void *stream);
 

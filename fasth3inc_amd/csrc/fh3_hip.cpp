@@ -660,10 +660,27 @@ static int product(const Fh3W *w, const void *prep, int n_tok, const float *bias
     return FH3_OK;
 }
 
+// k_gemm addresses its weight matrix with 32-bit byte offsets (buffer
+// resources): the Q4_K / Q5_K / Q6_K products it runs, above 64 tokens, need
+// out * row_bytes < 2^32.  Refused before any work is enqueued.
+static int check_gemm_span(const Fh3W *w, int n_tok, const char *fn) {
+    if (general_rows(w->in)) return FH3_OK;
+    const bool gemm = w->type == FH3_QUANT_Q4_K
+                          ? choose_path(n_tok, w->in) == FH3_HIP_PATH_GEMM
+                          : reads_in_place_q(w, n_tok) && path16(n_tok, w->in) != FH3_HIP_PATH_SKINNY;
+    const uint64_t span = (uint64_t)w->out * (uint64_t)fh3_row_bytes(w->type, w->in);
+    if (gemm && span >= (1ull << 32))
+        return set_err(FH3_E_INVALID, "%s: n_tok=%d with out * row_bytes = %llu bytes of weights; products of more "
+                                      "than 64 tokens take less than 2^32 bytes (32-bit row offsets)",
+                       fn, n_tok, (unsigned long long)span);
+    return FH3_OK;
+}
+
 extern "C" int fh3_hip_matmul_prepared_dev(const Fh3W *w, const void *d_prep, float *d_y, int n_tok,
                                            const float *d_bias_or_null, void *stream) {
     int rc = check_weights(w, "fh3_hip_matmul_prepared_dev");
     if (rc != FH3_OK) return rc;
+    if (n_tok > 0 && (rc = check_gemm_span(w, n_tok, "fh3_hip_matmul_prepared_dev")) != FH3_OK) return rc;
     if (!d_prep || !d_y || n_tok <= 0)
         return set_err(FH3_E_INVALID, "fh3_hip_matmul_prepared_dev: NULL pointer or n_tok <= 0");
     if ((uintptr_t)d_prep & 15u)
@@ -694,6 +711,7 @@ static int matmul_dev(const Fh3W *w, const float *d_x, float *d_y, int n_tok, co
     if ((rc = check_epi(w, epi, aux, fn)) != FH3_OK) return rc;
     if (!d_x || !d_y || n_tok <= 0)
         return set_err(FH3_E_INVALID, "%s: NULL pointer or n_tok <= 0", fn);
+    if ((rc = check_gemm_span(w, n_tok, fn)) != FH3_OK) return rc;
     if ((uintptr_t)d_x & 15u) return set_err(FH3_E_INVALID, "%s: x must be 16-byte aligned", fn);
     rc = ensure_init();
     if (rc != FH3_OK) return rc;
@@ -744,6 +762,7 @@ extern "C" int fh3_hip_matmul_prepared_epi_dev(const Fh3W *w, const void *d_prep
     if (rc != FH3_OK) return rc;
     if ((rc = check_epi(w, epi, d_aux, fn)) != FH3_OK) return rc;
     if (!d_prep || !d_out || n_tok <= 0) return set_err(FH3_E_INVALID, "%s: NULL pointer or n_tok <= 0", fn);
+    if ((rc = check_gemm_span(w, n_tok, fn)) != FH3_OK) return rc;
     if ((uintptr_t)d_prep & 15u) return set_err(FH3_E_INVALID, "%s: prepared buffer must be 16-byte aligned", fn);
     rc = ensure_init();
     if (rc != FH3_OK) return rc;
@@ -777,6 +796,7 @@ extern "C" int fh3_hip_matmul_noalloc_dev(const Fh3W *w, const float *d_x, float
                        (long long)w->in, fh3k_max_in());
     if (!d_x || !d_y || n_tok <= 0) return set_err(FH3_E_INVALID, "%s: NULL pointer or n_tok <= 0", fn);
     if ((uintptr_t)d_x & 15u) return set_err(FH3_E_INVALID, "%s: x must be 16-byte aligned", fn);
+    if ((rc = check_gemm_span(w, n_tok, fn)) != FH3_OK) return rc;
     if (!g.init || !g_scratch[g.device])
         return set_err(FH3_E_INVALID, "%s: call fh3_hip_init first (it binds the scratch memory)", fn);
     hipStream_t st = stream ? (hipStream_t)stream : g.stream;

@@ -61,6 +61,10 @@ State g;
 thread_local char g_err[512] = "";
 // Set on a thread between fh3_hip_graph_begin and fh3_hip_graph_end.
 thread_local bool t_own_capture = false;
+// fh3_hip_free calls made on that thread meanwhile: a hipFree there would end
+// the (thread-local) capture with an error, so they wait for
+// fh3_hip_graph_end.
+thread_local std::vector<void *> t_deferred_free;
 // Device address of the fixed scratch array of fh3_kernels.hip, per device
 // (bound once per device by fh3_hip_init).
 void *g_scratch[64];
@@ -325,6 +329,10 @@ extern "C" int fh3_hip_malloc(void **dptr, size_t bytes) {
 
 extern "C" int fh3_hip_free(void *dptr) {
     if (!dptr) return FH3_OK;
+    if (t_own_capture) {
+        t_deferred_free.push_back(dptr);
+        return FH3_OK;
+    }
     FH3_HIPCALL(hipFree(dptr));
     return FH3_OK;
 }
@@ -377,7 +385,10 @@ extern "C" int fh3_hip_graph_end(void *stream, void **graph_exec) {
     if (!graph_exec) return set_err(FH3_E_INVALID, "fh3_hip_graph_end: NULL out pointer");
     hipGraph_t graph = nullptr;
     t_own_capture = false;
-    FH3_HIPCALL(hipStreamEndCapture(stream ? (hipStream_t)stream : g.stream, &graph));
+    const hipError_t ec = hipStreamEndCapture(stream ? (hipStream_t)stream : g.stream, &graph);
+    for (void *p : t_deferred_free) (void)hipFree(p);
+    t_deferred_free.clear();
+    if (ec != hipSuccess) return hip_fail(ec, "hipStreamEndCapture");
     hipGraphExec_t exec = nullptr;
     hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);

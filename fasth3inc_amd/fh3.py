@@ -8,6 +8,7 @@ this module computes on the CPU: if the library or a GPU is missing, calls
 raise.
 """
 import ctypes
+import gc
 import os
 
 import numpy as np
@@ -530,17 +531,28 @@ class Graph:
 
 
 def capture(fn, stream_ptr=None):
-    """Capture the fh3_hip_* work fn() enqueues on the stream into a Graph."""
-    _check(lib().fh3_hip_graph_begin(stream_ptr), "fh3_hip_graph_begin")
-    ex = ctypes.c_void_p()
+    """Capture the fh3_hip_* work fn() enqueues on the stream into a Graph.
+
+    The garbage collector is run first and paused while fn() records: a
+    collection inside the capture could run a DeviceBuffer's or Graph's
+    __del__ there, and destroying a graph during a capture ends it."""
+    gc.collect()
+    was_enabled = gc.isenabled()
+    gc.disable()
     try:
-        fn()
-    except BaseException:
-        # end the capture; the partial graph is of no use
-        if lib().fh3_hip_graph_end(stream_ptr, ctypes.byref(ex)) == FH3_OK:
-            lib().fh3_hip_graph_destroy(ex.value)
-        raise
-    _check(lib().fh3_hip_graph_end(stream_ptr, ctypes.byref(ex)), "fh3_hip_graph_end")
+        _check(lib().fh3_hip_graph_begin(stream_ptr), "fh3_hip_graph_begin")
+        ex = ctypes.c_void_p()
+        try:
+            fn()
+        except BaseException:
+            # end the capture; the partial graph is of no use
+            if lib().fh3_hip_graph_end(stream_ptr, ctypes.byref(ex)) == FH3_OK:
+                lib().fh3_hip_graph_destroy(ex.value)
+            raise
+        _check(lib().fh3_hip_graph_end(stream_ptr, ctypes.byref(ex)), "fh3_hip_graph_end")
+    finally:
+        if was_enabled:
+            gc.enable()
     return Graph(ex.value)
 
 

@@ -31,7 +31,9 @@ const char *fh3_hip_last_error(void);
 /* The library's compute stream (a hipStream_t) after initialisation, else NULL. */
 void *fh3_hip_stream(void);
 
-/* Device memory helpers (synchronous). */
+/* Device memory helpers (synchronous).  fh3_hip_free called on a thread
+ * between fh3_hip_graph_begin and fh3_hip_graph_end is carried out by
+ * fh3_hip_graph_end (a free during the capture would end it with an error). */
 int fh3_hip_malloc(void **dptr, size_t bytes);
 int fh3_hip_free(void *dptr);
 int fh3_hip_memcpy_htod(void *dst, const void *src, size_t bytes);

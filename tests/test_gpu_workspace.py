@@ -117,3 +117,41 @@ def test_first_capture_of_unprepared_product_refused(fresh):
             assert np.array_equal(_bits(dy.download(np.float32, (M, N))), _bits(want)), rep
     finally:
         g.close()
+
+
+def test_free_inside_capture_is_deferred(gpu):
+    """fh3_hip_free on the capturing thread between fh3_hip_graph_begin and
+    fh3_hip_graph_end (here an explicit close; in Python also a collected
+    DeviceBuffer) is carried out at fh3_hip_graph_end: the capture survives,
+    and every replay equals the eager products."""
+    F = gpu
+    K, N, M = 2048, 640, 24
+    print("case: free inside a capture, M=%d K=%d N=%d" % (M, K, N), flush=True)
+    dw = _weights(F, K, N, 11)
+    dx = F.DeviceBuffer.from_array(F.synth_x("normal", 11, 1, M, K))
+    want = F.DeviceBuffer(M * N * 4)
+    F.matmul_dev(dw, K, N, dx, want, M)          # eager first: the workspace exists
+    F.synchronize()
+    ref = want.download(np.float32, (M, N))
+    dy, dy2 = F.DeviceBuffer(M * N * 4), F.DeviceBuffer(M * N * 4)
+    spare = F.DeviceBuffer(1 << 20)
+
+    def body():
+        F.matmul_dev(dw, K, N, dx, dy, M)
+        spare.close()
+        F.matmul_dev(dw, K, N, dx, dy2, M)
+
+    g = F.capture(body)
+    try:
+        for rep in range(3):
+            dy.fill(0)
+            dy2.fill(0)
+            F.synchronize()
+            g.launch()
+            F.synchronize()
+            assert np.array_equal(_bits(dy.download(np.float32, (M, N))), _bits(ref)), rep
+            assert np.array_equal(_bits(dy2.download(np.float32, (M, N))), _bits(ref)), rep
+    finally:
+        g.close()
+    for b in (dw, dx, want, dy, dy2):
+        b.close()

@@ -39,7 +39,7 @@ def _wide(name, seed):
     return raw, N, rb
 
 
-@pytest.fixture(scope="module", params=["Q4_K", "Q6_K"])
+@pytest.fixture(scope="module")
 def wide(request, gpu):
     F = gpu
     name = request.param
@@ -49,7 +49,9 @@ def wide(request, gpu):
     dw.close()
 
 
-CASES = [(1, None), (4, None), (16, None), (40, None), (8, "SKINNY"), (24, "MIDM")]
+# weight type, tokens, forced path (None: the automatic choice); k_midm takes Q4_K only
+CASES = [(t, M, None) for t in ("Q4_K", "Q6_K") for M in (1, 4, 16, 40)] + [
+    ("Q4_K", 8, "SKINNY"), ("Q6_K", 8, "SKINNY"), ("Q4_K", 24, "MIDM")]
 
 
 def _rows(N, rb):
@@ -57,13 +59,11 @@ def _rows(N, rb):
     return np.unique(np.r_[0:16, mark - 16:mark + 16, N - 16:N])
 
 
-@pytest.mark.parametrize("M,path", CASES)
+@pytest.mark.parametrize("wide,M,path", CASES, indirect=["wide"])
 def test_rows_past_4gib(gpu, oracle, wide, M, path):
     F = gpu
     name, raw, N, rb, dw = wide
     qtype = H.QTYPES[name][0]
-    if name == "Q6_K" and path == "MIDM":
-        pytest.skip("k_midm takes Q4_K weights only")
     rng = np.random.default_rng(M)
     x = rng.standard_normal((M, K)).astype(np.float32)
     bias = rng.standard_normal(N).astype(np.float32)
@@ -91,7 +91,7 @@ def test_rows_past_4gib(gpu, oracle, wide, M, path):
     assert err <= TOL
 
 
-@pytest.mark.parametrize("M", [65, 300])
+@pytest.mark.parametrize("wide,M", [(t, M) for t in ("Q4_K", "Q6_K") for M in (65, 300)], indirect=["wide"])
 def test_gemm_refuses_past_4gib(gpu, wide, M):
     F = gpu
     name, raw, N, rb, dw = wide

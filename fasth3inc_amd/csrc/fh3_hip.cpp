@@ -1176,6 +1176,11 @@ extern "C" void fh3_matmul(const Fh3W *w, const float *x, float *y, int n_tok, c
         report("fh3_matmul", FH3_E_INVALID);
         return;
     }
+    // refusals the device call would make, before the weights are staged
+    if (w->in % fh3k_dequant_block_len(w->type) == 0 && (rc = check_gemm_span(w, n_tok, "fh3_matmul")) != FH3_OK) {
+        report("fh3_matmul", rc);
+        return;
+    }
     std::lock_guard<std::recursive_mutex> lk(g.mu);
     const size_t wb = fh3_row_bytes(w->type, w->in) * (size_t)w->out;
     const size_t xb = (size_t)n_tok * (size_t)w->in * sizeof(float);

@@ -108,6 +108,11 @@ def test_gemm_refuses_past_4gib(gpu, wide, M):
     # nothing was written
     head = dy.download(np.uint8, (4096,))
     assert (head == 0x7F).all()
+    # the host-pointer fh3_matmul refuses it before staging the weights: y
+    # stays as it was (the wrapper fills it with NaN) and the reason is kept
+    yh = F.matmul(raw, K, N, x, qtype=qtype)
+    assert np.isnan(yh).all()
+    assert b"2^32" in F.lib().fh3_hip_last_error()
     # and the next call in range still works
     y = F.DeviceBuffer(4 * N)
     F.matmul_dev(dw, K, N, dx, y, 1, None, qtype=qtype)
